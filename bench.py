@@ -1,0 +1,257 @@
+"""Decode benchmark: Qwen3-4B bf16 greedy decode on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config c2|c3|c4|c5] [--gpus 1]
+
+Workload (the config the headline metric is quoted
+on): Qwen3-4B architecture, bf16, random-init N(0, 0.02) weights from seed 0
+written as a Hugging Face checkpoint directory and loaded through
+``Engine(model_path)``; batch 1, 512 prompt tokens uniform over the vocab
+(seed 1), 256 greedy new tokens.  A step is one decode step of the whole
+batch (one hipGraph replay: embed, 36 layers, lm_head + argmax).  The timed
+region holds exactly K replays bracketed by device synchronisations; the
+prompt is prefilled before it and positions cycle through the workload's
+own range [512, 767], so every timed step does the work of a real step of
+this workload.
+
+Printed JSON fields beyond the driver contract:
+  roofline      gate/up GEMM (the dominant kernel, 44.6% of weight bytes),
+                algorithmic bytes per launch / its average duration measured
+                with HIP events on the engine's stream;
+  cpu_baseline  the Transformers CPU greedy loop on the same checkpoint
+                (the reference's own oracle path), on a bounded sample;
+  step_hbm      algorithmic bytes per step (weights + KV read/write) / step time.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "dryft-challenge_amd")
+for _p in (PKG, REPO):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    # name: (batch, prompt, new tokens, description)
+    "c2": (1, 512, 256, "qwen3-4b bf16 bs1 prompt512 new256"),
+    "c3": (8, 1024, 512, "qwen3-4b bf16 bs8 prompt1024 new512"),
+    "c4": (32, 4096, 256, "qwen3-4b bf16 bs32 prompt4096 new256"),
+}
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def step_bytes(model_cfg, weight_bytes, batch, pos):
+    """Algorithmic HBM bytes of one decode step at position ``pos``: all
+    weights once, the KV read of slots 0..pos and the KV write of slot pos."""
+    per_tok = 2 * model_cfg.n_layers * model_cfg.nkv * model_cfg.head_dim * 2
+    return weight_bytes + batch * per_tok * (pos + 1) + batch * per_tok
+
+
+def time_gemm_role(engine, state, role, reps=5):
+    """Average duration (s) of one launch of ``role``'s GEMM, over all layers'
+    weights (so nothing is served from the 256 MB MALL), HIP events on the
+    engine's stream."""
+    import torch
+    lib = engine.lib
+    rows = state.batch
+    args = [state._gemm_args(role, i, rows) for i in range(engine.model.cfg.n_layers)]
+    s = torch.cuda.current_stream()
+    for a in args:  # warm
+        lib.gemm(a, s.cuda_stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    for _ in range(reps):
+        for a in args:
+            lib.gemm(a, s.cuda_stream)
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (reps * len(args))
+
+
+def cpu_baseline(ckpt, cfg, prompt_len, budget_s=25.0):
+    """Transformers' greedy loop on the host CPU over the same checkpoint
+    (bf16, sdpa), bounded: a short prefill, then decode steps until the
+    budget or 8 steps.  Falls back to the oracle restatement if Transformers
+    is unavailable."""
+    import torch
+    cores = len(os.sched_getaffinity(0))
+    threads = min(cores, 16)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, cfg["vocab_size"], (1, prompt_len), generator=g)
+    try:
+        from transformers import AutoModelForCausalLM, DynamicCache
+        os.environ.setdefault("USE_HUB_KERNELS", "0")
+        t0 = time.perf_counter()
+        model = AutoModelForCausalLM.from_pretrained(ckpt, dtype=torch.bfloat16, attn_implementation="sdpa",
+                                                     local_files_only=True).eval()
+        log(f"cpu baseline: transformers loaded in {time.perf_counter() - t0:.1f}s")
+        kind = "reference"
+        with torch.no_grad():
+            cache = DynamicCache(config=model.config)
+            out = model(input_ids=ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+            times = []
+            start = time.perf_counter()
+            while len(times) < 8 and time.perf_counter() - start < budget_s:
+                t = time.perf_counter()
+                out = model(input_ids=nxt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+                nxt = out.logits[:, -1].argmax(-1, keepdim=True)
+                times.append(time.perf_counter() - t)
+        what = "transformers Qwen3ForCausalLM bf16 sdpa"
+    except ImportError:
+        from oracle.qwen3_oracle import Qwen3Oracle
+        from qdec.checkpoint import load_tensors
+        kind = "port"
+        o = Qwen3Oracle(cfg, load_tensors(ckpt), mode="bf16")
+        kc, vc = o.new_cache(1, prompt_len + 16)
+        nxt = o.forward(ids, [0], kc, vc)[:, -1].argmax(-1, keepdim=True)
+        times = []
+        start = time.perf_counter()
+        while len(times) < 8 and time.perf_counter() - start < budget_s:
+            t = time.perf_counter()
+            nxt = o.forward(nxt, [prompt_len + len(times)], kc, vc)[:, -1].argmax(-1, keepdim=True)
+            times.append(time.perf_counter() - t)
+        what = "oracle restatement (torch CPU fp32 with bf16 rounding)"
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{what}; batch 1, prefill {prompt_len} tokens (untimed), then {len(times)} greedy "
+                      f"decode steps, median {med:.3f} s/step; same seed-0 checkpoint as the GPU run"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--ckpt", default=os.environ.get("QDEC_BENCH_CKPT", "/tmp/qdec_qwen3_4b_seed0"))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-prompt", type=int, default=64)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (every box has one MI355X); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from engine import Engine
+    from qdec.checkpoint import ensure_checkpoint, qwen3_config
+
+    B, S, N, desc = CONFIGS[args.config]
+    cfg = qwen3_config()
+    t0 = time.perf_counter()
+    ensure_checkpoint(args.ckpt, cfg, seed=0)
+    log(f"checkpoint ready at {args.ckpt} ({time.perf_counter() - t0:.1f}s)")
+    t0 = time.perf_counter()
+    eng = Engine(args.ckpt)
+    log(f"engine loaded ({time.perf_counter() - t0:.1f}s)")
+    mc = eng.model.cfg
+    wbytes = eng.model.weight_bytes()
+
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, mc.vocab, (B, S), generator=g)
+    sh = eng._shape_for(B, S, N)
+    st = sh.state
+    t0 = time.perf_counter()
+    st.prefill(prompt.to(eng.device))
+    torch.cuda.synchronize()
+    log(f"prefill {B}x{S}: {time.perf_counter() - t0:.3f}s")
+    graph = sh.graph
+    last_pos = S + N - 2  # the last decode step of the workload feeds position S+N-2
+    span = last_pos - S + 1
+
+    positions = []
+
+    def run(k):
+        for _ in range(k):
+            p = S + (len(positions) % span)
+            if p == S and positions:
+                st.lens.fill_(S)
+            positions.append(p)
+            graph.replay()
+
+    run(args.warmup)
+    positions.clear()
+    st.lens.fill_(S)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    run(args.steps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) / 1e3
+    elapsed = max(wall, gpu_s)
+    tok_s = B * args.steps / elapsed
+    ms = 1e3 * elapsed / args.steps
+    total_bytes = sum(step_bytes(mc, wbytes, B, p) for p in positions)
+    step_tbs = total_bytes / elapsed / 1e12
+    log(f"{args.steps} steps: {ms:.4f} ms/step (events {1e3 * gpu_s / args.steps:.4f}), "
+        f"{tok_s:.1f} tok/s, {step_tbs:.3f} TB/s algorithmic")
+
+    # dominant kernel: gate/up (NORM_IN + GLU), bytes = both weight halves +
+    # activations in + act out.
+    t_gu = time_gemm_role(eng, st, "gate_up")
+    gu_bytes = 2 * mc.inter * mc.hidden * 2 + B * mc.hidden * 2 + B * mc.inter * 2 + mc.hidden * 2
+    gu_gbs = gu_bytes / t_gu / 1e9
+    log(f"gate_up GEMM: {t_gu * 1e6:.2f} us/launch, {gu_gbs:.1f} GB/s")
+    roles = {}
+    for role in ("qkv", "o", "down", "lm"):
+        roles[role] = round(time_gemm_role(eng, st, role) * 1e6, 2)
+    log(f"other roles us/launch: {roles}")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        del eng, sh, st, graph
+        torch.cuda.empty_cache()
+        try:
+            cpu = cpu_baseline(args.ckpt, cfg, args.cpu_prompt)
+        except Exception as exc:  # reported, never fatal for the GPU number
+            log(f"cpu baseline failed: {type(exc).__name__}: {exc}")
+
+    line = {
+        "metric": "Qwen3-4B bf16 decode tok/s (bs1, bs32) + achieved HBM TB/s vs peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights seed 0, uniform random prompt tokens seed 1)",
+        "config": {"workload": desc, "batch": B, "prompt_len": S, "new_tokens": N,
+                   "decode_positions": [S, last_pos], "graph": "hipGraph per decode step",
+                   "parallelism": "single GPU"},
+        "step_hbm": {"achieved_TBs": round(step_tbs, 4), "peak_TBs": HBM_PEAK_GBS / 1e3,
+                     "frac": round(step_tbs * 1e3 / HBM_PEAK_GBS, 4),
+                     "bytes_per_step_mean": int(total_bytes / len(positions))},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemm_kernel<1, NORM_IN|GLU> (gate/up, 9728x2x2560)",
+                     "algorithmic_bytes_per_launch": gu_bytes,
+                     "avg_launch_us": round(t_gu * 1e6, 3)},
+        "role_us_per_launch": roles,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,238 @@
+// extern "C" entry points of libqdec.so: argument validation, workspace
+// sizing and launch-plan derivation around the kernels.  Validation runs
+// before any HIP call, so a bad call fails cleanly even without a GPU.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <algorithm>
+
+#include "qdec_common.h"
+#include "qdec_kernels.h"
+
+namespace qdec {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char *what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(QDEC_ELAUNCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  g_err[0] = '\0';
+  return QDEC_OK;
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static int launch_status(hipError_t e, const char *what) {
+  if (e != hipSuccess) return set_error(QDEC_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return check_launch(what);
+}
+
+// Derive the launch plan of a GEMM call; returns QDEC_OK or an error code.
+static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) {
+  if (!a) return set_error(QDEC_EINVAL, "qdec_gemm: null args");
+  const uint32_t f = a->flags;
+  if (!gemm_flags_supported(f)) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: flags 0x%x not supported", f);
+  if (a->rows < 1 || a->rows > 64) return set_error(QDEC_EINVAL, "qdec_gemm: rows %d not in [1, 64]", a->rows);
+  if (a->n <= 0 || a->n % 16) return set_error(QDEC_EINVAL, "qdec_gemm: n %d not a positive multiple of 16", a->n);
+  if (a->k <= 0 || a->k % 32) return set_error(QDEC_EINVAL, "qdec_gemm: k %d not a positive multiple of 32", a->k);
+  if (a->waves < 1 || a->waves > 8) return set_error(QDEC_EINVAL, "qdec_gemm: waves %d not in [1, 8]", a->waves);
+  if (a->ksplit < 1) return set_error(QDEC_EINVAL, "qdec_gemm: ksplit %d < 1", a->ksplit);
+  const int KS = a->k / 32;
+  if (KS % a->ksplit) return set_error(QDEC_EINVAL, "qdec_gemm: k/32=%d not divisible by ksplit %d", KS, a->ksplit);
+  if ((KS / a->ksplit) % a->waves)
+    return set_error(QDEC_EINVAL, "qdec_gemm: k steps per split %d not divisible by waves %d", KS / a->ksplit, a->waves);
+  const bool arg = (f & QDEC_ARGMAX) != 0;
+  const bool glu = (f & QDEC_GLU) != 0;
+  const int ntiles = a->n / 16;
+  if (a->tiles_per_wg < 1) return set_error(QDEC_EINVAL, "qdec_gemm: tiles_per_wg %d < 1", a->tiles_per_wg);
+  if (!arg && a->tiles_per_wg != 1) return set_error(QDEC_EINVAL, "qdec_gemm: tiles_per_wg > 1 needs QDEC_ARGMAX");
+  if (ntiles % a->tiles_per_wg) return set_error(QDEC_EINVAL, "qdec_gemm: n/16=%d not divisible by tiles_per_wg %d", ntiles, a->tiles_per_wg);
+  if (arg && a->ksplit != 1) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: QDEC_ARGMAX needs ksplit 1");
+  if (need_scratch && (!a->x || !a->w)) return set_error(QDEC_EINVAL, "qdec_gemm: null x or w");
+  if (need_scratch && (f & QDEC_NORM_IN) && !a->norm_w) return set_error(QDEC_EINVAL, "qdec_gemm: NORM_IN needs norm_w");
+  if (need_scratch && (f & QDEC_RES_OUT) && !a->res) return set_error(QDEC_EINVAL, "qdec_gemm: RES_OUT needs res");
+  if (need_scratch && !(f & (QDEC_RES_OUT | QDEC_ARGMAX)) && !a->out) return set_error(QDEC_EINVAL, "qdec_gemm: null out");
+  if (need_scratch && arg && (!a->ids_out || !a->partial || !a->counters))
+    return set_error(QDEC_EINVAL, "qdec_gemm: ARGMAX needs ids_out, partial and counters");
+  if (need_scratch && a->ksplit > 1 && (!a->partial || !a->counters))
+    return set_error(QDEC_EINVAL, "qdec_gemm: ksplit > 1 needs partial and counters");
+  if (!aligned16(a->x) || !aligned16(a->w) || (a->out && !aligned16(a->out)) || (a->res && !aligned16(a->res)) ||
+      (a->norm_w && !aligned16(a->norm_w)))
+    return set_error(QDEC_EALIGN, "qdec_gemm: x, w, out, res and norm_w must be 16-byte aligned");
+
+  const int nacc = glu ? 2 : 1;
+  const int mt = (a->rows + 15) / 16;
+  p->x = a->x; p->w = a->w; p->out = a->out; p->res = a->res; p->norm_w = a->norm_w;
+  p->partial = a->partial; p->counters = a->counters; p->ids_out = a->ids_out; p->lens_inc = a->lens_inc;
+  p->eps = a->eps; p->rows = a->rows; p->n = a->n; p->k = a->k;
+  p->ksplit = a->ksplit; p->waves = a->waves; p->tiles_per_wg = a->tiles_per_wg;
+  p->KS = KS;
+  p->ksw = KS / a->ksplit / a->waves;
+  p->up_tiles = ntiles;
+  const int kpmax = glu ? kGemmKpMaxGlu : kGemmKpMax;
+  // k steps per pass: register budget, then LDS budget for rows x waves x kp x 32.
+  const size_t red_bytes = (size_t)(a->waves - 1) * nacc * mt * 64 * 16;
+  const size_t head = 784;
+  const size_t budget = kGemmLdsX - red_bytes - head;
+  int kp = std::min(p->ksw, kpmax);
+  while (kp > 1 && (size_t)a->rows * (a->waves * kp * 32 + 8) * 2 > budget) --kp;
+  p->kp = kp;
+  p->npass = (p->ksw + kp - 1) / kp;
+  p->xstride = a->waves * kp * 32 + 8;
+  p->lds_red_off = (int)head;
+  p->lds_x_off = (int)(head + red_bytes);
+  p->lds_bytes = head + red_bytes + (size_t)a->rows * p->xstride * 2;
+  if (p->lds_bytes > (size_t)kGemmLdsX)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: rows %d x waves %d needs %zu B of LDS", a->rows, a->waves,
+                     p->lds_bytes);
+  return QDEC_OK;
+}
+
+static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) {
+  if (!a) return set_error(QDEC_EINVAL, "qdec_attn: null args");
+  if (a->head_dim != 128) return set_error(QDEC_EUNSUPPORTED, "qdec_attn: head_dim %d (only 128)", a->head_dim);
+  if (a->nkv < 1 || a->nq != 4 * a->nkv)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: nq %d / nkv %d (only 4 query heads per kv head)", a->nq, a->nkv);
+  if (a->batch < 1 || a->batch > 65535) return set_error(QDEC_EINVAL, "qdec_attn: batch %d", a->batch);
+  if (a->t_rows < 1 || a->t_rows > 16) return set_error(QDEC_EINVAL, "qdec_attn: t_rows %d not in [1, 16]", a->t_rows);
+  if (a->cap < 32 || a->cap % 32) return set_error(QDEC_EINVAL, "qdec_attn: cap %d not a positive multiple of 32", a->cap);
+  if (a->chunk < 32 || a->chunk % 32) return set_error(QDEC_EINVAL, "qdec_attn: chunk %d not a positive multiple of 32", a->chunk);
+  const int nchunks = (a->cap + a->chunk - 1) / a->chunk;
+  if (!need_scratch) goto fill;
+  if (!a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->lens || !a->k_cache ||
+      !a->v_cache || !a->out)
+    return set_error(QDEC_EINVAL, "qdec_attn: null pointer argument");
+  if (nchunks > 1 && (!a->partial || !a->counters))
+    return set_error(QDEC_EINVAL, "qdec_attn: more than one chunk needs partial and counters");
+  if (!aligned16(a->qkv) || !aligned16(a->q_norm_w) || !aligned16(a->k_norm_w) || !aligned16(a->cos_tab) ||
+      !aligned16(a->sin_tab) || !aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->out))
+    return set_error(QDEC_EALIGN, "qdec_attn: tensor pointers must be 16-byte aligned");
+fill:
+  p->qkv = a->qkv; p->q_norm_w = a->q_norm_w; p->k_norm_w = a->k_norm_w;
+  p->cos_tab = a->cos_tab; p->sin_tab = a->sin_tab; p->lens = a->lens;
+  p->k_cache = a->k_cache; p->v_cache = a->v_cache; p->out = a->out;
+  p->partial = a->partial; p->counters = a->counters;
+  p->eps = a->eps;
+  p->scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p->batch = a->batch; p->t_rows = a->t_rows; p->nq = a->nq; p->nkv = a->nkv;
+  p->cap = a->cap; p->chunk = a->chunk; p->nchunks = nchunks;
+  return QDEC_OK;
+}
+
+}  // namespace qdec
+
+using namespace qdec;
+
+extern "C" {
+
+int qdec_version(void) { return QDEC_ABI_VERSION; }
+
+const char *qdec_last_error(void) { return g_err; }
+
+int qdec_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+int64_t qdec_tiled_offset(int64_t n, int64_t k, int64_t K) {
+  if (K <= 0 || K % 32 || n < 0 || k < 0 || k >= K) return -1;
+  const int64_t nt = n / 16, ks = k / 32;
+  const int64_t lane = (n % 16) + 16 * ((k % 32) / 8);
+  return ((nt * (K / 32) + ks) * 64 + lane) * 8 + (k % 8);
+}
+
+int qdec_pack_tiles(const void *src, void *dst, int64_t n, int64_t k, qdec_stream_t stream) {
+  if (!src || !dst) return set_error(QDEC_EINVAL, "qdec_pack_tiles: null pointer");
+  if (n <= 0 || n % 16 || k <= 0 || k % 32)
+    return set_error(QDEC_EINVAL, "qdec_pack_tiles: shape [%lld, %lld] needs n %% 16 == 0 and k %% 32 == 0",
+                     (long long)n, (long long)k);
+  if (!aligned16(src) || !aligned16(dst)) return set_error(QDEC_EALIGN, "qdec_pack_tiles: pointers must be 16-byte aligned");
+  return launch_status(launch_pack(src, dst, n, k, (hipStream_t)stream), "qdec_pack_tiles");
+}
+
+int qdec_embed(const qdec_embed_args *a, qdec_stream_t stream) {
+  if (!a || !a->ids || !a->emb || !a->h) return set_error(QDEC_EINVAL, "qdec_embed: null pointer");
+  if (a->rows < 1 || a->hidden <= 0 || a->hidden % 32 || a->vocab <= 0 || a->vocab % 16)
+    return set_error(QDEC_EINVAL, "qdec_embed: rows %d hidden %d vocab %d", a->rows, a->hidden, a->vocab);
+  if (!aligned16(a->emb) || !aligned16(a->h)) return set_error(QDEC_EALIGN, "qdec_embed: emb and h must be 16-byte aligned");
+  return launch_status(launch_embed(a->ids, a->emb, a->h, a->rows, a->hidden, a->vocab, (hipStream_t)stream),
+                       "qdec_embed");
+}
+
+int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes, size_t *counter_bytes) {
+  GemmParams p;
+  const int rc = plan_gemm(a, &p, false);
+  if (rc != QDEC_OK) return rc;
+  const int ntiles = a->n / 16;
+  size_t pb = 0, cb = 0;
+  if (a->flags & QDEC_ARGMAX) {
+    pb = 2 * sizeof(float) * (size_t)(ntiles / a->tiles_per_wg) * a->rows;
+    cb = sizeof(uint32_t);
+  } else if (a->ksplit > 1) {
+    pb = sizeof(float) * (size_t)a->ksplit * a->rows * a->n * ((a->flags & QDEC_GLU) ? 2 : 1);
+    cb = sizeof(uint32_t) * (size_t)ntiles;
+  }
+  if (partial_bytes) *partial_bytes = pb;
+  if (counter_bytes) *counter_bytes = cb;
+  return QDEC_OK;
+}
+
+int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream) {
+  GemmParams p;
+  const int rc = plan_gemm(a, &p, true);
+  if (rc != QDEC_OK) return rc;
+  return launch_status(launch_gemm(p, a->flags, (hipStream_t)stream), "qdec_gemm");
+}
+
+int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes, size_t *counter_bytes) {
+  AttnParams p;
+  const int rc = plan_attn(a, &p, false);
+  if (rc != QDEC_OK) return rc;
+  const size_t R = (size_t)a->t_rows * (a->nq / a->nkv);
+  if (partial_bytes)
+    *partial_bytes = p.nchunks > 1 ? sizeof(float) * (size_t)a->batch * a->nkv * p.nchunks * R * (a->head_dim + 2) : 0;
+  if (counter_bytes) *counter_bytes = p.nchunks > 1 ? sizeof(uint32_t) * (size_t)a->batch * a->nkv : 0;
+  return QDEC_OK;
+}
+
+int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream) {
+  AttnParams p;
+  const int rc = plan_attn(a, &p, true);
+  if (rc != QDEC_OK) return rc;
+  return launch_status(launch_attn(p, (hipStream_t)stream), "qdec_attn");
+}
+
+int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream) {
+  if (!a || !a->hist || !a->lens || !a->ids || !a->draft) return set_error(QDEC_EINVAL, "qdec_ngram_draft: null pointer");
+  if (a->batch < 1 || a->cap < 1 || a->k < 1 || a->primary < 1 || a->backoff < 1)
+    return set_error(QDEC_EINVAL, "qdec_ngram_draft: batch %d cap %d k %d primary %d backoff %d", a->batch, a->cap,
+                     a->k, a->primary, a->backoff);
+  return launch_status(
+      launch_draft(a->hist, a->lens, a->ids, a->draft, a->batch, a->cap, a->primary, a->backoff, a->k,
+                   (hipStream_t)stream),
+      "qdec_ngram_draft");
+}
+
+int qdec_spec_accept(const qdec_accept_args *a, qdec_stream_t stream) {
+  if (!a || !a->out_tok || !a->draft || !a->hist || !a->lens || !a->naccept)
+    return set_error(QDEC_EINVAL, "qdec_spec_accept: null pointer");
+  if (a->batch < 1 || a->cap < 1 || a->k < 1)
+    return set_error(QDEC_EINVAL, "qdec_spec_accept: batch %d cap %d k %d", a->batch, a->cap, a->k);
+  return launch_status(launch_accept(a->out_tok, a->draft, a->hist, a->lens, a->naccept, a->batch, a->cap, a->k,
+                                     a->stop_len, (hipStream_t)stream),
+                       "qdec_spec_accept");
+}
+
+}  // extern "C"

@@ -1,0 +1,422 @@
+// Weight-streaming skinny GEMM for the decode step: y = x' . W^T, 1..64 rows.
+//
+// One workgroup owns one 16-column output tile (or several, for the lm_head)
+// and a contiguous k range; its waves split that range into equal contiguous
+// pieces.  Each wave streams its part of the tiled weight -- one 1 KiB block
+// per k step, one 16-byte load per lane -- straight into the A operand of
+// v_mfma_f32_16x16x32_bf16, while the activations (normalised on the way in
+// when NORM_IN) are staged once per workgroup in LDS and read as the B
+// operand.  The product is computed transposed (y^T = W . x'^T), so a lane
+// ends up holding 4 consecutive output columns of one row.
+//
+// Summation order of an output element: MFMA chain over the wave's k steps in
+// increasing order, then waves 0..W-1 added in order, then k splits 0..S-1
+// added in order by the workgroup that arrives last.  None of it depends on
+// the number of rows, which is what lets a verify pass over B*T rows
+// reproduce the plain B-row step bit for bit.
+//
+// Reference behaviour replaced: engine/kernels/fused.py:33-235 (_gemv_kernel,
+// _gemv_vec_kernel, _gemv_splitk_kernel + reduce) and the lm_head + argmax of
+// engine/engine.py:492-498, 542-545.
+#include "qdec_common.h"
+#include "qdec_kernels.h"
+
+namespace qdec {
+
+namespace {
+
+constexpr int kMaxRows = 64;
+
+template <int MT, uint32_t FLAGS>
+__global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
+  constexpr bool NORM = (FLAGS & QDEC_NORM_IN) != 0;
+  constexpr bool GLU = (FLAGS & QDEC_GLU) != 0;
+  constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
+  constexpr bool ARG = (FLAGS & QDEC_ARGMAX) != 0;
+  constexpr int NACC = GLU ? 2 : 1;
+  constexpr int KPMAX = GLU ? kGemmKpMaxGlu : kGemmKpMax;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  float *s_rstd = reinterpret_cast<float *>(smem);                     // [64]
+  uint32_t *s_flag = reinterpret_cast<uint32_t *>(smem + 256);         // [4]
+  float *s_red = reinterpret_cast<float *>(smem + 272);                // [8*? floats]
+  uint16_t *s_x = reinterpret_cast<uint16_t *>(smem + p.lds_x_off);    // [rows][xstride]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nthr = blockDim.x;
+  const int rows = p.rows;
+  const int col = lane & 15;   // row of x inside an M tile
+  const int grp = lane >> 4;   // k group / output column group
+
+  const int ngroups = gridDim.x / p.ksplit;
+  const int tg = blockIdx.x / p.ksplit;        // tile group
+  const int split = blockIdx.x - tg * p.ksplit;
+  const int ks_wg = split * (p.KS / p.ksplit); // first k step of this workgroup
+  const int ks_wave = ks_wg + wave * p.ksw;    // first k step of this wave
+  const int xstride = p.xstride;
+  const uint4 *__restrict__ W = reinterpret_cast<const uint4 *>(p.w);
+  const uint16_t *__restrict__ X = reinterpret_cast<const uint16_t *>(p.x);
+
+  // ---- RMSNorm statistics of the workgroup's input rows (whole row, in a
+  // fixed thread/lane order so every workgroup gets the same rstd bits).
+  if constexpr (NORM) {
+    const int nvec = p.k >> 3;
+    for (int m0 = 0; m0 < rows; m0 += 8) {
+      float ss[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss[j] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int m = m0 + j;
+        if (m < rows) {
+          const uint4 *xr = reinterpret_cast<const uint4 *>(X + (size_t)m * p.k);
+          for (int v = tid; v < nvec; v += nthr) {
+            float f[8];
+            unpack8(xr[v], f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss[j] += f[e] * f[e];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float v = ss[j];
+        v += shfl_xor(v, 32);
+        v += shfl_xor(v, 16);
+        v += shfl_xor(v, 8);
+        v += shfl_xor(v, 4);
+        v += shfl_xor(v, 2);
+        v += shfl_xor(v, 1);
+        if (lane == 0) s_red[wave * 8 + j] = v;
+      }
+      __syncthreads();
+      if (tid < 8 && m0 + tid < rows) {
+        float t = 0.f;
+        for (int w2 = 0; w2 < (nthr >> 6); ++w2) t += s_red[w2 * 8 + tid];
+        s_rstd[m0 + tid] = 1.0f / sqrtf(t / (float)p.k + p.eps);
+      }
+      __syncthreads();
+    }
+  }
+
+  // ARGMAX running best per M tile (lane-local, rows = mt*16 + col).
+  float best_v[MT];
+  int best_i[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    best_v[mt] = -__builtin_huge_valf();
+    best_i[mt] = 0x7fffffff;
+  }
+
+  bool staged = false;
+  for (int tt = 0; tt < p.tiles_per_wg; ++tt) {
+    const int tile = tg * p.tiles_per_wg + tt;
+    f32x4_t acc[NACC][MT];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[a][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int pass = 0; pass < p.npass; ++pass) {
+      const int kbeg = pass * p.kp;                       // wave-local first step
+      const int kcnt = min(p.kp, p.ksw - kbeg);           // steps in this pass
+      // Issue this pass's weight loads first so they overlap the staging.
+      uint4 wb[NACC][KPMAX];
+      {
+        const size_t blk0 = ((size_t)tile * p.KS + ks_wave + kbeg) * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < KPMAX; ++i) {
+          if (i < kcnt) {
+            wb[0][i] = W[blk0 + (size_t)i * 64];
+            if constexpr (GLU)
+              wb[NACC - 1][i] = W[blk0 + (size_t)p.up_tiles * p.KS * 64 + (size_t)i * 64];
+          }
+        }
+      }
+      // Stage x rows for every wave's k steps of this pass.
+      if (!staged || p.npass > 1) {
+        if (pass > 0 || tt > 0) __syncthreads();  // previous readers are done
+        const int nw = nthr >> 6;
+        const int per_row = nw * kcnt * 4;  // 16-byte vectors per row
+        const int total = rows * per_row;
+        for (int v = tid; v < total; v += nthr) {
+          const int m = v / per_row;
+          int r = v - m * per_row;
+          const int w2 = r / (kcnt * 4);
+          r -= w2 * (kcnt * 4);
+          const int i = r >> 2;
+          const int q = r & 3;
+          const int kg = (ks_wg + w2 * p.ksw + kbeg + i) * 32 + q * 8;
+          uint4 xv = *reinterpret_cast<const uint4 *>(X + (size_t)m * p.k + kg);
+          if constexpr (NORM) {
+            const uint4 nv = *reinterpret_cast<const uint4 *>(
+                reinterpret_cast<const uint16_t *>(p.norm_w) + kg);
+            float f[8], g[8];
+            unpack8(xv, f);
+            unpack8(nv, g);
+            const float rs = s_rstd[m];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = g[e] * rbf(f[e] * rs);
+            xv = pack8(f);
+          }
+          *reinterpret_cast<uint4 *>(s_x + (size_t)m * xstride + (w2 * p.kp + i) * 32 + q * 8) = xv;
+        }
+        __syncthreads();
+        staged = true;
+      }
+      // MFMA over this pass.
+#pragma unroll
+      for (int i = 0; i < KPMAX; ++i) {
+        if (i < kcnt) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + col;
+            uint4 b = zero4();
+            if (m < rows)
+              b = *reinterpret_cast<const uint4 *>(s_x + (size_t)m * xstride +
+                                                   (wave * p.kp + i) * 32 + grp * 8);
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) acc[a][mt] = mfma16x16x32(wb[a][i], b, acc[a][mt]);
+          }
+        }
+      }
+    }
+
+    // ---- merge the waves of the workgroup in wave order.
+    const int nw = nthr >> 6;
+    if (nw > 1) {
+      __syncthreads();
+      float4 *red = reinterpret_cast<float4 *>(smem + p.lds_red_off);
+      if (wave > 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            red[(((wave - 1) * NACC + a) * MT + mt) * 64 + lane] =
+                make_float4(acc[a][mt][0], acc[a][mt][1], acc[a][mt][2], acc[a][mt][3]);
+      }
+      __syncthreads();
+      if (wave == 0) {
+        for (int w2 = 1; w2 < nw; ++w2) {
+#pragma unroll
+          for (int a = 0; a < NACC; ++a)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const float4 r = red[(((w2 - 1) * NACC + a) * MT + mt) * 64 + lane];
+              acc[a][mt][0] += r.x;
+              acc[a][mt][1] += r.y;
+              acc[a][mt][2] += r.z;
+              acc[a][mt][3] += r.w;
+            }
+        }
+      }
+    }
+
+    const int n0 = tile * 16 + grp * 4;  // first of this lane's 4 output columns
+
+    // ---- k split across workgroups: partials, last arrival sums them.
+    if (p.ksplit > 1) {
+      if (wave == 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + col;
+            if (m < rows) {
+              float *dst = p.partial + ((size_t)(a * p.ksplit + split) * rows + m) * p.n + n0;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) store_coherent(dst + i, acc[a][mt][i]);
+            }
+          }
+      }
+      if (!arrive_last(p.counters + tile, (uint32_t)p.ksplit, s_flag)) return;
+      if (wave == 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + col;
+            if (m < rows) {
+              f32x4_t t = f32x4_t{0.f, 0.f, 0.f, 0.f};
+              for (int s = 0; s < p.ksplit; ++s) {
+                const float *src = p.partial + ((size_t)(a * p.ksplit + s) * rows + m) * p.n + n0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                  const float v = load_coherent(src + i);
+                  t[i] = (s == 0) ? v : t[i] + v;
+                }
+              }
+              acc[a][mt] = t;
+            }
+          }
+      }
+    }
+
+    // ---- epilogues (wave 0 holds the finished tile).
+    if (wave == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + col;
+        if (m >= rows) continue;
+        if constexpr (ARG) {
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = rbf(acc[0][mt][i]);
+          if (p.out) {
+            uint2 o;
+            o.x = pack2(v[0], v[1]);
+            o.y = pack2(v[2], v[3]);
+            *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (v[i] > best_v[mt]) {
+              best_v[mt] = v[i];
+              best_i[mt] = n0 + i;
+            }
+        } else if constexpr (RES) {
+          uint16_t *rp = reinterpret_cast<uint16_t *>(p.res) + (size_t)m * p.n + n0;
+          const uint2 r = *reinterpret_cast<const uint2 *>(rp);
+          uint2 o;
+          o.x = pack2(lo16(r.x) + rbf(acc[0][mt][0]), hi16(r.x) + rbf(acc[0][mt][1]));
+          o.y = pack2(lo16(r.y) + rbf(acc[0][mt][2]), hi16(r.y) + rbf(acc[0][mt][3]));
+          *reinterpret_cast<uint2 *>(rp) = o;
+        } else if constexpr (GLU) {
+          float o4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float g = rbf(acc[0][mt][i]);
+            const float u = rbf(acc[1][mt][i]);
+            const float s = rbf(g / (1.0f + expf(-g)));
+            o4[i] = s * u;
+          }
+          uint2 o;
+          o.x = pack2(o4[0], o4[1]);
+          o.y = pack2(o4[2], o4[3]);
+          *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+        } else {
+          uint2 o;
+          o.x = pack2(acc[0][mt][0], acc[0][mt][1]);
+          o.y = pack2(acc[0][mt][2], acc[0][mt][3]);
+          *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+        }
+      }
+    }
+  }
+
+  if constexpr (ARG) {
+    // Reduce the 4 column groups of each row, lowest index on equal values.
+    float *pv = p.partial;                                              // [G][rows]
+    int *pi = reinterpret_cast<int *>(p.partial + (size_t)gridDim.x * rows);  // [G][rows]
+    if (wave == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1) {
+          const float ov = shfl_xor(best_v[mt], off);
+          const int oi = __shfl_xor(best_i[mt], off, kWave);
+          if (ov > best_v[mt] || (ov == best_v[mt] && oi < best_i[mt])) {
+            best_v[mt] = ov;
+            best_i[mt] = oi;
+          }
+        }
+        const int m = mt * 16 + col;
+        if (grp == 0 && m < rows) {
+          store_coherent(pv + (size_t)blockIdx.x * rows + m, best_v[mt]);
+          store_coherent_i(pi + (size_t)blockIdx.x * rows + m, best_i[mt]);
+        }
+      }
+    }
+    if (!arrive_last(p.counters, gridDim.x, s_flag)) return;
+    (void)ngroups;
+    float *sv = s_red;                                      // [waves]
+    int *si = reinterpret_cast<int *>(s_red + 8);           // [waves]
+    for (int m = 0; m < rows; ++m) {
+      float bv = -__builtin_huge_valf();
+      int bi = 0x7fffffff;
+      for (int g = tid; g < (int)gridDim.x; g += nthr) {
+        const float v = load_coherent(pv + (size_t)g * rows + m);
+        const int i = load_coherent_i(pi + (size_t)g * rows + m);
+        if (v > bv || (v == bv && i < bi)) {
+          bv = v;
+          bi = i;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        for (int w2 = 1; w2 < (nthr >> 6); ++w2)
+          if (sv[w2] > bv || (sv[w2] == bv && si[w2] < bi)) {
+            bv = sv[w2];
+            bi = si[w2];
+          }
+        p.ids_out[m] = (int64_t)bi;
+        if (p.lens_inc) p.lens_inc[m] += 1;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int MT>
+hipError_t launch_mt(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds,
+                     hipStream_t s) {
+  switch (flags) {
+    case 0:
+      hipLaunchKernelGGL((gemm_kernel<MT, 0u>), grid, block, lds, s, p);
+      break;
+    case QDEC_NORM_IN:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN>), grid, block, lds, s, p);
+      break;
+    case QDEC_NORM_IN | QDEC_GLU:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_GLU>), grid, block, lds, s, p);
+      break;
+    case QDEC_RES_OUT:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT>), grid, block, lds, s, p);
+      break;
+    case QDEC_NORM_IN | QDEC_ARGMAX:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_ARGMAX>), grid, block, lds, s, p);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
+
+}  // namespace
+
+bool gemm_flags_supported(uint32_t flags) {
+  return flags == 0u || flags == QDEC_NORM_IN || flags == (QDEC_NORM_IN | QDEC_GLU) ||
+         flags == QDEC_RES_OUT || flags == (QDEC_NORM_IN | QDEC_ARGMAX);
+}
+
+hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
+  const int mt = (p.rows + 15) / 16;
+  const int ntiles = p.n / 16;
+  dim3 grid((ntiles / p.tiles_per_wg) * p.ksplit);
+  dim3 block(64 * p.waves);
+  const size_t lds = p.lds_bytes;
+  switch (mt) {
+    case 1: return launch_mt<1>(p, flags, grid, block, lds, s);
+    case 2: return launch_mt<2>(p, flags, grid, block, lds, s);
+    case 3: return launch_mt<3>(p, flags, grid, block, lds, s);
+    case 4: return launch_mt<4>(p, flags, grid, block, lds, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace qdec

@@ -1,0 +1,106 @@
+// Shared device helpers of the qdec kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qdec.h"
+
+namespace qdec {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kTileN = 16;   // tile rows of a weight block (output columns)
+constexpr int kTileK = 32;   // k per MFMA step
+constexpr int kBlockElems = kTileN * kTileK;  // 512 bf16 = 1 KiB
+
+// ---------------------------------------------------------------- bf16 math
+// Round-to-nearest-even float -> bf16, the rounding torch's .to(bfloat16)
+// performs; NaN maps to the canonical quiet NaN.
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+// Value of f after a round trip through bf16.
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// The 8 bf16 of a 16-byte vector.
+__device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ void unpack8(const uint4 &v, float f[8]) {
+  f[0] = lo16(v.x); f[1] = hi16(v.x);
+  f[2] = lo16(v.y); f[3] = hi16(v.y);
+  f[4] = lo16(v.z); f[5] = hi16(v.z);
+  f[6] = lo16(v.w); f[7] = hi16(v.w);
+}
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return f2bf(a) | (f2bf(b) << 16);
+}
+__device__ __forceinline__ uint4 pack8(const float f[8]) {
+  uint4 v;
+  v.x = pack2(f[0], f[1]);
+  v.y = pack2(f[2], f[3]);
+  v.z = pack2(f[4], f[5]);
+  v.w = pack2(f[6], f[7]);
+  return v;
+}
+
+// D = A(16x32) * B(32x16) + C; lane l supplies A row / B column (l & 15),
+// k = 8*(l >> 4) .. +8; the result lane l holds rows 4*(l >> 4) + i, column
+// (l & 15), i = 0..3.
+__device__ __forceinline__ f32x4_t mfma16x16x32(const uint4 &a, const uint4 &b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// Global loads that bypass caches which another XCD may hold stale, for data
+// written by other workgroups of the same grid (split partials).
+__device__ __forceinline__ float load_coherent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int load_coherent_i(const int *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent_i(int *p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival at a per-tile counter after this workgroup's partial results were
+// stored (all threads must call it).  Returns true in every thread of the
+// workgroup that arrived last; that workgroup resets the counter to zero.
+__device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected,
+                                            uint32_t *lds_flag) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t last = (old == expected - 1u) ? 1u : 0u;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds_flag = last;
+  }
+  __syncthreads();
+  bool last = *lds_flag != 0u;
+  if (last) __threadfence();
+  return last;
+}
+
+// Cross-lane helpers (wave64).
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
+
+}  // namespace qdec
+
+// Error plumbing shared by the entry points (api.hip).
+namespace qdec {
+int set_error(int code, const char *fmt, ...);
+int check_launch(const char *what);
+}  // namespace qdec

@@ -1,0 +1,67 @@
+// Launch parameter blocks and launchers of the qdec kernels (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qdec {
+
+// Register budget of the GEMM: weight blocks a wave holds in flight per pass.
+constexpr int kGemmKpMax = 20;
+constexpr int kGemmKpMaxGlu = 10;
+// LDS the GEMM may use for staged activations.
+constexpr int kGemmLdsX = 64 * 1024;
+
+struct GemmParams {
+  const void *x;
+  const void *w;
+  void *out;
+  void *res;
+  const void *norm_w;
+  float *partial;
+  uint32_t *counters;
+  int64_t *ids_out;
+  int32_t *lens_inc;
+  float eps;
+  int rows, n, k;
+  int ksplit, waves, tiles_per_wg;
+  int KS;        // k / 32
+  int ksw;       // k steps per wave
+  int kp;        // k steps per wave per LDS pass
+  int npass;
+  int up_tiles;  // GLU: tile offset of the up half
+  int xstride;   // LDS row stride of staged activations (elements)
+  int lds_red_off, lds_x_off;
+  size_t lds_bytes;
+};
+bool gemm_flags_supported(uint32_t flags);
+hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
+
+struct AttnParams {
+  const void *qkv;
+  const void *q_norm_w;
+  const void *k_norm_w;
+  const void *cos_tab;
+  const void *sin_tab;
+  const int32_t *lens;
+  void *k_cache;
+  void *v_cache;
+  void *out;
+  float *partial;
+  uint32_t *counters;
+  float eps;
+  float scale_log2;  // log2(e) / sqrt(head_dim)
+  int batch, t_rows, nq, nkv, cap, chunk, nchunks;
+};
+hipError_t launch_attn(const AttnParams &p, hipStream_t s);
+
+hipError_t launch_embed(const int64_t *ids, const void *emb, void *h, int rows, int hidden,
+                        int vocab, hipStream_t s);
+hipError_t launch_pack(const void *src, void *dst, int64_t n, int64_t k, hipStream_t s);
+hipError_t launch_draft(const int64_t *hist, const int32_t *lens, int64_t *ids, int64_t *draft,
+                        int batch, int cap, int primary, int backoff, int k, hipStream_t s);
+hipError_t launch_accept(const int64_t *out_tok, const int64_t *draft, int64_t *hist,
+                         int32_t *lens, int32_t *naccept, int batch, int cap, int k,
+                         int stop_len, hipStream_t s);
+
+}  // namespace qdec

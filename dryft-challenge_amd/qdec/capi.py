@@ -1,0 +1,151 @@
+"""ctypes binding of libqdec.so (the C ABI declared in include/qdec.h).
+
+Argument blocks mirror the C structs field for field.  Every call raises
+``QdecError`` with ``qdec_last_error()`` when the library returns an error.
+There is no fallback: if the library is missing the import of the engine
+fails loudly.
+"""
+
+import ctypes
+import os
+import re
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqdec.so")
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
+                      "include", "qdec.h")
+
+NORM_IN, GLU, RES_OUT, ARGMAX = 1, 2, 4, 8
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+F32 = ctypes.c_float
+
+
+class QdecError(RuntimeError):
+    """A libqdec entry point returned a negative status."""
+
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+class EmbedArgs(ctypes.Structure):
+    _fields_ = [("ids", P), ("emb", P), ("h", P), ("rows", I32), ("hidden", I32), ("vocab", I32)]
+
+
+class GemmArgs(ctypes.Structure):
+    _fields_ = [("x", P), ("w", P), ("out", P), ("res", P), ("norm_w", P), ("partial", P),
+                ("counters", P), ("ids_out", P), ("lens_inc", P), ("eps", F32), ("rows", I32),
+                ("n", I32), ("k", I32), ("flags", ctypes.c_uint32), ("ksplit", I32), ("waves", I32),
+                ("tiles_per_wg", I32)]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("qkv", P), ("q_norm_w", P), ("k_norm_w", P), ("cos_tab", P), ("sin_tab", P),
+                ("lens", P), ("k_cache", P), ("v_cache", P), ("out", P), ("partial", P),
+                ("counters", P), ("eps", F32), ("sm_scale", F32), ("batch", I32), ("t_rows", I32),
+                ("nq", I32), ("nkv", I32), ("head_dim", I32), ("cap", I32), ("chunk", I32)]
+
+
+class DraftArgs(ctypes.Structure):
+    _fields_ = [("hist", P), ("lens", P), ("ids", P), ("draft", P), ("batch", I32), ("cap", I32),
+                ("primary", I32), ("backoff", I32), ("k", I32)]
+
+
+class AcceptArgs(ctypes.Structure):
+    _fields_ = [("out_tok", P), ("draft", P), ("hist", P), ("lens", P), ("naccept", P),
+                ("batch", I32), ("cap", I32), ("k", I32), ("stop_len", I32)]
+
+
+def declared_functions(header=HEADER):
+    """Names of every function declared in include/qdec.h."""
+    with open(header) as f:
+        text = f.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qdec_[a-z_0-9]+)\s*\(", text)))
+
+
+class Lib:
+    """Thin wrapper: one method per entry point, raising on error."""
+
+    def __init__(self, path=LIB_PATH):
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"libqdec.so not found at {path}; build it with "
+                "`python -m qdec.build` (or __graft_entry__.build())")
+        self.path = path
+        self.so = ctypes.CDLL(path)
+        so = self.so
+        so.qdec_version.restype = ctypes.c_int
+        so.qdec_last_error.restype = ctypes.c_char_p
+        so.qdec_device_count.restype = ctypes.c_int
+        so.qdec_tiled_offset.restype = ctypes.c_int64
+        so.qdec_tiled_offset.argtypes = [ctypes.c_int64] * 3
+        so.qdec_pack_tiles.argtypes = [P, P, ctypes.c_int64, ctypes.c_int64, P]
+        for name, st in (("qdec_embed", EmbedArgs), ("qdec_gemm", GemmArgs), ("qdec_attn", AttnArgs),
+                         ("qdec_ngram_draft", DraftArgs), ("qdec_spec_accept", AcceptArgs)):
+            fn = getattr(so, name)
+            fn.argtypes = [ctypes.POINTER(st), P]
+            fn.restype = ctypes.c_int
+        for name, st in (("qdec_gemm_workspace", GemmArgs), ("qdec_attn_workspace", AttnArgs)):
+            fn = getattr(so, name)
+            fn.argtypes = [ctypes.POINTER(st), ctypes.POINTER(ctypes.c_size_t),
+                           ctypes.POINTER(ctypes.c_size_t)]
+            fn.restype = ctypes.c_int
+
+    def _check(self, fn, rc):
+        if rc != 0:
+            raise QdecError(fn, rc, self.so.qdec_last_error().decode(errors="replace"))
+
+    def version(self):
+        return self.so.qdec_version()
+
+    def device_count(self):
+        return self.so.qdec_device_count()
+
+    def last_error(self):
+        return self.so.qdec_last_error().decode(errors="replace")
+
+    def tiled_offset(self, n, k, K):
+        return self.so.qdec_tiled_offset(n, k, K)
+
+    def pack_tiles(self, src, dst, n, k, stream):
+        self._check("qdec_pack_tiles", self.so.qdec_pack_tiles(src, dst, n, k, stream))
+
+    def embed(self, args, stream):
+        self._check("qdec_embed", self.so.qdec_embed(ctypes.byref(args), stream))
+
+    def gemm(self, args, stream):
+        self._check("qdec_gemm", self.so.qdec_gemm(ctypes.byref(args), stream))
+
+    def attn(self, args, stream):
+        self._check("qdec_attn", self.so.qdec_attn(ctypes.byref(args), stream))
+
+    def ngram_draft(self, args, stream):
+        self._check("qdec_ngram_draft", self.so.qdec_ngram_draft(ctypes.byref(args), stream))
+
+    def spec_accept(self, args, stream):
+        self._check("qdec_spec_accept", self.so.qdec_spec_accept(ctypes.byref(args), stream))
+
+    def gemm_workspace(self, args):
+        pb, cb = ctypes.c_size_t(), ctypes.c_size_t()
+        self._check("qdec_gemm_workspace",
+                    self.so.qdec_gemm_workspace(ctypes.byref(args), ctypes.byref(pb), ctypes.byref(cb)))
+        return pb.value, cb.value
+
+    def attn_workspace(self, args):
+        pb, cb = ctypes.c_size_t(), ctypes.c_size_t()
+        self._check("qdec_attn_workspace",
+                    self.so.qdec_attn_workspace(ctypes.byref(args), ctypes.byref(pb), ctypes.byref(cb)))
+        return pb.value, cb.value
+
+
+_LIB = None
+
+
+def lib():
+    """The process-wide library handle (loaded on first use)."""
+    global _LIB
+    if _LIB is None:
+        _LIB = Lib()
+    return _LIB

@@ -1,0 +1,349 @@
+"""Device-side state of the decode engine and the step that drives the kernels.
+
+``DeviceModel`` holds the packed weights of one Qwen3 checkpoint in HBM:
+
+* per role one contiguous buffer over all layers, each layer's matrix in the
+  tiled MFMA layout of include/qdec.h -- ``qkv`` ([q; k; v] rows, 6144 x 2560
+  for Qwen3-4B, as engine/engine.py:273-275 concatenates them), ``o``,
+  ``gate_up`` ([gate; up] rows, engine/engine.py:277), ``down``;
+* the embedding once, tiled; the tied lm_head streams the same buffer
+  (engine/engine.py:266-269);
+* norm weights row-major.
+
+``DecodeState`` holds everything one (batch, capacity) shape needs: the static
+KV cache, the activation buffers, the per-step device scalars (``ids``,
+``lens``) and the scratch of the split reductions.  ``run_step`` issues one
+forward over ``t_rows`` rows per sequence -- plain decode (1), speculative
+verify (k + 1) or a prefill chunk -- as ~5 kernel launches per layer on one
+stream, so it can be captured into a hipGraph as is.
+
+Per-role launch plans are functions of the matrix shape only, never of the
+row count: that keeps every output element's summation order the same for a
+1-row and a 36-row call (the basis of lossless speculation).
+"""
+
+import math
+
+import torch
+
+from . import capi
+
+GEMM_MAX_ROWS = 64
+ATTN_MAX_T = 16
+ATTN_TARGET_WGS = 2048
+# Loss-free speculation needs identical arithmetic in the plain and verify
+# steps, so attention chunking depends on (batch, capacity) only.
+
+
+def round_up(x, m):
+    return (x + m - 1) // m * m
+
+
+class ModelConfig:
+    """The shape fields of a Hugging Face Qwen3 config dict."""
+
+    def __init__(self, cfg):
+        self.raw = dict(cfg)
+        self.hidden = cfg["hidden_size"]
+        self.inter = cfg["intermediate_size"]
+        self.n_layers = cfg["num_hidden_layers"]
+        self.nq = cfg["num_attention_heads"]
+        self.nkv = cfg["num_key_value_heads"]
+        self.head_dim = cfg.get("head_dim") or self.hidden // self.nq
+        self.vocab = cfg["vocab_size"]
+        self.eps = float(cfg.get("rms_norm_eps", 1e-6))
+        rp = cfg.get("rope_parameters") or {}
+        self.theta = float(rp.get("rope_theta", cfg.get("rope_theta", 10000.0)))
+        self.tied = bool(cfg.get("tie_word_embeddings", True))
+        self.n_qkv = (self.nq + 2 * self.nkv) * self.head_dim
+
+    def check_supported(self):
+        problems = []
+        if self.head_dim != 128:
+            problems.append(f"head_dim {self.head_dim} (kernels implement 128)")
+        if self.nq != 4 * self.nkv:
+            problems.append(f"{self.nq} q heads / {self.nkv} kv heads (kernels implement 4 per kv head)")
+        for name, v, m in (("hidden", self.hidden, 32), ("intermediate", self.inter, 32),
+                           ("vocab", self.vocab, 16)):
+            if v % m:
+                problems.append(f"{name} {v} not a multiple of {m}")
+        if not self.tied:
+            problems.append("untied lm_head (engine streams the tied embedding)")
+        if problems:
+            raise ValueError("unsupported Qwen3 shape: " + "; ".join(problems))
+
+
+def rope_tables(cap, head_dim, theta):
+    """bf16 cos/sin ``[cap, head_dim]`` exactly as Transformers' rotary module
+    builds them (transformers/models/qwen3/modeling_qwen3.py:106-137): fp32
+    ``inv_freq``, one fp32 product per (position, frequency), fp32 cos/sin,
+    then one rounding to bf16.  Computed on the host so the values do not
+    depend on a device libm."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).to(torch.float32) / head_dim))
+    pos = torch.arange(cap, dtype=torch.float32)
+    freqs = pos[:, None] * inv_freq[None, :]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+
+
+def role_plan(n, k, role):
+    """(ksplit, waves, tiles_per_wg) of one projection role.
+
+    Output tiles are 16 columns.  Roles with few tiles (N = hidden) split k
+    across workgroups so the grid covers all 256 CUs; the others keep one
+    workgroup per tile.  Only (n, k, role) decide it."""
+    ks = k // 32
+    ntiles = n // 16
+    waves = 4
+    ksplit = 1
+    if role in ("o", "down"):
+        # Aim for >= 512 workgroups while keeping >= 8 k steps per wave.
+        ksplit = 1
+        for cand in (2, 4, 8):
+            if ks % (cand * waves) == 0 and ks // (cand * waves) >= 8 and ntiles * ksplit < 512:
+                ksplit = cand
+    while (ks // ksplit) % waves:
+        waves //= 2
+    tiles = 1
+    if role == "lm":
+        for cand in (4, 2, 1):
+            if ntiles % cand == 0:
+                tiles = cand
+                break
+    return ksplit, waves, tiles
+
+
+def attn_chunk(batch, nkv, cap):
+    """Slots per attention workgroup: enough chunks to launch ~2048
+    workgroups, at least 64 slots each (absolute-slot chunking)."""
+    want = max(1, math.ceil(ATTN_TARGET_WGS / (batch * nkv)))
+    chunk = round_up(max(1, math.ceil(cap / want)), 32)
+    return max(64, min(chunk, round_up(cap, 32)))
+
+
+class DeviceModel:
+    """Packed Qwen3 weights in device memory."""
+
+    def __init__(self, cfg, tensors, device="cuda:0", stream=None):
+        self.cfg = ModelConfig(cfg)
+        self.cfg.check_supported()
+        self.device = torch.device(device)
+        self.lib = capi.lib()
+        c = self.cfg
+        L, H, I, V = c.n_layers, c.hidden, c.inter, c.vocab
+        dev = self.device
+        bf = torch.bfloat16
+        stream = stream or torch.cuda.current_stream(dev)
+        s = stream.cuda_stream
+
+        def get(name):
+            t = tensors[name]
+            return t.to(device=dev, dtype=bf).contiguous()
+
+        def pack(dst, src):
+            n, k = src.shape
+            self.lib.pack_tiles(src.data_ptr(), dst.data_ptr(), n, k, s)
+
+        self.w_qkv = torch.empty((L, c.n_qkv * H), dtype=bf, device=dev)
+        self.w_o = torch.empty((L, H * c.nq * c.head_dim), dtype=bf, device=dev)
+        self.w_gu = torch.empty((L, 2 * I * H), dtype=bf, device=dev)
+        self.w_down = torch.empty((L, H * I), dtype=bf, device=dev)
+        self.in_w = torch.empty((L, H), dtype=bf, device=dev)
+        self.post_w = torch.empty((L, H), dtype=bf, device=dev)
+        self.q_norm = torch.empty((L, c.head_dim), dtype=bf, device=dev)
+        self.k_norm = torch.empty((L, c.head_dim), dtype=bf, device=dev)
+        with torch.cuda.stream(stream):
+            for i in range(L):
+                p = f"model.layers.{i}."
+                qkv = torch.cat([get(p + "self_attn.q_proj.weight"), get(p + "self_attn.k_proj.weight"),
+                                 get(p + "self_attn.v_proj.weight")], dim=0)
+                pack(self.w_qkv[i], qkv)
+                pack(self.w_o[i], get(p + "self_attn.o_proj.weight"))
+                gu = torch.cat([get(p + "mlp.gate_proj.weight"), get(p + "mlp.up_proj.weight")], dim=0)
+                pack(self.w_gu[i], gu)
+                pack(self.w_down[i], get(p + "mlp.down_proj.weight"))
+                self.in_w[i].copy_(get(p + "input_layernorm.weight"))
+                self.post_w[i].copy_(get(p + "post_attention_layernorm.weight"))
+                self.q_norm[i].copy_(get(p + "self_attn.q_norm.weight"))
+                self.k_norm[i].copy_(get(p + "self_attn.k_norm.weight"))
+                del qkv, gu
+            self.norm_w = get("model.norm.weight")
+            self.emb = torch.empty((V * H,), dtype=bf, device=dev)
+            pack(self.emb, get("model.embed_tokens.weight"))
+        stream.synchronize()
+        self.plans = {
+            "qkv": role_plan(c.n_qkv, H, "qkv"),
+            "o": role_plan(H, c.nq * c.head_dim, "o"),
+            "gate_up": role_plan(I, H, "gate_up"),
+            "down": role_plan(H, I, "down"),
+            "lm": role_plan(V, H, "lm"),
+        }
+
+    def weight_bytes(self):
+        """Bytes of weights one decode step streams (norm vectors included)."""
+        ts = (self.w_qkv, self.w_o, self.w_gu, self.w_down, self.emb, self.in_w, self.post_w,
+              self.q_norm, self.k_norm, self.norm_w)
+        return sum(t.numel() * t.element_size() for t in ts)
+
+
+class DecodeState:
+    """Buffers for one (batch, capacity) shape and the step over them."""
+
+    def __init__(self, model, batch, capacity, max_t=1, keep_logits=False):
+        c = model.cfg
+        self.model, self.lib = model, model.lib
+        self.batch = batch
+        self.cap = round_up(capacity, 32)
+        self.max_t = max(1, min(max_t, ATTN_MAX_T, GEMM_MAX_ROWS // batch))
+        if batch > GEMM_MAX_ROWS:
+            raise ValueError(f"batch {batch} > {GEMM_MAX_ROWS} rows per step")
+        self.max_rows = batch * self.max_t
+        dev, bf = model.device, torch.bfloat16
+        L, H, D = c.n_layers, c.hidden, c.head_dim
+        self.chunk = attn_chunk(batch, c.nkv, self.cap)
+        cache_shape = (L, batch, c.nkv, self.cap, D)
+        self.k_cache = torch.zeros(cache_shape, dtype=bf, device=dev)
+        self.v_cache = torch.zeros(cache_shape, dtype=bf, device=dev)
+        self.layer_elems = batch * c.nkv * self.cap * D
+        R = self.max_rows
+        self.h = torch.zeros((R, H), dtype=bf, device=dev)
+        self.qkv = torch.zeros((R, c.n_qkv), dtype=bf, device=dev)
+        self.attn_out = torch.zeros((R, c.nq * D), dtype=bf, device=dev)
+        self.act = torch.zeros((R, c.inter), dtype=bf, device=dev)
+        self.logits = torch.zeros((R, c.vocab), dtype=bf, device=dev) if keep_logits else None
+        self.ids = torch.zeros((R,), dtype=torch.int64, device=dev)
+        self.out_tok = torch.zeros((R,), dtype=torch.int64, device=dev)
+        self.lens = torch.zeros((batch,), dtype=torch.int32, device=dev)
+        cos, sin = rope_tables(self.cap, D, c.theta)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+        # scratch: sized for the largest call of every kernel.
+        gw = 0
+        gc = 1
+        for role in ("qkv", "o", "gate_up", "down", "lm"):
+            a = self._gemm_args(role, 0, R)
+            pb, cb = self.lib.gemm_workspace(a)
+            gw, gc = max(gw, pb), max(gc, cb)
+        self.gemm_partial = torch.zeros((max(gw, 16) // 4 + 4,), dtype=torch.float32, device=dev)
+        self.gemm_counters = torch.zeros((max(gc, 4) // 4 + 4,), dtype=torch.int32, device=dev)
+        aw, ac = self.lib.attn_workspace(self._attn_args(0, self.max_t))
+        self.attn_partial = torch.zeros((max(aw, 16) // 4 + 4,), dtype=torch.float32, device=dev)
+        self.attn_counters = torch.zeros((max(ac, 4) // 4 + 4,), dtype=torch.int32, device=dev)
+        self._gemm_cache = {}
+        self._attn_cache = {}
+
+    # ----------------------------------------------------------- arguments
+    def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None):
+        m, c = self.model, self.model.cfg
+        ksplit, waves, tiles = m.plans[role]
+        a = capi.GemmArgs()
+        a.eps, a.rows, a.ksplit, a.waves, a.tiles_per_wg = c.eps, rows, ksplit, waves, 1
+        if role == "qkv":
+            a.x, a.w, a.out = self.h.data_ptr(), m.w_qkv[layer].data_ptr(), self.qkv.data_ptr()
+            a.norm_w = m.in_w[layer].data_ptr()
+            a.n, a.k, a.flags = c.n_qkv, c.hidden, capi.NORM_IN
+        elif role == "o":
+            a.x, a.w, a.res = self.attn_out.data_ptr(), m.w_o[layer].data_ptr(), self.h.data_ptr()
+            a.n, a.k, a.flags = c.hidden, c.nq * c.head_dim, capi.RES_OUT
+        elif role == "gate_up":
+            a.x, a.w, a.out = self.h.data_ptr(), m.w_gu[layer].data_ptr(), self.act.data_ptr()
+            a.norm_w = m.post_w[layer].data_ptr()
+            a.n, a.k, a.flags = c.inter, c.hidden, capi.NORM_IN | capi.GLU
+        elif role == "down":
+            a.x, a.w, a.res = self.act.data_ptr(), m.w_down[layer].data_ptr(), self.h.data_ptr()
+            a.n, a.k, a.flags = c.hidden, c.inter, capi.RES_OUT
+        elif role == "lm":
+            a.x, a.w = self.h.data_ptr(), m.emb.data_ptr()
+            a.norm_w = m.norm_w.data_ptr()
+            a.n, a.k, a.flags = c.vocab, c.hidden, capi.NORM_IN | capi.ARGMAX
+            a.tiles_per_wg = tiles
+            a.out = self.logits.data_ptr() if self.logits is not None else None
+            a.ids_out = (ids_out if ids_out is not None else self.ids).data_ptr()
+            a.lens_inc = lens_inc.data_ptr() if lens_inc is not None else None
+        if hasattr(self, "gemm_partial"):
+            a.partial = self.gemm_partial.data_ptr()
+            a.counters = self.gemm_counters.data_ptr()
+        return a
+
+    def _attn_args(self, layer, t_rows):
+        m, c = self.model, self.model.cfg
+        a = capi.AttnArgs()
+        a.qkv, a.q_norm_w, a.k_norm_w = self.qkv.data_ptr(), m.q_norm[layer].data_ptr(), m.k_norm[layer].data_ptr()
+        a.cos_tab, a.sin_tab, a.lens = self.cos.data_ptr(), self.sin.data_ptr(), self.lens.data_ptr()
+        a.k_cache = self.k_cache[layer].data_ptr()
+        a.v_cache = self.v_cache[layer].data_ptr()
+        a.out = self.attn_out.data_ptr()
+        if hasattr(self, "attn_partial"):
+            a.partial, a.counters = self.attn_partial.data_ptr(), self.attn_counters.data_ptr()
+        a.eps, a.sm_scale = c.eps, c.head_dim ** -0.5
+        a.batch, a.t_rows, a.nq, a.nkv, a.head_dim = self.batch, t_rows, c.nq, c.nkv, c.head_dim
+        a.cap, a.chunk = self.cap, self.chunk
+        return a
+
+    # ---------------------------------------------------------------- step
+    def run_step(self, t_rows=1, lm_head=True, ids_out=None, advance=True, stream=None):
+        """One forward of ``t_rows`` rows per sequence at positions
+        ``lens[b] .. lens[b] + t_rows - 1`` (device ``lens``), fed from
+        ``ids[b * t_rows + t]``.
+
+        With ``lm_head`` the greedy pick of every row goes to ``ids_out``
+        (default ``ids``: the next step's input) and, with ``advance``,
+        ``lens[b] += 1`` (plain decode; requires ``t_rows == 1``)."""
+        if t_rows < 1 or t_rows > self.max_t:
+            raise ValueError(f"t_rows {t_rows} not in [1, {self.max_t}]")
+        if advance and lm_head and t_rows != 1:
+            raise ValueError("advance needs t_rows == 1")
+        lib, m, c = self.lib, self.model, self.model.cfg
+        s = (stream or torch.cuda.current_stream(m.device)).cuda_stream
+        rows = self.batch * t_rows
+        e = capi.EmbedArgs()
+        e.ids, e.emb, e.h = self.ids.data_ptr(), m.emb.data_ptr(), self.h.data_ptr()
+        e.rows, e.hidden, e.vocab = rows, c.hidden, c.vocab
+        lib.embed(e, s)
+        for i in range(c.n_layers):
+            lib.gemm(self._cached_gemm("qkv", i, rows), s)
+            lib.attn(self._cached_attn(i, t_rows), s)
+            lib.gemm(self._cached_gemm("o", i, rows), s)
+            lib.gemm(self._cached_gemm("gate_up", i, rows), s)
+            lib.gemm(self._cached_gemm("down", i, rows), s)
+        if lm_head:
+            a = self._gemm_args("lm", 0, rows, ids_out=ids_out,
+                                lens_inc=self.lens if (advance and t_rows == 1) else None)
+            lib.gemm(a, s)
+
+    def _cached_gemm(self, role, layer, rows):
+        key = (role, layer, rows)
+        a = self._gemm_cache.get(key)
+        if a is None:
+            a = self._gemm_args(role, layer, rows)
+            self._gemm_cache[key] = a
+        return a
+
+    def _cached_attn(self, layer, t_rows):
+        key = (layer, t_rows)
+        a = self._attn_cache.get(key)
+        if a is None:
+            a = self._attn_args(layer, t_rows)
+            self._attn_cache[key] = a
+        return a
+
+    # ------------------------------------------------------------- prefill
+    def prefill(self, prompt, stream=None):
+        """Fill cache slots ``0 .. S-1`` from ``prompt`` ``[B, S]`` (device
+        int64) in chunks of ``max_t`` rows per sequence through the same
+        kernels as decode; returns with ``ids[:B]`` = the first generated
+        token and ``lens[:] = S``."""
+        B, S = prompt.shape
+        if B != self.batch:
+            raise ValueError(f"prompt batch {B} != state batch {self.batch}")
+        if S < 1 or S >= self.cap:
+            raise ValueError(f"prompt length {S} must be in [1, {self.cap})")
+        T = self.max_t
+        for c0 in range(0, S, T):
+            t = min(T, S - c0)
+            self.ids[:B * t].view(B, t).copy_(prompt[:, c0:c0 + t])
+            self.lens.fill_(c0)
+            last = c0 + t >= S
+            self.run_step(t_rows=t, lm_head=last, ids_out=self.out_tok, advance=False, stream=stream)
+        t = (S - 1) % T + 1
+        self.ids[:B].copy_(self.out_tok[:B * t].view(B, t)[:, t - 1])
+        self.lens.fill_(S)

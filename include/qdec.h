@@ -1,0 +1,232 @@
+/*
+ * qdec.h -- C ABI of the MI355X (gfx950) Qwen3 greedy-decode kernel library.
+ *
+ * Every decode-step operation of a Qwen3 model (the reference engine's
+ * engine/kernels/{ops,fused}.py and notes/v10/spec.py, all Triton) is one
+ * hand-written HIP kernel behind one entry point here.  Conventions:
+ *
+ *   - All device pointers are owned by the caller (the Python host allocates
+ *     them as PyTorch-ROCm tensors).  The library never allocates, frees or
+ *     synchronises inside an entry point, so every call may be recorded into
+ *     a hipGraph.  Scratch buffers (split partials, arrival counters) are
+ *     caller-provided; their sizes come from the *_workspace queries.
+ *   - Arrival counters must be zero before the first call that uses them;
+ *     every kernel leaves the counters it used at zero again, so one zeroed
+ *     buffer serves any number of calls on one stream.  Two calls that share
+ *     a counter or partial buffer must not run concurrently.
+ *   - Per-step scalars (token ids, cache lengths) are device pointers, never
+ *     host ints, so a captured graph stays valid across replays.
+ *   - Entry points return QDEC_OK (0) or a negative QDEC_E* code; the text of
+ *     the last error on the calling thread is qdec_last_error().  Argument
+ *     validation happens before any HIP call, so it also works on a host
+ *     without a GPU.
+ *   - bf16 tensors are passed as void* holding IEEE bfloat16 bit patterns.
+ *   - `stream` is a hipStream_t (NULL = the default stream).
+ *
+ * Data layouts (all row-major unless stated):
+ *   tiled weight  : a [N, K] bf16 matrix (N % 16 == 0, K % 32 == 0) stored as
+ *                   1 KiB blocks, block (nt, ks) at element ((nt*(K/32))+ks)*512;
+ *                   inside a block lane l (0..63) owns elements [8l, 8l+8) =
+ *                   W[16*nt + (l & 15)][32*ks + 8*(l >> 4) + e], e = 0..7.
+ *                   One wavefront reads one block with one 16-byte load per
+ *                   lane; the block is the A operand of one
+ *                   v_mfma_f32_16x16x32_bf16.
+ *   K cache slab  : [batch][n_kv_heads][cap][head_dim] bf16, per layer.
+ *   V cache slab  : [batch][n_kv_heads][cap/8][head_dim][8] bf16, per layer:
+ *                   8 consecutive slots of one channel are 16 contiguous bytes
+ *                   (the A operand of the P.V product).
+ *   cap is a multiple of 32.
+ */
+#ifndef QDEC_H
+#define QDEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QDEC_ABI_VERSION 1
+
+#define QDEC_OK 0
+#define QDEC_EINVAL (-1)       /* bad shape or argument */
+#define QDEC_EALIGN (-2)       /* pointer not 16-byte aligned */
+#define QDEC_EUNSUPPORTED (-3) /* configuration the kernels do not implement */
+#define QDEC_ELAUNCH (-4)      /* hipGetLastError after the launch */
+#define QDEC_ENODEV (-5)       /* no usable HIP device */
+
+/* qdec_gemm flags */
+#define QDEC_NORM_IN 1u  /* x is the residual stream; RMSNorm(x) * norm_w feeds the product */
+#define QDEC_GLU 2u      /* w holds gate tiles then up tiles; out = silu(gate) * up */
+#define QDEC_RES_OUT 4u  /* res += x @ W^T, rounded as the reference rounds */
+#define QDEC_ARGMAX 8u   /* greedy argmax of the bf16 logits of every row into ids_out */
+
+typedef void *qdec_stream_t;
+
+/* Library ABI version (QDEC_ABI_VERSION). */
+int qdec_version(void);
+
+/* Text of the last error returned on this thread ("" if none). */
+const char *qdec_last_error(void);
+
+/* Number of visible HIP devices (0 on a host without a GPU; never fails). */
+int qdec_device_count(void);
+
+/* ------------------------------------------------------------------ layout */
+
+/* Element offset of W[n][k] inside the tiled layout of a [*, K] matrix.
+ * Host-only helper; returns -1 for an invalid K or index. */
+int64_t qdec_tiled_offset(int64_t n, int64_t k, int64_t K);
+
+/* Repack a row-major [n, k] bf16 matrix into the tiled layout.
+ * Replaces the load-time packing of engine/engine.py:271-287 (which only
+ * concatenates q|k|v and gate|up; the tiling is this library's own). */
+int qdec_pack_tiles(const void *src, void *dst, int64_t n, int64_t k,
+                    qdec_stream_t stream);
+
+/* ------------------------------------------------------------- embedding */
+
+/* h[m, :] = E[ids[m], :] for m < rows.  E is the tiled [vocab, hidden]
+ * embedding (the same buffer feeds the tied lm_head).
+ * Replaces fused.embed_ssq, engine/kernels/fused.py:341-357 (the sum of
+ * squares it also produced is recomputed by each NORM_IN consumer). */
+typedef struct {
+  const int64_t *ids; /* [rows] */
+  const void *emb;    /* tiled [vocab, hidden] bf16 */
+  void *h;            /* [rows, hidden] bf16 out */
+  int32_t rows;
+  int32_t hidden;
+  int32_t vocab;
+} qdec_embed_args;
+int qdec_embed(const qdec_embed_args *a, qdec_stream_t stream);
+
+/* ------------------------------------------------------------ skinny GEMM */
+
+/* y[m, n] = sum_k x'[m, k] * W[n, k] over the tiled weight, for m < rows
+ * (1 <= rows <= 64), fp32 accumulation, one rounding to bf16, then:
+ *   plain   : out = bf16(y)
+ *   NORM_IN : x' = bf16(norm_w * bf16(x * rsqrt(mean(x^2) + eps))) per row
+ *   GLU     : out = bf16(bf16(silu(bf16(y_gate))) * bf16(y_up)), n = #act cols
+ *   RES_OUT : res = bf16(res + bf16(y))   (in place; out unused)
+ *   ARGMAX  : ids_out[m] = lowest index of max_n bf16(y[m, n]);
+ *             out (optional, may be NULL) receives the bf16 logits;
+ *             lens_inc (optional) gets lens_inc[m] += 1 after the pick.
+ * The summation order of every output element depends only on k, ksplit and
+ * waves -- never on rows -- so a row's result is bit-identical whether it is
+ * computed alone or inside a larger batch.
+ * Replaces fused.gemv (engine/kernels/fused.py:33-338: NORM_IN / GLU /
+ * RES_OUT / split-K) and the lm_head + torch.argmax pair of
+ * engine/engine.py:492-498, 542-545. */
+typedef struct {
+  const void *x;        /* [rows, k] bf16 */
+  const void *w;        /* tiled weight: [n, k], or [2n, k] with QDEC_GLU */
+  void *out;            /* [rows, n] bf16 (plain, GLU, optional with ARGMAX) */
+  void *res;            /* [rows, n] bf16 residual (RES_OUT) */
+  const void *norm_w;   /* [k] bf16 (NORM_IN) */
+  float *partial;       /* split-K / argmax scratch (qdec_gemm_workspace) */
+  uint32_t *counters;   /* zeroed arrival counters (qdec_gemm_workspace) */
+  int64_t *ids_out;     /* [rows] (ARGMAX) */
+  int32_t *lens_inc;    /* [rows] or NULL (ARGMAX) */
+  float eps;
+  int32_t rows;
+  int32_t n;
+  int32_t k;
+  uint32_t flags;
+  int32_t ksplit;       /* workgroups sharing one output tile along k (>= 1) */
+  int32_t waves;        /* wavefronts per workgroup, splitting its k range (1..8) */
+  int32_t tiles_per_wg; /* output tiles per workgroup, ARGMAX only (>= 1) */
+} qdec_gemm_args;
+int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream);
+/* Scratch sizes (bytes) a qdec_gemm call with these arguments needs. */
+int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes,
+                        size_t *counter_bytes);
+
+/* --------------------------------------------------- GQA decode attention */
+
+/* For every sequence b and query row t < t_rows (absolute position
+ * lens[b] + t), from the raw projection row qkv[b*t_rows + t]:
+ *   q, k = per-head RMSNorm (q_norm_w / k_norm_w, rounded as Qwen3RMSNorm),
+ *          then RoPE  bf16(bf16(y*cos) + bf16(rotate_half(y)*sin));
+ *   the new k and the raw v are written into cache slot lens[b] + t;
+ *   out  = softmax(q . K^T / sqrt(D)) . V over slots 0 .. lens[b] + t,
+ *          fp32 scores and accumulation, probabilities rounded to bf16
+ *          before the P.V product (flash-decoding), output rounded once.
+ * Slots are processed in chunks of `chunk` slots keyed to absolute slot
+ * numbers, one workgroup per (chunk, kv head, sequence); the last workgroup
+ * of a (sequence, kv head) to finish merges the chunk partials in chunk
+ * order.  A row's result therefore does not depend on t_rows.
+ * Replaces fused.attention_fused (engine/kernels/fused.py:360-479),
+ * ops.qkv_post + ops.DecodeAttention (engine/kernels/ops.py:84-431) and the
+ * multi-row verify attention of notes/v10/spec.py:111-182. */
+typedef struct {
+  const void *qkv;      /* [batch*t_rows, (nq + 2*nkv)*head_dim] bf16 */
+  const void *q_norm_w; /* [head_dim] bf16 */
+  const void *k_norm_w; /* [head_dim] bf16 */
+  const void *cos_tab;  /* [cap, head_dim] bf16 */
+  const void *sin_tab;  /* [cap, head_dim] bf16 */
+  const int32_t *lens;  /* [batch] slots already in the cache per sequence */
+  void *k_cache;        /* K slab of this layer */
+  void *v_cache;        /* V slab of this layer */
+  void *out;            /* [batch*t_rows, nq*head_dim] bf16 */
+  float *partial;       /* chunk partials (qdec_attn_workspace) */
+  uint32_t *counters;   /* zeroed arrival counters (qdec_attn_workspace) */
+  float eps;
+  float sm_scale;       /* 1/sqrt(head_dim) */
+  int32_t batch;
+  int32_t t_rows;       /* query rows per sequence (1 = plain decode) */
+  int32_t nq;
+  int32_t nkv;
+  int32_t head_dim;     /* 128 */
+  int32_t cap;          /* slots per sequence, multiple of 32 */
+  int32_t chunk;        /* slots per workgroup, multiple of 32 */
+} qdec_attn_args;
+int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream);
+int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,
+                        size_t *counter_bytes);
+
+/* ------------------------------------------------ n-gram speculation */
+
+/* Suffix-match drafter over each sequence's own history hist[b, 0..lens[b]]
+ * (hist[b, lens[b]] is the token not yet fed).  Pattern = the last `primary`
+ * tokens; the most recent earlier occurrence whose k-token continuation lies
+ * inside the history wins; otherwise the same with `backoff` tokens;
+ * otherwise the draft is all zeros.  Writes ids[b*(k+1)] = hist[b, lens[b]],
+ * ids[b*(k+1) + 1 + t] = draft[b*k + t].
+ * Replaces notes/v10/spec.py:36-108 (_ngram_draft_kernel / ngram_draft). */
+typedef struct {
+  const int64_t *hist; /* [batch, cap] */
+  const int32_t *lens; /* [batch] */
+  int64_t *ids;        /* [batch*(k+1)] out */
+  int64_t *draft;      /* [batch*k] out */
+  int32_t batch;
+  int32_t cap;
+  int32_t primary;
+  int32_t backoff;
+  int32_t k;
+} qdec_draft_args;
+int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream);
+
+/* Longest-prefix greedy acceptance: a = number of leading drafts equal to the
+ * model's argmax at the same row; rows 0..a are appended to the history at
+ * lens[b]+1 ..; lens[b] += a+1.  A sequence with lens[b] >= stop_len is
+ * frozen (a = 0, nothing written).  naccept[b] = a.
+ * Replaces notes/v10/spec.py:185-224 (_accept_kernel / accept). */
+typedef struct {
+  const int64_t *out_tok; /* [batch*(k+1)] argmax per verify row */
+  const int64_t *draft;   /* [batch*k] */
+  int64_t *hist;          /* [batch, cap] */
+  int32_t *lens;          /* [batch] */
+  int32_t *naccept;       /* [batch] out */
+  int32_t batch;
+  int32_t cap;
+  int32_t k;
+  int32_t stop_len;
+} qdec_accept_args;
+int qdec_spec_accept(const qdec_accept_args *a, qdec_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QDEC_H */

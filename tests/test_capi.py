@@ -1,0 +1,141 @@
+"""The C ABI without a GPU: the library loads, exports every symbol that
+include/qdec.h declares, validates arguments before touching HIP, and its
+layout helper agrees with the tiled layout the kernels assume."""
+
+import ctypes
+
+import pytest
+
+from qdec import capi
+
+
+def test_exports_every_declared_symbol(qlib):
+    names = capi.declared_functions()
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(qlib.so, n)]
+    assert not missing, missing
+    assert qlib.version() == 1
+
+
+def test_structs_match_header_fields():
+    """Every field of every args struct in the header exists in the ctypes
+    mirror, in the same order."""
+    import re
+    text = open(capi.HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    for cname, st in (("qdec_embed_args", capi.EmbedArgs), ("qdec_gemm_args", capi.GemmArgs),
+                      ("qdec_attn_args", capi.AttnArgs), ("qdec_draft_args", capi.DraftArgs),
+                      ("qdec_accept_args", capi.AcceptArgs)):
+        body = re.search(r"typedef struct \{([^{}]*)\}\s*" + cname + ";", text).group(1)
+        fields = re.findall(r"\*?\s*(\w+)\s*;", body)
+        assert fields == [f[0] for f in st._fields_], cname
+
+
+def test_device_count_without_gpu_is_safe(qlib):
+    assert qlib.device_count() >= 0
+
+
+def test_tiled_offset_layout(qlib):
+    K = 96
+    seen = set()
+    for n in range(32):
+        for k in range(K):
+            off = qlib.tiled_offset(n, k, K)
+            nt, ks = n // 16, k // 32
+            lane = (n % 16) + 16 * ((k % 32) // 8)
+            assert off == ((nt * (K // 32) + ks) * 64 + lane) * 8 + k % 8
+            seen.add(off)
+    assert seen == set(range(32 * K))  # a permutation of the matrix
+    assert qlib.tiled_offset(0, 0, 100) == -1
+    assert qlib.tiled_offset(0, 96, 96) == -1
+
+
+def _gemm(**kw):
+    a = capi.GemmArgs()
+    a.x = a.w = a.out = a.res = a.norm_w = a.partial = a.counters = a.ids_out = 16
+    a.eps, a.rows, a.n, a.k, a.flags, a.ksplit, a.waves, a.tiles_per_wg = 1e-6, 1, 256, 256, 0, 1, 4, 1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(rows=0), -1, "rows"),
+    (dict(rows=65), -1, "rows"),
+    (dict(n=250), -1, "multiple of 16"),
+    (dict(k=100), -1, "multiple of 32"),
+    (dict(waves=9), -1, "waves"),
+    (dict(ksplit=3), -1, "ksplit"),
+    (dict(flags=capi.GLU), -3, "not supported"),
+    (dict(flags=capi.ARGMAX | capi.NORM_IN, ksplit=2), -3, "ksplit 1"),
+    (dict(tiles_per_wg=2), -1, "tiles_per_wg"),
+    (dict(x=8), -2, "aligned"),
+    (dict(out=None), -1, "null out"),
+])
+def test_gemm_validation(qlib, kw, code, needle):
+    rc = qlib.so.qdec_gemm(ctypes.byref(_gemm(**kw)), None)
+    assert rc == code
+    assert needle in qlib.last_error()
+    with pytest.raises(capi.QdecError):
+        qlib.gemm(_gemm(**kw), None)
+
+
+def test_gemm_workspace_sizes(qlib):
+    pb, cb = qlib.gemm_workspace(_gemm(flags=capi.RES_OUT, ksplit=2, n=2560, k=4096, rows=3))
+    assert pb == 2 * 3 * 2560 * 4 and cb == 160 * 4
+    pb, cb = qlib.gemm_workspace(_gemm(flags=capi.NORM_IN | capi.ARGMAX, n=151936, k=2560, rows=2,
+                                       tiles_per_wg=4))
+    assert pb == 2 * 4 * (9496 // 4) * 2 and cb == 4
+    pb, cb = qlib.gemm_workspace(_gemm(flags=capi.NORM_IN, n=6144, k=2560))
+    assert pb == 0 and cb == 0
+
+
+def _attn(**kw):
+    a = capi.AttnArgs()
+    for f in ("qkv", "q_norm_w", "k_norm_w", "cos_tab", "sin_tab", "lens", "k_cache", "v_cache", "out",
+              "partial", "counters"):
+        setattr(a, f, 16)
+    a.eps, a.sm_scale = 1e-6, 128 ** -0.5
+    a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = 2, 1, 32, 8, 128, 256, 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(head_dim=64), -3), (dict(nq=16), -3), (dict(t_rows=17), -1), (dict(cap=100), -1),
+    (dict(chunk=48), -1), (dict(out=None), -1), (dict(partial=None), -1), (dict(qkv=8), -2),
+])
+def test_attn_validation(qlib, kw, code):
+    assert qlib.so.qdec_attn(ctypes.byref(_attn(**kw)), None) == code
+
+
+def test_attn_workspace(qlib):
+    pb, cb = qlib.attn_workspace(_attn(t_rows=3, batch=2, cap=256, chunk=64))
+    assert pb == 4 * 2 * 8 * 4 * 12 * 130 and cb == 2 * 8 * 4
+    pb, cb = qlib.attn_workspace(_attn(cap=64, chunk=64))
+    assert pb == 0 and cb == 0
+
+
+def test_other_validation(qlib):
+    assert qlib.so.qdec_pack_tiles(None, None, 16, 32, None) == -1
+    assert qlib.so.qdec_pack_tiles(16, 16, 17, 32, None) == -1
+    e = capi.EmbedArgs(ids=16, emb=16, h=16, rows=1, hidden=100, vocab=16)
+    assert qlib.so.qdec_embed(ctypes.byref(e), None) == -1
+    d = capi.DraftArgs(hist=16, lens=16, ids=16, draft=16, batch=1, cap=8, primary=3, backoff=2, k=0)
+    assert qlib.so.qdec_ngram_draft(ctypes.byref(d), None) == -1
+    a = capi.AcceptArgs(out_tok=16, draft=16, hist=16, lens=16, naccept=None, batch=1, cap=8, k=1, stop_len=1)
+    assert qlib.so.qdec_spec_accept(ctypes.byref(a), None) == -1
+
+
+def test_role_plans_do_not_depend_on_rows():
+    from qdec.runtime import attn_chunk, role_plan
+    for role, n, k in (("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 9728, 2560),
+                       ("down", 2560, 9728), ("lm", 151936, 2560)):
+        ks, w, t = role_plan(n, k, role)
+        assert (k // 32) % (ks * w) == 0
+        assert (n // 16) % t == 0
+    assert role_plan(2560, 9728, "down")[0] > 1 and role_plan(2560, 4096, "o")[0] > 1
+    for b, cap in ((1, 800), (4, 1568), (32, 4384)):
+        c = attn_chunk(b, 8, cap)
+        assert c % 32 == 0 and c >= 64

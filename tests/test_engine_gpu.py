@@ -1,0 +1,134 @@
+"""The engine end to end on the GPU against the oracle.
+
+Model: Qwen3-4B widths (hidden 2560, intermediate 9728, 32 q / 8 kv heads,
+head_dim 128, vocab 151936, tied, theta 5e6) with 2 layers, seeded random
+init, norm weights jittered N(1, 0.05) so a norm applied at the wrong place
+shows.  Parity is judged teacher-forced on the engine's own tokens, as the
+reference's judge replays a submission (QWEN_ENGINE_CONTRACT.md:105-123):
+
+* per-step logits within 2e-2 of the row's max |logit| (normalised max err);
+* every emitted token is the oracle's argmax, or the oracle's top-2 gap at
+  that step is below the tolerance (a documented near-tie);
+* the graph-replayed generate, the eager step and the speculative path emit
+  identical tokens.
+"""
+
+import os
+
+import pytest
+import torch
+
+from oracle.qwen3_oracle import Qwen3Oracle, normalized_max_err, top2_gap
+from qdec.checkpoint import load_tensors, qwen3_config, write_checkpoint
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def ckpt(tmp_path_factory):
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    cfg = qwen3_config(num_hidden_layers=2)
+    path = str(tmp_path_factory.mktemp("qwen3_l2"))
+    write_checkpoint(path, cfg, seed=0, norm_jitter=0.05)
+    return path, cfg
+
+
+@pytest.fixture(scope="module")
+def engine(ckpt):
+    from engine import Engine
+    return Engine(ckpt[0])
+
+
+@pytest.fixture(scope="module")
+def oracle(ckpt):
+    path, cfg = ckpt
+    return Qwen3Oracle(cfg, load_tensors(path), mode="bf16", attn="decode")
+
+
+def prompts(B, S, seed, vocab=151936):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (B, S), generator=g)
+
+
+def run_state(engine, prompt, n):
+    """Eager runtime steps with logits kept: (tokens [B, n], logits [B, n, V])."""
+    from qdec.runtime import DecodeState
+    B, S = prompt.shape
+    st = DecodeState(engine.model, B, S + n + 18, max_t=16, keep_logits=True)
+    st.prefill(prompt.to(engine.device))
+    t_last = (S - 1) % st.max_t + 1
+    first_logits = st.logits[:B * t_last].view(B, t_last, -1)[:, t_last - 1].float().cpu()
+    toks = [st.ids[:B].cpu()]
+    logits = [first_logits]
+    for _ in range(n - 1):
+        st.run_step(t_rows=1)
+        toks.append(st.ids[:B].cpu())
+        logits.append(st.logits[:B].float().cpu())
+    torch.cuda.synchronize()
+    assert st.lens.cpu().tolist() == [S + n - 1] * B
+    return torch.stack(toks, 1), torch.stack(logits, 1)
+
+
+@pytest.mark.parametrize("B,S,n,seed", [(1, 40, 10, 1), (3, 21, 8, 2)])
+def test_logits_and_tokens_vs_oracle(engine, oracle, B, S, n, seed):
+    prompt = prompts(B, S, seed)
+    toks, logits = run_state(engine, prompt, n)
+    ref = oracle.teacher_forced(prompt, toks)  # [B, n, V]
+    err = normalized_max_err(logits, ref)
+    print(f"B={B} S={S}: normalised max err {err.max().item():.4g}, mean {err.mean().item():.4g}")
+    assert err.max().item() <= TOL
+    ref_pick = ref.argmax(-1)
+    gap = top2_gap(ref)
+    mism = (ref_pick != toks)
+    near = gap < TOL * ref.abs().amax(-1)
+    assert bool((~mism | near).all()), f"non-near-tie divergence: {mism.nonzero().tolist()}"
+
+
+def test_generate_matches_eager_steps(engine):
+    prompt = prompts(2, 33, 5)
+    toks, _ = run_state(engine, prompt, 12)
+    out = list(engine.generate(prompt.tolist(), 12))
+    assert len(out) == 12 and all(len(s) == 2 for s in out)
+    assert torch.tensor(out).T.tolist() == toks.tolist()
+    # a second call of the same shape reuses the graph and resets all state
+    out2 = list(engine.generate(prompt.tolist(), 12))
+    assert out2 == out
+
+
+def test_generate_contract(engine):
+    assert list(engine.generate([[1, 2, 3]], 0)) == []
+    assert list(engine.generate([[1, 2, 3]], -4)) == []
+    steps = list(engine.generate([[5, 6, 7, 8]], 3))
+    assert len(steps) == 3 and all(isinstance(t, int) for s in steps for t in s)
+    one = list(engine.generate([[9] * 70], 1))
+    assert len(one) == 1 and len(one[0]) == 1
+
+
+def motif_prompts(B, S, seed, vocab=151936, motif=64, noise=0.1):
+    """a seeded 64-token motif tiled to S, with a
+    fraction of positions replaced by uniform random tokens."""
+    g = torch.Generator().manual_seed(seed)
+    base = torch.randint(0, vocab, (motif,), generator=g)
+    rows = []
+    for b in range(B):
+        r = base.repeat((S + motif - 1) // motif)[:S].clone()
+        m = torch.rand(S, generator=g) < noise
+        r[m] = torch.randint(0, vocab, (int(m.sum()),), generator=g)
+        rows.append(r)
+    return torch.stack(rows)
+
+
+def test_speculative_equals_plain_greedy(ckpt, engine):
+    from engine import Engine
+    spec = Engine.from_tensors(engine.model.cfg.raw, load_tensors(ckpt[0]), speculate=True)
+    for B, S, n, seed in ((4, 200, 40, 7), (2, 64, 25, 8), (1, 30, 17, 9)):
+        prompt = motif_prompts(B, S, seed)
+        plain = list(engine.generate(prompt.tolist(), n))
+        fast = list(spec.generate(prompt.tolist(), n))
+        assert fast == plain, (B, S, n)
+        stats = spec.stats["spec"]
+        print(f"spec B={B} S={S} n={n}: {stats}")
+        assert stats["iterations"] <= n - 1

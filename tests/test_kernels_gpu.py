@@ -1,0 +1,383 @@
+"""Every kernel of libqdec.so against the oracle, on the GPU, through the C ABI.
+
+Tolerances: bit-exact for layout, gather, cache writes, argmax and the
+drafter / acceptance; for the floating-point products the reference's own
+agreement rule (engine/engine.py:349-358 ``_agree``): max |err| <= 2% of the
+reference's max |value| and, where only the fp32 summation order differs, at
+least 98% of the bf16 outputs bit-identical.  Row- and t_rows-invariance is
+checked bit for bit: it is what makes speculative decoding lossless.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle.qwen3_oracle import (argmax_lowest, attention, bf16, head_norm_rope, linear, rms_norm,
+                                 rope_tables, silu_mul)
+from oracle.spec_oracle import accept as accept_ref
+from oracle.spec_oracle import ngram_draft as draft_ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+H, I, V, NQ, NKV, D = 2560, 9728, 151936, 32, 8, 128
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    from qdec import capi
+    return capi.lib()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def rnd(*shape, scale=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def agree(fast, ref, min_exact=0.98, tol=0.02):
+    fast, ref = fast.float().cpu(), ref.float().cpu()
+    assert torch.isfinite(fast).all()
+    exact = (fast == ref).float().mean().item()
+    err = (fast - ref).abs().max().item()
+    scale = ref.abs().max().item()
+    assert err <= tol * scale + 1e-3, f"max err {err} vs scale {scale}"
+    assert exact >= min_exact, f"exact fraction {exact}"
+    return exact, err
+
+
+def pack(lib, w):
+    n, k = w.shape
+    dst = torch.empty(n * k, dtype=torch.bfloat16, device=DEV)
+    lib.pack_tiles(w.data_ptr(), dst.data_ptr(), n, k, stream())
+    return dst
+
+
+class Gemm:
+    """Call qdec_gemm for one role with device tensors."""
+
+    def __init__(self, lib, flags, n, k, ksplit=1, waves=4, tiles=1):
+        from qdec import capi
+        self.lib, self.capi = lib, capi
+        self.flags, self.n, self.k = flags, n, k
+        self.ksplit, self.waves, self.tiles = ksplit, waves, tiles
+        self.partial = torch.zeros(4 << 20, dtype=torch.float32, device=DEV)
+        self.counters = torch.zeros(16384, dtype=torch.int32, device=DEV)
+
+    def __call__(self, x, w_tiled, out=None, res=None, norm_w=None, ids=None, lens=None):
+        a = self.capi.GemmArgs()
+        a.x, a.w = x.data_ptr(), w_tiled.data_ptr()
+        a.out = out.data_ptr() if out is not None else None
+        a.res = res.data_ptr() if res is not None else None
+        a.norm_w = norm_w.data_ptr() if norm_w is not None else None
+        a.partial, a.counters = self.partial.data_ptr(), self.counters.data_ptr()
+        a.ids_out = ids.data_ptr() if ids is not None else None
+        a.lens_inc = lens.data_ptr() if lens is not None else None
+        a.eps, a.rows, a.n, a.k = 1e-6, x.shape[0], self.n, self.k
+        a.flags, a.ksplit, a.waves, a.tiles_per_wg = self.flags, self.ksplit, self.waves, self.tiles
+        pb, _ = self.lib.gemm_workspace(a)
+        assert pb <= self.partial.numel() * 4
+        assert x.shape[1] == self.k and x.is_contiguous() and w_tiled.numel() == self.k * self.n * (
+            2 if self.flags & self.capi.GLU else 1)
+        self.lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        assert int(self.counters.abs().sum()) == 0, "arrival counters not reset"
+
+
+# ----------------------------------------------------------------- layout
+
+def test_pack_tiles_layout(lib):
+    n, k = 48, 96
+    w = torch.arange(n * k, dtype=torch.int32).view(n, k)
+    src = w.to(torch.float32).to(torch.bfloat16)  # exact for < 256? use bits instead
+    src = w.to(torch.int16).view(torch.bfloat16).contiguous().to(DEV)
+    out = pack(lib, src).view(torch.int16).cpu().to(torch.int32)
+    idx = torch.tensor([lib.tiled_offset(r, c, k) for r in range(n) for c in range(k)])
+    assert torch.equal(out[idx], w.flatten().to(torch.int16).to(torch.int32))
+
+
+def test_embed_gather_exact(lib):
+    from qdec import capi
+    vocab, hid = 512, 256
+    E = rnd(vocab, hid, seed=1)
+    Et = pack(lib, E.to(DEV))
+    ids = torch.tensor([0, 511, 7, 7, 300], dtype=torch.int64, device=DEV)
+    h = torch.zeros(5, hid, dtype=torch.bfloat16, device=DEV)
+    e = capi.EmbedArgs(ids=ids.data_ptr(), emb=Et.data_ptr(), h=h.data_ptr(), rows=5, hidden=hid, vocab=vocab)
+    lib.embed(e, stream())
+    torch.cuda.synchronize()
+    assert torch.equal(h.cpu(), E[ids.cpu()])
+
+
+# ------------------------------------------------------------------- GEMM
+
+@pytest.mark.parametrize("rows", [1, 4, 17, 36, 64])
+@pytest.mark.parametrize("role", ["qkv", "o", "gate_up", "down"])
+def test_gemm_roles_vs_oracle(lib, role, rows):
+    from qdec import capi
+    from qdec.runtime import role_plan
+    n, k, flags = {"qkv": (6144, H, capi.NORM_IN), "o": (H, 4096, capi.RES_OUT),
+                   "gate_up": (I, H, capi.NORM_IN | capi.GLU), "down": (H, I, capi.RES_OUT)}[role]
+    ks, waves, _ = role_plan(n, k, role)
+    seed = hash((role, rows)) % 1000
+    x = rnd(rows, k, scale=3.0, seed=seed)
+    wn = 2 * n if flags & capi.GLU else n
+    W = rnd(wn, k, scale=0.02, seed=seed + 1)
+    nw = bf16(1 + 0.2 * torch.randn(k, generator=torch.Generator().manual_seed(seed + 2))).to(torch.bfloat16)
+    g = Gemm(lib, flags, n, k, ksplit=ks, waves=waves)
+    xd, Wt = x.to(DEV), pack(lib, W.to(DEV))
+    if flags & capi.NORM_IN:
+        xin = rms_norm(x.float(), nw.float(), 1e-6)
+    else:
+        xin = x.float()
+    if flags & capi.GLU:
+        out = torch.zeros(rows, n, dtype=torch.bfloat16, device=DEV)
+        g(xd, Wt, out=out, norm_w=nw.to(DEV))
+        ref = silu_mul(linear(xin, W[:n].float()), linear(xin, W[n:].float()))
+    elif flags & capi.RES_OUT:
+        res0 = rnd(rows, n, scale=2.0, seed=seed + 3)
+        res = res0.to(DEV).clone()
+        g(xd, Wt, res=res)
+        out = res
+        ref = bf16(res0.float() + linear(xin, W.float()))
+    else:
+        out = torch.zeros(rows, n, dtype=torch.bfloat16, device=DEV)
+        g(xd, Wt, out=out, norm_w=nw.to(DEV))
+        ref = linear(xin, W.float())
+    agree(out, ref)
+
+
+@pytest.mark.parametrize("role", ["qkv", "o", "gate_up", "down"])
+def test_gemm_row_invariance_bitexact(lib, role):
+    """A row's output bits do not depend on how many rows share the call or
+    where the row sits (MFMA column, M tile, LDS pass)."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    n, k, flags = {"qkv": (6144, H, capi.NORM_IN), "o": (H, 4096, capi.RES_OUT),
+                   "gate_up": (I, H, capi.NORM_IN | capi.GLU), "down": (H, I, capi.RES_OUT)}[role]
+    ks, waves, _ = role_plan(n, k, role)
+    big = 64
+    x = rnd(big, k, scale=3.0, seed=11).to(DEV)
+    W = pack(lib, rnd(2 * n if flags & capi.GLU else n, k, scale=0.02, seed=12).to(DEV))
+    nw = rnd(k, scale=0.2, seed=13).to(DEV)
+    res0 = rnd(big, n, scale=2.0, seed=14).to(DEV)
+    g = Gemm(lib, flags, n, k, ksplit=ks, waves=waves)
+
+    def run(rows_idx):
+        xs = x[rows_idx].contiguous()
+        if flags & capi.RES_OUT:
+            r = res0[rows_idx].contiguous().clone()
+            g(xs, W, res=r)
+            return r
+        o = torch.zeros(len(rows_idx), n, dtype=torch.bfloat16, device=DEV)
+        g(xs, W, out=o, norm_w=nw)
+        return o
+
+    full = run(list(range(big)))
+    for rows_idx in ([5], [0, 1, 2, 3], list(range(36)), [63, 9, 40], list(range(17, 34))):
+        part = run(rows_idx)
+        assert torch.equal(part.view(torch.int16), full[rows_idx].view(torch.int16)), rows_idx
+
+
+def test_lmhead_argmax_and_ties(lib):
+    """Greedy pick over 151936 columns: the lowest index of the max bf16
+    logit, bit-exact; logits within tolerance of the oracle; lens advance."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    _, waves, tiles = role_plan(V, H, "lm")
+    rows = 5
+    x = rnd(rows, H, scale=2.0, seed=21)
+    E = rnd(V, H, scale=0.02, seed=22)
+    # plant exact ties: duplicate rows -> identical logits at two indices.
+    E[100000] = E[77]
+    E[150000] = E[3]
+    nw = bf16(1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(23))).to(torch.bfloat16)
+    # make rows 0/1 pick the planted duplicates: x aligned with E[77] / E[3]
+    x[0] = (E[77].float() * 200).to(torch.bfloat16)
+    x[1] = (E[3].float() * 200).to(torch.bfloat16)
+    Et = pack(lib, E.to(DEV))
+    g = Gemm(lib, capi.NORM_IN | capi.ARGMAX, V, H, waves=waves, tiles=tiles)
+    logits = torch.zeros(rows, V, dtype=torch.bfloat16, device=DEV)
+    ids = torch.full((rows,), -1, dtype=torch.int64, device=DEV)
+    lens = torch.arange(rows, dtype=torch.int32, device=DEV)
+    g(x.to(DEV), Et, out=logits, norm_w=nw.to(DEV), ids=ids, lens=lens)
+    lg = logits.float().cpu()
+    assert ids.cpu().tolist() == argmax_lowest(lg).tolist()
+    assert ids.cpu().tolist()[:2] == [77, 3]
+    assert lens.cpu().tolist() == [1, 2, 3, 4, 5]
+    ref = linear(rms_norm(x.float(), nw.float(), 1e-6), E.float())
+    agree(lg, ref)
+
+
+# -------------------------------------------------------------- attention
+
+def v_layout(v):
+    """[..., cap, D] -> the channel-major V cache layout [..., cap/8, D, 8]."""
+    *lead, cap, d = v.shape
+    return v.reshape(*lead, cap // 8, 8, d).transpose(-1, -2).contiguous()
+
+
+def attn_case(lib, B, T, lens, cap, chunk, seed):
+    from qdec import capi
+    g = torch.Generator().manual_seed(seed)
+    W = (NQ + 2 * NKV) * D
+    qkv = (torch.randn(B * T, W, generator=g) * 2).to(torch.bfloat16)
+    qn = bf16(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kn = bf16(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    kc = (torch.randn(B, NKV, cap, D, generator=g)).to(torch.bfloat16)
+    vc = (torch.randn(B, NKV, cap, D, generator=g)).to(torch.bfloat16)
+    cos, sin = rope_tables(cap, D, 5e6, "bf16")
+    lens_t = torch.tensor(lens, dtype=torch.int32)
+    a = capi.AttnArgs()
+    dq = qkv.to(DEV)
+    dqn, dkn = qn.to(DEV), kn.to(DEV)
+    dcos, dsin = cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
+    dl = lens_t.to(DEV)
+    dk, dv = kc.to(DEV).contiguous(), v_layout(vc).to(DEV)
+    out = torch.zeros(B * T, NQ * D, dtype=torch.bfloat16, device=DEV)
+    a.qkv, a.q_norm_w, a.k_norm_w, a.cos_tab, a.sin_tab, a.lens = (dq.data_ptr(), dqn.data_ptr(), dkn.data_ptr(),
+                                                                 dcos.data_ptr(), dsin.data_ptr(), dl.data_ptr())
+    a.k_cache, a.v_cache, a.out = dk.data_ptr(), dv.data_ptr(), out.data_ptr()
+    a.eps, a.sm_scale = 1e-6, D ** -0.5
+    a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = B, T, NQ, NKV, D, cap, chunk
+    pb, cb = lib.attn_workspace(a)
+    part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
+    cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
+    a.partial, a.counters = part.data_ptr(), cnt.data_ptr()
+    assert max(lens) + T <= cap
+    lib.attn(a, stream())
+    torch.cuda.synchronize()
+    assert int(cnt.abs().sum()) == 0
+    return dict(qkv=qkv, qn=qn, kn=kn, kc=kc, vc=vc, cos=cos, sin=sin, lens=lens, out=out.cpu(),
+                k_after=dk.cpu(), v_after=dv.cpu())
+
+
+def attn_oracle(c, B, T):
+    qkv = c["qkv"].float().view(B, T, NQ + 2 * NKV, D)
+    kc, vc = c["kc"].float().clone(), c["vc"].float().clone()
+    outs = torch.zeros(B, T, NQ, D)
+    for b in range(B):
+        L = c["lens"][b]
+        pos = torch.arange(L, L + T)
+        cs, sn = c["cos"][pos][:, None, :], c["sin"][pos][:, None, :]
+        q = head_norm_rope(qkv[b, :, :NQ], c["qn"].float(), cs, sn, 1e-6)
+        k = head_norm_rope(qkv[b, :, NQ:NQ + NKV], c["kn"].float(), cs, sn, 1e-6)
+        v = qkv[b, :, NQ + NKV:]
+        kc[b, :, pos] = k.transpose(0, 1)
+        vc[b, :, pos] = v.transpose(0, 1)
+        cap = kc.shape[2]
+        for h in range(NQ):
+            kvh = h // (NQ // NKV)
+            vis = torch.arange(cap)[None, :] <= pos[:, None]
+            outs[b, :, h] = attention(q[:, h], kc[b, kvh], vc[b, kvh], vis, D ** -0.5)
+    return outs.view(B * T, NQ * D), kc, vc
+
+
+@pytest.mark.parametrize("B,T,lens,cap,chunk", [
+    (1, 1, [0], 64, 64),
+    (1, 1, [31], 64, 64),
+    (1, 1, [100], 256, 64),
+    (2, 1, [63, 200], 256, 64),
+    (3, 1, [5, 64, 129], 192, 128),
+    (1, 4, [60], 128, 64),
+    (2, 9, [0, 170], 256, 64),
+    (4, 9, [1000, 1017, 31, 64], 1056, 96),
+])
+def test_attention_vs_oracle(lib, B, T, lens, cap, chunk):
+    c = attn_case(lib, B, T, lens, cap, chunk, seed=B * 100 + T * 10 + lens[0])
+    ref, kc, vc = attn_oracle(c, B, T)
+    agree(c["out"], ref, min_exact=0.0, tol=0.02)
+    # new K (normed, rotated) and raw V bit-exact in the cache; the rest untouched
+    assert torch.equal(c["k_after"].float(), kc)
+    assert torch.equal(c["v_after"].float(), v_layout(vc.to(torch.bfloat16)).float())
+
+
+@pytest.mark.parametrize("cap,chunk,L", [(256, 64, 100), (256, 64, 63), (1056, 96, 1000), (512, 128, 0)])
+def test_attention_t_invariance_bitexact(lib, cap, chunk, L):
+    """Verify row t (t_rows = 9) at position L + t equals the plain T = 1 step
+    at that position, bit for bit, given the same cache contents."""
+    B, T = 2, 9
+    c9 = attn_case(lib, B, T, [L, L + 3], cap, chunk, seed=77)
+    for t in range(T):
+        # plain step at position L + t: cache holds the verify pass's K/V for
+        # slots < L + t (the first pass already wrote them) and the same qkv row.
+        pos_lens = [L + t, L + 3 + t]
+        one = attn_case_from(lib, c9, B, T, t, pos_lens, cap, chunk)
+        for b in range(B):
+            assert torch.equal(one[b].view(torch.int16), c9["out"][b * T + t].view(torch.int16)), (t, b)
+
+
+def attn_case_from(lib, c9, B, T, t, lens, cap, chunk):
+    """Run T = 1 on row t of every sequence of case c9, with the cache as the
+    T = 9 call left it."""
+    from qdec import capi
+    W = (NQ + 2 * NKV) * D
+    qkv = c9["qkv"].view(B, T, W)[:, t].contiguous()
+    dq, dqn, dkn = qkv.to(DEV), c9["qn"].to(DEV), c9["kn"].to(DEV)
+    dcos, dsin = c9["cos"].to(torch.bfloat16).to(DEV), c9["sin"].to(torch.bfloat16).to(DEV)
+    dl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    dk, dv = c9["k_after"].to(DEV).clone(), c9["v_after"].to(DEV).clone()
+    out = torch.zeros(B, NQ * D, dtype=torch.bfloat16, device=DEV)
+    a = capi.AttnArgs()
+    a.qkv, a.q_norm_w, a.k_norm_w, a.cos_tab, a.sin_tab, a.lens = (dq.data_ptr(), dqn.data_ptr(), dkn.data_ptr(),
+                                                                 dcos.data_ptr(), dsin.data_ptr(), dl.data_ptr())
+    a.k_cache, a.v_cache, a.out = dk.data_ptr(), dv.data_ptr(), out.data_ptr()
+    a.eps, a.sm_scale = 1e-6, D ** -0.5
+    a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = B, 1, NQ, NKV, D, cap, chunk
+    pb, cb = lib.attn_workspace(a)
+    part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
+    cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
+    a.partial, a.counters = part.data_ptr(), cnt.data_ptr()
+    lib.attn(a, stream())
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+# ---------------------------------------------------------- speculation
+
+def test_draft_and_accept_vs_oracle(lib):
+    from qdec import capi
+    import random
+    rng = random.Random(3)
+    B, cap, K = 5, 96, 6
+    T = K + 1
+    for trial in range(20):
+        hist = [[rng.randint(0, 4) for _ in range(cap)] for _ in range(B)]
+        lens = [rng.randint(0, cap - 2 * T - 1) for _ in range(B)]
+        dh = torch.tensor(hist, dtype=torch.int64, device=DEV)
+        dl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+        ids = torch.zeros(B * T, dtype=torch.int64, device=DEV)
+        dr = torch.zeros(B * K, dtype=torch.int64, device=DEV)
+        d = capi.DraftArgs(hist=dh.data_ptr(), lens=dl.data_ptr(), ids=ids.data_ptr(), draft=dr.data_ptr(),
+                           batch=B, cap=cap, primary=3, backoff=2, k=K)
+        lib.ngram_draft(d, stream())
+        torch.cuda.synchronize()
+        exp_ids, exp_dr = [], []
+        for b in range(B):
+            i, dd = draft_ref(hist[b], lens[b], 3, 2, K)
+            exp_ids += i
+            exp_dr += dd
+        assert ids.cpu().tolist() == exp_ids and dr.cpu().tolist() == exp_dr
+        # accept with model outputs that agree with the draft for a random prefix
+        out_tok = []
+        for b in range(B):
+            agree_n = rng.randint(0, K)
+            row = [exp_ids[b * T + 1 + t] if t < agree_n else rng.randint(5, 9) for t in range(K)]
+            out_tok += row + [rng.randint(0, 9)]
+        stop = rng.randint(0, cap)
+        dot = torch.tensor(out_tok, dtype=torch.int64, device=DEV)
+        nacc = torch.zeros(B, dtype=torch.int32, device=DEV)
+        a = capi.AcceptArgs(out_tok=dot.data_ptr(), draft=dr.data_ptr(), hist=dh.data_ptr(), lens=dl.data_ptr(),
+                            naccept=nacc.data_ptr(), batch=B, cap=cap, k=K, stop_len=stop)
+        lib.spec_accept(a, stream())
+        torch.cuda.synchronize()
+        for b in range(B):
+            h = list(hist[b])
+            na, nl = accept_ref(out_tok[b * T:(b + 1) * T], exp_dr[b * K:(b + 1) * K], h, lens[b], K, stop)
+            assert nacc[b].item() == na and dl[b].item() == nl and dh[b].cpu().tolist() == h
