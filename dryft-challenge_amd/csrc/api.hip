@@ -90,6 +90,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->lds_red_off = (int)head;
   p->lds_x_off = (int)(head + red_bytes);
   p->lds_bytes = head + red_bytes + (size_t)a->rows * p->xstride * 2;
+  p->xfast = gemm_fast_path(*p, f) ? 1 : 0;
   if (p->lds_bytes > (size_t)kGemmLdsX)
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: rows %d x waves %d needs %zu B of LDS", a->rows, a->waves,
                      p->lds_bytes);
@@ -105,6 +106,7 @@ static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) 
   if (a->t_rows < 1 || a->t_rows > 16) return set_error(QDEC_EINVAL, "qdec_attn: t_rows %d not in [1, 16]", a->t_rows);
   if (a->cap < 32 || a->cap % 32) return set_error(QDEC_EINVAL, "qdec_attn: cap %d not a positive multiple of 32", a->cap);
   if (a->chunk < 32 || a->chunk % 32) return set_error(QDEC_EINVAL, "qdec_attn: chunk %d not a positive multiple of 32", a->chunk);
+  if (a->waves < 1 || a->waves > 4) return set_error(QDEC_EINVAL, "qdec_attn: waves %d not in [1, 4]", a->waves);
   const int nchunks = (a->cap + a->chunk - 1) / a->chunk;
   if (!need_scratch) goto fill;
   if (!a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->lens || !a->k_cache ||
@@ -123,7 +125,7 @@ fill:
   p->eps = a->eps;
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
   p->batch = a->batch; p->t_rows = a->t_rows; p->nq = a->nq; p->nkv = a->nkv;
-  p->cap = a->cap; p->chunk = a->chunk; p->nchunks = nchunks;
+  p->cap = a->cap; p->chunk = a->chunk; p->nchunks = nchunks; p->waves = a->waves;
   return QDEC_OK;
 }
 

@@ -9,11 +9,20 @@
 // operand.  The product is computed transposed (y^T = W . x'^T), so a lane
 // ends up holding 4 consecutive output columns of one row.
 //
+// Latency: the first pass's weight loads are issued before anything else;
+// for small row counts the activations are then loaded once into registers
+// (statistics and LDS staging come from those registers), so the norm
+// prologue overlaps the weight stream instead of preceding it.  With several
+// tiles per workgroup the next tile's weights are requested before the
+// current tile's epilogue.
+//
 // Summation order of an output element: MFMA chain over the wave's k steps in
 // increasing order, then waves 0..W-1 added in order, then k splits 0..S-1
-// added in order by the workgroup that arrives last.  None of it depends on
-// the number of rows, which is what lets a verify pass over B*T rows
-// reproduce the plain B-row step bit for bit.
+// added in order by the workgroup that arrives last.  The RMSNorm statistic
+// of a row is summed by thread t over the row's 16-byte vectors t, t+T, ...
+// and then across lanes and waves in a fixed tree, whatever the path.  None
+// of it depends on the number of rows, which is what lets a verify pass over
+// B*T rows reproduce the plain B-row step bit for bit.
 //
 // Reference behaviour replaced: engine/kernels/fused.py:33-235 (_gemv_kernel,
 // _gemv_vec_kernel, _gemv_splitk_kernel + reduce) and the lm_head + argmax of
@@ -25,7 +34,34 @@ namespace qdec {
 
 namespace {
 
-constexpr int kMaxRows = 64;
+// Fast activation path: up to kFastRows rows, 2 vectors per thread per row.
+constexpr int kFastRows = 4;
+constexpr int kFastVec = 2;
+
+// Sum one fp32 value per thread of the workgroup for up to 8 rows in a fixed
+// order (lane tree, then waves in order); thread m < nrows gets row m's total.
+__device__ __forceinline__ void block_row_sums(float (&ss)[8], float *s_red, int nrows,
+                                               float *dst_rstd, int m0, int k, float eps) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float v = ss[j];
+    v += shfl_xor(v, 32);
+    v += shfl_xor(v, 16);
+    v += shfl_xor(v, 8);
+    v += shfl_xor(v, 4);
+    v += shfl_xor(v, 2);
+    v += shfl_xor(v, 1);
+    if (lane == 0) s_red[wave * 8 + j] = v;
+  }
+  __syncthreads();
+  if (tid < 8 && tid < nrows) {
+    float t = 0.f;
+    for (int w2 = 0; w2 < (int)(blockDim.x >> 6); ++w2) t += s_red[w2 * 8 + tid];
+    dst_rstd[m0 + tid] = 1.0f / sqrtf(t / (float)k + eps);
+  }
+  __syncthreads();
+}
 
 template <int MT, uint32_t FLAGS>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
@@ -39,18 +75,18 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   float *s_rstd = reinterpret_cast<float *>(smem);                     // [64]
   uint32_t *s_flag = reinterpret_cast<uint32_t *>(smem + 256);         // [4]
-  float *s_red = reinterpret_cast<float *>(smem + 272);                // [8*? floats]
+  float *s_red = reinterpret_cast<float *>(smem + 272);                // [64 floats]
   uint16_t *s_x = reinterpret_cast<uint16_t *>(smem + p.lds_x_off);    // [rows][xstride]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int nthr = blockDim.x;
+  const int nw = nthr >> 6;
   const int rows = p.rows;
   const int col = lane & 15;   // row of x inside an M tile
   const int grp = lane >> 4;   // k group / output column group
 
-  const int ngroups = gridDim.x / p.ksplit;
   const int tg = blockIdx.x / p.ksplit;        // tile group
   const int split = blockIdx.x - tg * p.ksplit;
   const int ks_wg = split * (p.KS / p.ksplit); // first k step of this workgroup
@@ -58,10 +94,81 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   const int xstride = p.xstride;
   const uint4 *__restrict__ W = reinterpret_cast<const uint4 *>(p.w);
   const uint16_t *__restrict__ X = reinterpret_cast<const uint16_t *>(p.x);
+  const size_t up_off = (size_t)p.up_tiles * p.KS * 64;
 
-  // ---- RMSNorm statistics of the workgroup's input rows (whole row, in a
-  // fixed thread/lane order so every workgroup gets the same rstd bits).
-  if constexpr (NORM) {
+  // Straight-line weight loads of one pass; indices past the pass are clamped
+  // to its last block (a redundant, cache-served load) instead of branched
+  // around, so all of them stay in flight together.
+  uint4 wb[NACC][KPMAX];
+  auto issue_w = [&](int tile, int kbeg, int kcnt) {
+    const size_t blk0 = ((size_t)tile * p.KS + ks_wave + kbeg) * 64 + lane;
+#pragma unroll
+    for (int i = 0; i < KPMAX; ++i) {
+      const size_t off = blk0 + (size_t)min(i, kcnt - 1) * 64;
+      wb[0][i] = W[off];
+      if constexpr (GLU) wb[NACC - 1][i] = W[off + up_off];
+    }
+  };
+
+  const int tile0 = tg * p.tiles_per_wg;
+  issue_w(tile0, 0, min(p.kp, p.ksw));
+
+  bool staged = false;
+  if (p.xfast) {
+    // Activations into registers: row m, vectors vr = tid + j*nthr of the
+    // workgroup's k range (per_row of them).
+    const int per_row = p.ksw * nw * 4;
+    uint4 xr[kFastRows][kFastVec];
+#pragma unroll
+    for (int m = 0; m < kFastRows; ++m)
+#pragma unroll
+      for (int j = 0; j < kFastVec; ++j) {
+        const int vr = tid + j * nthr;
+        const bool ok = m < rows && vr < per_row;
+        const int mm = ok ? m : 0, vv = ok ? vr : 0;
+        const uint4 v = *reinterpret_cast<const uint4 *>(X + (size_t)mm * p.k + ks_wg * 32 + 8 * vv);
+        xr[m][j] = ok ? v : zero4();
+      }
+    if constexpr (NORM) {
+      float ss[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss[j] = 0.f;
+#pragma unroll
+      for (int m = 0; m < kFastRows; ++m)
+#pragma unroll
+        for (int j = 0; j < kFastVec; ++j) {
+          float f[8];
+          unpack8(xr[m][j], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss[m] += f[e] * f[e];
+        }
+      block_row_sums(ss, s_red, rows, s_rstd, 0, p.k, p.eps);
+    }
+#pragma unroll
+    for (int m = 0; m < kFastRows; ++m)
+#pragma unroll
+      for (int j = 0; j < kFastVec; ++j) {
+        const int vr = tid + j * nthr;
+        if (m < rows && vr < per_row) {
+          uint4 xv = xr[m][j];
+          if constexpr (NORM) {
+            const uint4 nv = *reinterpret_cast<const uint4 *>(
+                reinterpret_cast<const uint16_t *>(p.norm_w) + ks_wg * 32 + 8 * vr);
+            float f[8], g[8];
+            unpack8(xv, f);
+            unpack8(nv, g);
+            const float rs = s_rstd[m];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = g[e] * rbf(f[e] * rs);
+            xv = pack8(f);
+          }
+          *reinterpret_cast<uint4 *>(s_x + (size_t)m * xstride + 8 * vr) = xv;
+        }
+      }
+    __syncthreads();
+    staged = true;
+  } else if constexpr (NORM) {
+    // Whole-row statistics, same per-thread vector assignment and order.
     const int nvec = p.k >> 3;
     for (int m0 = 0; m0 < rows; m0 += 8) {
       float ss[8];
@@ -71,33 +178,16 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       for (int j = 0; j < 8; ++j) {
         const int m = m0 + j;
         if (m < rows) {
-          const uint4 *xr = reinterpret_cast<const uint4 *>(X + (size_t)m * p.k);
+          const uint4 *xv = reinterpret_cast<const uint4 *>(X + (size_t)m * p.k);
           for (int v = tid; v < nvec; v += nthr) {
             float f[8];
-            unpack8(xr[v], f);
+            unpack8(xv[v], f);
 #pragma unroll
             for (int e = 0; e < 8; ++e) ss[j] += f[e] * f[e];
           }
         }
       }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float v = ss[j];
-        v += shfl_xor(v, 32);
-        v += shfl_xor(v, 16);
-        v += shfl_xor(v, 8);
-        v += shfl_xor(v, 4);
-        v += shfl_xor(v, 2);
-        v += shfl_xor(v, 1);
-        if (lane == 0) s_red[wave * 8 + j] = v;
-      }
-      __syncthreads();
-      if (tid < 8 && m0 + tid < rows) {
-        float t = 0.f;
-        for (int w2 = 0; w2 < (nthr >> 6); ++w2) t += s_red[w2 * 8 + tid];
-        s_rstd[m0 + tid] = 1.0f / sqrtf(t / (float)p.k + p.eps);
-      }
-      __syncthreads();
+      block_row_sums(ss, s_red, rows - m0, s_rstd, m0, p.k, p.eps);
     }
   }
 
@@ -110,9 +200,9 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
     best_i[mt] = 0x7fffffff;
   }
 
-  bool staged = false;
+  bool have_w = true;  // wb holds the next pass's weights already
   for (int tt = 0; tt < p.tiles_per_wg; ++tt) {
-    const int tile = tg * p.tiles_per_wg + tt;
+    const int tile = tile0 + tt;
     f32x4_t acc[NACC][MT];
 #pragma unroll
     for (int a = 0; a < NACC; ++a)
@@ -120,26 +210,13 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       for (int mt = 0; mt < MT; ++mt) acc[a][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     for (int pass = 0; pass < p.npass; ++pass) {
-      const int kbeg = pass * p.kp;                       // wave-local first step
-      const int kcnt = min(p.kp, p.ksw - kbeg);           // steps in this pass
-      // Issue this pass's weight loads first so they overlap the staging.
-      uint4 wb[NACC][KPMAX];
-      {
-        const size_t blk0 = ((size_t)tile * p.KS + ks_wave + kbeg) * 64 + lane;
-#pragma unroll
-        for (int i = 0; i < KPMAX; ++i) {
-          if (i < kcnt) {
-            wb[0][i] = W[blk0 + (size_t)i * 64];
-            if constexpr (GLU)
-              wb[NACC - 1][i] = W[blk0 + (size_t)p.up_tiles * p.KS * 64 + (size_t)i * 64];
-          }
-        }
-      }
-      // Stage x rows for every wave's k steps of this pass.
+      const int kbeg = pass * p.kp;
+      const int kcnt = min(p.kp, p.ksw - kbeg);
+      if (!have_w) issue_w(tile, kbeg, kcnt);
+      have_w = false;
       if (!staged || p.npass > 1) {
         if (pass > 0 || tt > 0) __syncthreads();  // previous readers are done
-        const int nw = nthr >> 6;
-        const int per_row = nw * kcnt * 4;  // 16-byte vectors per row
+        const int per_row = nw * kcnt * 4;  // 16-byte vectors per row in this pass
         const int total = rows * per_row;
         for (int v = tid; v < total; v += nthr) {
           const int m = v / per_row;
@@ -183,9 +260,13 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         }
       }
     }
+    // Request the next tile's weights before this tile's epilogue.
+    if (p.npass == 1 && tt + 1 < p.tiles_per_wg) {
+      issue_w(tile + 1, 0, min(p.kp, p.ksw));
+      have_w = true;
+    }
 
     // ---- merge the waves of the workgroup in wave order.
-    const int nw = nthr >> 6;
     if (nw > 1) {
       __syncthreads();
       float4 *red = reinterpret_cast<float4 *>(smem + p.lds_red_off);
@@ -308,7 +389,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 
   if constexpr (ARG) {
     // Reduce the 4 column groups of each row, lowest index on equal values.
-    float *pv = p.partial;                                              // [G][rows]
+    float *pv = p.partial;                                                    // [G][rows]
     int *pi = reinterpret_cast<int *>(p.partial + (size_t)gridDim.x * rows);  // [G][rows]
     if (wave == 0) {
 #pragma unroll
@@ -330,7 +411,6 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       }
     }
     if (!arrive_last(p.counters, gridDim.x, s_flag)) return;
-    (void)ngroups;
     float *sv = s_red;                                      // [waves]
     int *si = reinterpret_cast<int *>(s_red + 8);           // [waves]
     for (int m = 0; m < rows; ++m) {
@@ -359,7 +439,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       }
       __syncthreads();
       if (tid == 0) {
-        for (int w2 = 1; w2 < (nthr >> 6); ++w2)
+        for (int w2 = 1; w2 < nw; ++w2)
           if (sv[w2] > bv || (sv[w2] == bv && si[w2] < bi)) {
             bv = sv[w2];
             bi = si[w2];
@@ -402,6 +482,12 @@ hipError_t launch_mt(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block,
 bool gemm_flags_supported(uint32_t flags) {
   return flags == 0u || flags == QDEC_NORM_IN || flags == (QDEC_NORM_IN | QDEC_GLU) ||
          flags == QDEC_RES_OUT || flags == (QDEC_NORM_IN | QDEC_ARGMAX);
+}
+
+bool gemm_fast_path(const GemmParams &p, uint32_t flags) {
+  const int per_row = p.ksw * p.waves * 4;
+  return p.npass == 1 && p.rows <= kFastRows && per_row <= kFastVec * 64 * p.waves &&
+         (!(flags & QDEC_NORM_IN) || p.ksplit == 1);
 }
 
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {

@@ -68,6 +68,14 @@ __device__ __forceinline__ float load_coherent(const float *p) {
 __device__ __forceinline__ void store_coherent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16-byte versions: volatile vector accesses compile to cache-bypassing
+// (system-scope) loads/stores, so several can be in flight at once.
+__device__ __forceinline__ f32x4_t load_coherent4(const float *p) {
+  return *reinterpret_cast<volatile const f32x4_t *>(p);
+}
+__device__ __forceinline__ void store_coherent4(float *p, f32x4_t v) {
+  *reinterpret_cast<volatile f32x4_t *>(p) = v;
+}
 __device__ __forceinline__ int load_coherent_i(const int *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -78,20 +86,32 @@ __device__ __forceinline__ void store_coherent_i(int *p, int v) {
 // Arrival at a per-tile counter after this workgroup's partial results were
 // stored (all threads must call it).  Returns true in every thread of the
 // workgroup that arrived last; that workgroup resets the counter to zero.
+//
+// Protocol (no cache-wide fences): every value handed between workgroups is
+// written with store_coherent and read with load_coherent, i.e. device-scope
+// accesses that are performed at the device's point of coherence and never
+// served from a stale cache line of another XCD.  Ordering is then only a
+// matter of completion: each thread waits for its own stores to complete
+// (s_waitcnt 0) before the workgroup barrier, and thread 0 bumps the counter
+// after the barrier, so the counter can only reach `expected` once every
+// partial of every arriving workgroup is visible; the last arriver reads the
+// partials after it has seen that value.  A full __threadfence() here would
+// write back and invalidate the whole L2 of the XCD for every workgroup.
 __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected,
                                             uint32_t *lds_flag) {
-  __threadfence();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t last = (old == expected - 1u) ? 1u : 0u;
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = (old == expected - 1u) ? 1u : 0u;
     if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *lds_flag = last;
   }
   __syncthreads();
-  bool last = *lds_flag != 0u;
-  if (last) __threadfence();
-  return last;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  return *lds_flag != 0u;
 }
 
 // Cross-lane helpers (wave64).

@@ -32,9 +32,11 @@ struct GemmParams {
   int up_tiles;  // GLU: tile offset of the up half
   int xstride;   // LDS row stride of staged activations (elements)
   int lds_red_off, lds_x_off;
+  int xfast;     // activations staged from registers (see gemm.hip)
   size_t lds_bytes;
 };
 bool gemm_flags_supported(uint32_t flags);
+bool gemm_fast_path(const GemmParams &p, uint32_t flags);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 
 struct AttnParams {
@@ -51,7 +53,7 @@ struct AttnParams {
   uint32_t *counters;
   float eps;
   float scale_log2;  // log2(e) / sqrt(head_dim)
-  int batch, t_rows, nq, nkv, cap, chunk, nchunks;
+  int batch, t_rows, nq, nkv, cap, chunk, nchunks, waves;
 };
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 

@@ -44,7 +44,8 @@ class AttnArgs(ctypes.Structure):
     _fields_ = [("qkv", P), ("q_norm_w", P), ("k_norm_w", P), ("cos_tab", P), ("sin_tab", P),
                 ("lens", P), ("k_cache", P), ("v_cache", P), ("out", P), ("partial", P),
                 ("counters", P), ("eps", F32), ("sm_scale", F32), ("batch", I32), ("t_rows", I32),
-                ("nq", I32), ("nkv", I32), ("head_dim", I32), ("cap", I32), ("chunk", I32)]
+                ("nq", I32), ("nkv", I32), ("head_dim", I32), ("cap", I32), ("chunk", I32),
+                ("waves", I32)]
 
 
 class DraftArgs(ctypes.Structure):

@@ -30,7 +30,7 @@ from . import capi
 
 GEMM_MAX_ROWS = 64
 ATTN_MAX_T = 16
-ATTN_TARGET_WGS = 2048
+ATTN_WAVES = 4
 # Loss-free speculation needs identical arithmetic in the plain and verify
 # steps, so attention chunking depends on (batch, capacity) only.
 
@@ -96,9 +96,11 @@ def role_plan(n, k, role):
     ntiles = n // 16
     waves = 4
     ksplit = 1
-    if role in ("o", "down"):
+    if role == "o":
+        # 160 tiles x 8 waves of 16 k steps measured faster than any k split.
+        waves = 8
+    elif role == "down":
         # Aim for >= 512 workgroups while keeping >= 8 k steps per wave.
-        ksplit = 1
         for cand in (2, 4, 8):
             if ks % (cand * waves) == 0 and ks // (cand * waves) >= 8 and ntiles * ksplit < 512:
                 ksplit = cand
@@ -114,11 +116,15 @@ def role_plan(n, k, role):
 
 
 def attn_chunk(batch, nkv, cap):
-    """Slots per attention workgroup: enough chunks to launch ~2048
-    workgroups, at least 64 slots each (absolute-slot chunking)."""
-    want = max(1, math.ceil(ATTN_TARGET_WGS / (batch * nkv)))
-    chunk = round_up(max(1, math.ceil(cap / want)), 32)
-    return max(64, min(chunk, round_up(cap, 32)))
+    """Slots per attention workgroup (a multiple of 32; absolute-slot
+    chunking).  Measured on MI355X with 4-wave workgroups: once batch x kv
+    heads fills half the CUs one chunk per sequence is fastest (no merge);
+    below that, 512-slot chunks (256 at batch 1) trade the cross-workgroup
+    merge against parallelism."""
+    cap = round_up(cap, 32)
+    if batch * nkv >= 128:
+        return cap
+    return min(cap, 512 if batch >= 4 else 256)
 
 
 class DeviceModel:
@@ -276,7 +282,7 @@ class DecodeState:
             a.partial, a.counters = self.attn_partial.data_ptr(), self.attn_counters.data_ptr()
         a.eps, a.sm_scale = c.eps, c.head_dim ** -0.5
         a.batch, a.t_rows, a.nq, a.nkv, a.head_dim = self.batch, t_rows, c.nq, c.nkv, c.head_dim
-        a.cap, a.chunk = self.cap, self.chunk
+        a.cap, a.chunk, a.waves = self.cap, self.chunk, ATTN_WAVES
         return a
 
     # ---------------------------------------------------------------- step

@@ -155,7 +155,8 @@ int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes,
  * Slots are processed in chunks of `chunk` slots keyed to absolute slot
  * numbers, one workgroup per (chunk, kv head, sequence); the last workgroup
  * of a (sequence, kv head) to finish merges the chunk partials in chunk
- * order.  A row's result therefore does not depend on t_rows.
+ * order.  A row's result therefore does not depend on t_rows (for a fixed
+ * chunk and waves).
  * Replaces fused.attention_fused (engine/kernels/fused.py:360-479),
  * ops.qkv_post + ops.DecodeAttention (engine/kernels/ops.py:84-431) and the
  * multi-row verify attention of notes/v10/spec.py:111-182. */
@@ -180,6 +181,8 @@ typedef struct {
   int32_t head_dim;     /* 128 */
   int32_t cap;          /* slots per sequence, multiple of 32 */
   int32_t chunk;        /* slots per workgroup, multiple of 32 */
+  int32_t waves;        /* wavefronts per workgroup (1..4); blocks of 32 slots
+                           are dealt to them round robin */
 } qdec_attn_args;
 int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream);
 int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,

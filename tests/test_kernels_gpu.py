@@ -246,6 +246,7 @@ def attn_case(lib, B, T, lens, cap, chunk, seed):
     a.k_cache, a.v_cache, a.out = dk.data_ptr(), dv.data_ptr(), out.data_ptr()
     a.eps, a.sm_scale = 1e-6, D ** -0.5
     a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = B, T, NQ, NKV, D, cap, chunk
+    a.waves = 4
     pb, cb = lib.attn_workspace(a)
     part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
     cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
@@ -330,6 +331,7 @@ def attn_case_from(lib, c9, B, T, t, lens, cap, chunk):
     a.k_cache, a.v_cache, a.out = dk.data_ptr(), dv.data_ptr(), out.data_ptr()
     a.eps, a.sm_scale = 1e-6, D ** -0.5
     a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = B, 1, NQ, NKV, D, cap, chunk
+    a.waves = 4
     pb, cb = lib.attn_workspace(a)
     part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
     cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
