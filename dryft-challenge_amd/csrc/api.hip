@@ -3,6 +3,7 @@
 // before any HIP call, so a bad call fails cleanly even without a GPU.
 #include <stdarg.h>
 #include <stdio.h>
+#include <string.h>
 
 #include <algorithm>
 
@@ -82,11 +83,16 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   const size_t red_bytes = (size_t)(a->waves - 1) * nacc * mt * 64 * 16;
   const size_t head = 784;
   const size_t budget = kGemmLdsX - red_bytes - head;
+  // Register passes of up to kpmax k steps; x staged for the whole range at
+  // once when it fits the LDS budget, else per pass (fewer steps per pass).
   int kp = std::min(p->ksw, kpmax);
-  while (kp > 1 && (size_t)a->rows * (a->waves * kp * 32 + 8) * 2 > budget) --kp;
+  const bool lds_all = (size_t)a->rows * (a->waves * p->ksw * 32 + 8) * 2 <= budget;
+  if (!lds_all)
+    while (kp > 1 && (size_t)a->rows * (a->waves * kp * 32 + 8) * 2 > budget) --kp;
   p->kp = kp;
   p->npass = (p->ksw + kp - 1) / kp;
-  p->xstride = a->waves * kp * 32 + 8;
+  p->lds_all = lds_all ? 1 : 0;
+  p->xstride = a->waves * (lds_all ? p->ksw : kp) * 32 + 8;
   p->lds_red_off = (int)head;
   p->lds_x_off = (int)(head + red_bytes);
   p->lds_bytes = head + red_bytes + (size_t)a->rows * p->xstride * 2;
@@ -106,7 +112,7 @@ static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) 
   if (a->t_rows < 1 || a->t_rows > 16) return set_error(QDEC_EINVAL, "qdec_attn: t_rows %d not in [1, 16]", a->t_rows);
   if (a->cap < 32 || a->cap % 32) return set_error(QDEC_EINVAL, "qdec_attn: cap %d not a positive multiple of 32", a->cap);
   if (a->chunk < 32 || a->chunk % 32) return set_error(QDEC_EINVAL, "qdec_attn: chunk %d not a positive multiple of 32", a->chunk);
-  if (a->waves < 1 || a->waves > 4) return set_error(QDEC_EINVAL, "qdec_attn: waves %d not in [1, 4]", a->waves);
+  if (a->waves != 4) return set_error(QDEC_EINVAL, "qdec_attn: waves %d (the kernel runs 4 wavefronts)", a->waves);
   const int nchunks = (a->cap + a->chunk - 1) / a->chunk;
   if (!need_scratch) goto fill;
   if (!a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->lens || !a->k_cache ||
@@ -214,6 +220,93 @@ int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream) {
   const int rc = plan_attn(a, &p, true);
   if (rc != QDEC_OK) return rc;
   return launch_status(launch_attn(p, (hipStream_t)stream), "qdec_attn");
+}
+
+size_t qdec_step_phase_bytes(void) { return sizeof(StepPhase); }
+
+int qdec_step_encode_embed(const qdec_embed_args *a, void *phase) {
+  if (!a || !a->ids || !a->emb || !a->h || !phase) return set_error(QDEC_EINVAL, "qdec_step_encode_embed: null pointer");
+  if (a->rows < 1 || a->hidden <= 0 || a->hidden % 32 || a->vocab <= 0 || a->vocab % 16)
+    return set_error(QDEC_EINVAL, "qdec_step_encode_embed: rows %d hidden %d vocab %d", a->rows, a->hidden, a->vocab);
+  if (!aligned16(a->emb) || !aligned16(a->h)) return set_error(QDEC_EALIGN, "qdec_step_encode_embed: emb and h must be 16-byte aligned");
+  StepPhase ph = {};
+  ph.kind = kPhaseEmbed;
+  ph.nblk = a->rows;
+  ph.rows = a->rows;
+  ph.e.ids = a->ids; ph.e.emb = a->emb; ph.e.h = a->h;
+  ph.e.rows = a->rows; ph.e.hidden = a->hidden; ph.e.vocab = a->vocab;
+  memcpy(phase, &ph, sizeof(ph));
+  return QDEC_OK;
+}
+
+int qdec_step_encode_gemm(const qdec_gemm_args *a, void *phase, size_t *lds_bytes) {
+  GemmParams p;
+  const int rc = plan_gemm(a, &p, true);
+  if (rc != QDEC_OK) return rc;
+  if (!phase) return set_error(QDEC_EINVAL, "qdec_step_encode_gemm: null phase");
+  if (a->waves != 4) return set_error(QDEC_EUNSUPPORTED, "qdec_step_encode_gemm: the step kernel runs 4 waves, not %d", a->waves);
+  StepPhase ph = {};
+  ph.kind = kPhaseGemm;
+  ph.flags = a->flags;
+  ph.nblk = (a->n / 16 / a->tiles_per_wg) * a->ksplit;
+  ph.rows = a->rows;
+  ph.g = p;
+  memcpy(phase, &ph, sizeof(ph));
+  if (lds_bytes) *lds_bytes = p.lds_bytes;
+  return QDEC_OK;
+}
+
+int qdec_step_encode_attn(const qdec_attn_args *a, void *phase, size_t *lds_bytes) {
+  AttnParams p;
+  const int rc = plan_attn(a, &p, true);
+  if (rc != QDEC_OK) return rc;
+  if (!phase) return set_error(QDEC_EINVAL, "qdec_step_encode_attn: null phase");
+  if (a->waves != 4) return set_error(QDEC_EUNSUPPORTED, "qdec_step_encode_attn: the step kernel runs 4 waves, not %d", a->waves);
+  StepPhase ph = {};
+  ph.kind = kPhaseAttn;
+  ph.nblk = a->batch * a->nkv * p.nchunks;
+  ph.rows = a->t_rows;
+  ph.a = p;
+  memcpy(phase, &ph, sizeof(ph));
+  if (lds_bytes) *lds_bytes = kAttnLds;
+  return QDEC_OK;
+}
+
+int qdec_step_workgroups(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  static int cached[64] = {0};
+  if (dev >= 0 && dev < 64 && cached[dev]) return cached[dev];
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  if (dev >= 0 && dev < 64) cached[dev] = prop.multiProcessorCount;
+  return prop.multiProcessorCount;
+}
+
+int qdec_step_run(const qdec_step_args *a, qdec_stream_t stream) {
+  if (!a || !a->phases || !a->ctl) return set_error(QDEC_EINVAL, "qdec_step_run: null pointer");
+  if (a->nphases < 1) return set_error(QDEC_EINVAL, "qdec_step_run: nphases %d", a->nphases);
+  if (a->max_rows < 1 || a->max_rows > 64) return set_error(QDEC_EINVAL, "qdec_step_run: max_rows %d", a->max_rows);
+  if (a->t_rows < 1 || a->t_rows > 16) return set_error(QDEC_EINVAL, "qdec_step_run: t_rows %d", a->t_rows);
+  if (a->lds_bytes < 0 || a->lds_bytes > kGemmLdsX) return set_error(QDEC_EINVAL, "qdec_step_run: lds_bytes %d", a->lds_bytes);
+  if (!aligned16(a->phases) || !aligned16(a->ctl)) return set_error(QDEC_EALIGN, "qdec_step_run: phases and ctl must be 16-byte aligned");
+  int nwg = a->workgroups;
+  if (nwg <= 0) nwg = qdec_step_workgroups();
+  if (nwg <= 0) return set_error(QDEC_ENODEV, "qdec_step_run: no HIP device");
+  const int mt = (a->max_rows + 15) / 16;
+  const int mtq = (a->t_rows * 4 + 15) / 16;
+  const uint32_t spin = a->spin_limit ? a->spin_limit : (1u << 22);
+  return launch_status(launch_step(reinterpret_cast<const StepPhase *>(a->phases), a->nphases,
+                                   reinterpret_cast<StepCtl *>(a->ctl), spin, mt, mtq, nwg,
+                                   (size_t)a->lds_bytes, reinterpret_cast<uint64_t *>(a->trace),
+                                   (hipStream_t)stream),
+                       "qdec_step_run");
 }
 
 int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream) {

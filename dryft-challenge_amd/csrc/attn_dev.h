@@ -1,0 +1,431 @@
+// Device body of the GQA decode attention with the head RMSNorm, RoPE and KV-cache write fused
+// in, for t_rows query rows per sequence (1 = plain decode, K+1 = verify).
+//
+// Grid (chunk, kv head, sequence); a workgroup of 4 wavefronts per cell.
+//   1. Every wave issues the K/V loads of its first two 32-slot blocks, then
+//      the raw loads of its share of the query rows (row r = G*t + g goes to
+//      wave r % 4) and of the new key/value rows (t % 4); a lane holds two
+//      channels of a row, so the head RMSNorm is one wave reduction and the
+//      rotate_half partner sits in lane ^ 32.  Normalised, rotated queries
+//      go to LDS; new keys go to LDS in row layout, new values in the
+//      channel-major cache layout, and the chunk owning a new slot writes it
+//      to the cache (nobody reads those cache slots in this launch).
+//   2. Each wave reads the queries back in the B-operand layout of
+//      v_mfma_f32_16x16x32_bf16 (query row r sits in MFMA column r % 16 of M
+//      tile r / 16) and walks its blocks (block j to wave j % 4, two blocks in
+//      flight): S^T = K . Q^T (two 16-slot MFMA tiles whose slot order makes
+//      the score registers exactly the B operand of the next product), online
+//      softmax in base 2, then O^T += V^T . P^T with V read from the
+//      channel-major V cache.  The block holding the new slots takes them
+//      from LDS with masks; slots past the last new one are zero.
+//   3. The waves merge in LDS in wave order; a sequence that needs one chunk
+//      is written out directly, otherwise the workgroup stores (acc, m, l) and
+//      the last chunk to arrive merges all chunks in chunk order.
+// Block-to-wave dealing and chunk boundaries are keyed to absolute slot
+// numbers, and every row's arithmetic is the same whatever t_rows is, so
+// verify rows reproduce plain decode bit for bit.
+//
+// Reference behaviour replaced: engine/kernels/fused.py:360-479
+// (_attn_fused_split_kernel), engine/kernels/ops.py:84-431 (_qkv_post_kernel,
+// _decode_attn_split_kernel, _decode_attn_reduce_kernel) and
+// notes/v10/spec.py:111-182 (_spec_attn_kernel).
+#pragma once
+
+#include "qdec_common.h"
+#include "qdec_kernels.h"
+
+namespace qdec {
+
+constexpr int kMaxT = 16;
+constexpr int kAttnWaves = 4;
+constexpr int kAttnRowStride = 128 + 8;  // bf16 per LDS row of queries / new keys (bank spread)
+// LDS layout (kAttnLds bytes).
+constexpr int kAttnKnOff = 0;                                    // new keys [kMaxT][row stride]
+constexpr int kAttnVpOff = kAttnKnOff + kMaxT * kAttnRowStride * 2;  // new values [3][128][8]
+constexpr int kAttnQOff = kAttnVpOff + 3 * 128 * 8 * 2;          // queries [64][row stride] or
+                                                                 // wave partials [4][8][64] f32x4
+constexpr int kAttnMOff = kAttnQOff + kAttnWaves * 8 * 64 * 16;  // wave row maxima [4][16]
+constexpr int kAttnLOff = kAttnMOff + kAttnWaves * 16 * 4;       // wave row sums [4][16]
+constexpr int kAttnFlagOff = kAttnLOff + kAttnWaves * 16 * 4;
+static_assert(64 * kAttnRowStride * 2 <= kAttnWaves * 8 * 64 * 16, "query rows fit the partials area");
+static_assert(kAttnLds == kAttnFlagOff + 16, "attention LDS size");
+
+template <int D, int G, int MTQ, bool COH>
+__device__ __forceinline__ void attn_block(const AttnParams &p, const int c, const int kvh, const int b,
+                                           unsigned char *smem) {
+  static_assert(D == 128 && G == 4, "head_dim 128, 4 query heads per kv head");
+  constexpr int NW = kAttnWaves;
+  constexpr int DS = D / 32;              // MFMA k steps over the head dimension
+  constexpr int DT = D / 16;              // 16-channel output tiles
+  constexpr int DTW = DT / NW;            // output tiles each wave finishes
+  constexpr bool DB = MTQ == 1;           // two blocks in flight (register budget)
+  constexpr int QPW = MTQ * 16 / NW;      // query rows per wave, at most
+  constexpr int KPW = kMaxT / NW;         // new rows per wave, at most
+  constexpr int RS = kAttnRowStride;
+
+  uint16_t *s_kn = reinterpret_cast<uint16_t *>(smem + kAttnKnOff);
+  uint16_t *s_vp = reinterpret_cast<uint16_t *>(smem + kAttnVpOff);
+  uint16_t *s_q = reinterpret_cast<uint16_t *>(smem + kAttnQOff);
+  f32x4_t *s_acc = reinterpret_cast<f32x4_t *>(smem + kAttnQOff);
+  float *s_m = reinterpret_cast<float *>(smem + kAttnMOff);
+  float *s_l = reinterpret_cast<float *>(smem + kAttnLOff);
+  uint32_t *s_flag = reinterpret_cast<uint32_t *>(smem + kAttnFlagOff);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
+  const int T = p.t_rows;
+  const int R = T * G;
+  const int L = p.lens[b];
+  const int last = L + T - 1;
+  const int c0 = c * p.chunk;
+  if (L < 0 || last >= p.cap) return;  // never index outside the cache slab
+  if (c0 > last) return;
+  const int n_active = last / p.chunk + 1;
+  const int c1 = c0 + p.chunk;                        // exclusive end of this chunk
+  const int nb = (min(c1, last + 1) - c0 + 31) / 32;  // blocks in this chunk
+  const int nq = p.nq, nkv = p.nkv;
+  const int width = (nq + 2 * nkv) * D;
+  const uint16_t *qkv = reinterpret_cast<const uint16_t *>(p.qkv);
+  const uint16_t *cos_t = reinterpret_cast<const uint16_t *>(p.cos_tab);
+  const uint16_t *sin_t = reinterpret_cast<const uint16_t *>(p.sin_tab);
+  const size_t slab = ((size_t)b * nkv + kvh) * (size_t)p.cap * D;
+  uint16_t *kc = reinterpret_cast<uint16_t *>(p.k_cache) + slab;
+  uint16_t *vc = reinterpret_cast<uint16_t *>(p.v_cache) + slab;
+  const float NEG_INF = -__builtin_huge_valf();
+
+  // K / V fragments of one 32-slot block.  K tile a row m -> slot
+  // s0 + 8*(m>>2) + (m&3), tile b -> +4; V from the channel-major cache.
+  struct Frag {
+    uint4 ka[DS], kb[DS], vf[DT];
+  };
+  auto load_block = [&](int s0, Frag &f) {
+    const int slot_a = s0 + 8 * (col >> 2) + (col & 3);
+    const int slot_b = slot_a + 4;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      f.ka[s] = *reinterpret_cast<const uint4 *>(kc + (size_t)slot_a * D + s * 32 + grp * 8);
+      f.kb[s] = *reinterpret_cast<const uint4 *>(kc + (size_t)slot_b * D + s * 32 + grp * 8);
+    }
+    const uint16_t *vblk = vc + ((size_t)((s0 >> 3) + grp) * D) * 8;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      f.vf[dt] = *reinterpret_cast<const uint4 *>(vblk + (size_t)(dt * 16 + col) * 8);
+  };
+  Frag f0, f1;
+  if (wave < nb) load_block(c0 + 32 * wave, f0);
+  if constexpr (DB) {
+    if (wave + NW < nb) load_block(c0 + 32 * (wave + NW), f1);
+  }
+
+  // ---- 1. raw query / new key / new value rows (clamped, straight-line loads).
+  const bool overlap = c1 > L;  // this chunk holds some of the new slots
+  uint32_t qraw[QPW], qcos[QPW], qsin[QPW];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int r = min(wave + NW * i, R - 1);
+    const int t = r / G, hq = r % G;
+    qraw[i] = ld4<COH>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + 2 * lane);
+    qcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
+    qsin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
+  }
+  const uint32_t qw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + 2 * lane);
+  uint32_t kraw[KPW], vraw[KPW], kcos[KPW], ksin[KPW], kw = 0u;
+  if (overlap) {
+    kw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + 2 * lane);
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int t = min(wave + NW * i, T - 1);
+      const uint16_t *row = qkv + (size_t)(b * T + t) * width;
+      kraw[i] = ld4<COH>(row + (size_t)(nq + kvh) * D + 2 * lane);
+      vraw[i] = ld4<COH>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
+      kcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
+      ksin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
+    }
+  }
+
+  // Head RMSNorm (weight w) and RoPE of the two channels 2*lane, 2*lane+1 of
+  // one head row; channel i pairs with i +- D/2, held by lane ^ 32.
+  auto norm_rope = [&](uint32_t raw, uint32_t w, uint32_t cw, uint32_t sw) -> uint32_t {
+    const float x0 = lo16(raw), x1 = hi16(raw);
+    float ss = x0 * x0 + x1 * x1;
+    ss += shfl_xor(ss, 32);
+    ss += shfl_xor(ss, 16);
+    ss += shfl_xor(ss, 8);
+    ss += shfl_xor(ss, 4);
+    ss += shfl_xor(ss, 2);
+    ss += shfl_xor(ss, 1);
+    const float rstd = 1.0f / sqrtf(ss / (float)D + p.eps);
+    const float y0 = rbf(lo16(w) * rbf(x0 * rstd));
+    const float y1 = rbf(hi16(w) * rbf(x1 * rstd));
+    const float p0 = shfl_xor(y0, 32), p1 = shfl_xor(y1, 32);
+    const bool first_half = lane < 32;
+    const float r0 = first_half ? -p0 : p0;
+    const float r1 = first_half ? -p1 : p1;
+    const float o0 = rbf(y0 * lo16(cw)) + rbf(r0 * lo16(sw));
+    const float o1 = rbf(y1 * hi16(cw)) + rbf(r1 * hi16(sw));
+    return pack2(o0, o1);
+  };
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int r = wave + NW * i;
+    if (r < R) *reinterpret_cast<uint32_t *>(s_q + r * RS + 2 * lane) = norm_rope(qraw[i], qw, qcos[i], qsin[i]);
+  }
+  if (overlap) {
+    const int g0 = L >> 3;
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int t = wave + NW * i;
+      if (t < T) {
+        const uint32_t kout = norm_rope(kraw[i], kw, kcos[i], ksin[i]);
+        const uint32_t vr = vraw[i];
+        const int slot = L + t;
+        const int gi = (slot >> 3) - g0, e = slot & 7;
+        *reinterpret_cast<uint32_t *>(s_kn + t * RS + 2 * lane) = kout;
+        s_vp[(gi * D + 2 * lane) * 8 + e] = (uint16_t)(vr & 0xffffu);
+        s_vp[(gi * D + 2 * lane + 1) * 8 + e] = (uint16_t)(vr >> 16);
+        if (slot >= c0 && slot < c1) {  // this chunk owns the slot
+          *reinterpret_cast<uint32_t *>(kc + (size_t)slot * D + 2 * lane) = kout;
+          uint16_t *vb = vc + ((size_t)(slot >> 3) * D) * 8 + e;
+          vb[(size_t)(2 * lane) * 8] = (uint16_t)(vr & 0xffffu);
+          vb[(size_t)(2 * lane + 1) * 8] = (uint16_t)(vr >> 16);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. flash-decode over this wave's blocks.
+  uint4 qf[MTQ][DS];
+  f32x4_t acc[MTQ][DT];
+  float m_run[MTQ], l_run[MTQ];
+  int lim[MTQ];  // highest slot each row may see
+#pragma unroll
+  for (int mt = 0; mt < MTQ; ++mt) {
+    const int r = mt * 16 + col;
+#pragma unroll
+    for (int s = 0; s < DS; ++s)
+      qf[mt][s] = (r < R) ? *reinterpret_cast<const uint4 *>(s_q + r * RS + s * 32 + grp * 8) : zero4();
+    m_run[mt] = NEG_INF;
+    l_run[mt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[mt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    lim[mt] = (r < R) ? L + r / G : -1;
+  }
+
+  // New slots L..last come from LDS; slots past `last` are zero (the cache
+  // may hold anything there, and 0 * NaN would poison the product).
+  auto patch = [&](Frag &f, int s0) {
+    const int slot_a = s0 + 8 * (col >> 2) + (col & 3);
+    const int slot_b = slot_a + 4;
+    const int ia = slot_a - L, ib = slot_b - L;
+    const bool new_a = (unsigned)ia < (unsigned)T, new_b = (unsigned)ib < (unsigned)T;
+    const bool zero_a = slot_a > last, zero_b = slot_b > last;
+    const uint16_t *kna = s_kn + min(max(ia, 0), kMaxT - 1) * RS + grp * 8;
+    const uint16_t *knb = s_kn + min(max(ib, 0), kMaxT - 1) * RS + grp * 8;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      const uint4 va = *reinterpret_cast<const uint4 *>(kna + s * 32);
+      const uint4 vb = *reinterpret_cast<const uint4 *>(knb + s * 32);
+      f.ka[s] = new_a ? va : (zero_a ? zero4() : f.ka[s]);
+      f.kb[s] = new_b ? vb : (zero_b ? zero4() : f.kb[s]);
+    }
+    // V: this lane's 8 slots vs0..vs0+7 of one channel per tile; keep the
+    // cache below L, take LDS for L..last, zero above.
+    const int vs0 = s0 + 8 * grp;
+    const int gi = min(max((vs0 >> 3) - (L >> 3), 0), 2);
+    uint32_t keep[4], take[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int e0 = vs0 + 2 * d, e1 = e0 + 1;
+      keep[d] = (e0 < L ? 0x0000ffffu : 0u) | (e1 < L ? 0xffff0000u : 0u);
+      take[d] = ((e0 >= L && e0 <= last) ? 0x0000ffffu : 0u) | ((e1 >= L && e1 <= last) ? 0xffff0000u : 0u);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint4 vn = *reinterpret_cast<const uint4 *>(s_vp + (size_t)(gi * D + dt * 16 + col) * 8);
+      uint4 &v = f.vf[dt];
+      v.x = (v.x & keep[0]) | (vn.x & take[0]);
+      v.y = (v.y & keep[1]) | (vn.y & take[1]);
+      v.z = (v.z & keep[2]) | (vn.z & take[2]);
+      v.w = (v.w & keep[3]) | (vn.w & take[3]);
+    }
+  };
+
+  auto process = [&](Frag &f, int j) {
+    const int s0 = c0 + 32 * j;
+    if (s0 + 32 > L) patch(f, s0);  // block touches new or unwritten slots
+#pragma unroll
+    for (int mt = 0; mt < MTQ; ++mt) {
+      f32x4_t sa = f32x4_t{0.f, 0.f, 0.f, 0.f}, sb = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        sa = mfma16x16x32(f.ka[s], qf[mt][s], sa);
+        sb = mfma16x16x32(f.kb[s], qf[mt][s], sb);
+      }
+      // lane holds slots s0 + 8*grp + j, j = 0..7, of query row mt*16 + col.
+      float sc[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sl_a = s0 + 8 * grp + i;
+        sc[i] = (sl_a <= lim[mt]) ? sa[i] * p.scale_log2 : NEG_INF;
+        sc[4 + i] = (sl_a + 4 <= lim[mt]) ? sb[i] * p.scale_log2 : NEG_INF;
+      }
+      float bmax = sc[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) bmax = fmaxf(bmax, sc[e]);
+      bmax = fmaxf(bmax, shfl_xor(bmax, 16));
+      bmax = fmaxf(bmax, shfl_xor(bmax, 32));
+      const float m_new = fmaxf(m_run[mt], bmax);
+      const float alpha = (m_new == NEG_INF) ? 1.0f : exp2f(m_run[mt] - m_new);
+      float pj[8];
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pj[e] = (sc[e] == NEG_INF) ? 0.f : exp2f(sc[e] - m_new);
+        psum += pj[e];
+      }
+      l_run[mt] = l_run[mt] * alpha + psum;
+      m_run[mt] = m_new;
+      const uint4 pf = pack8(pj);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        acc[mt][dt] *= alpha;
+        acc[mt][dt] = mfma16x16x32(f.vf[dt], pf, acc[mt][dt]);
+      }
+    }
+  };
+
+  if constexpr (DB) {
+    for (int j = wave; j < nb; j += 2 * NW) {
+      process(f0, j);
+      if (j + 2 * NW < nb) load_block(c0 + 32 * (j + 2 * NW), f0);
+      if (j + NW < nb) {
+        process(f1, j + NW);
+        if (j + 3 * NW < nb) load_block(c0 + 32 * (j + 3 * NW), f1);
+      }
+    }
+  } else {
+    for (int j = wave; j < nb; j += NW) {
+      if (j != wave) load_block(c0 + 32 * j, f0);
+      process(f0, j);
+    }
+  }
+
+  // ---- 3. merge the waves (wave order), then output or chunk partials.
+  uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
+  const size_t cstride = (size_t)R * (D + 2);  // floats per chunk partial: acc [R][D], m [R], l [R]
+  float *part_b = p.partial + ((size_t)b * nkv + kvh) * p.nchunks * cstride;
+  float *part = part_b + (size_t)c * cstride;
+#pragma unroll
+  for (int mt = 0; mt < MTQ; ++mt) {
+    const int r = mt * 16 + col;
+    float lw = l_run[mt] + shfl_xor(l_run[mt], 16);
+    lw += shfl_xor(lw, 32);  // this wave's row sum
+    __syncthreads();         // queries / the previous tile's partials are consumed
+    if (grp == 0) {
+      s_m[wave * 16 + col] = m_run[mt];
+      s_l[wave * 16 + col] = lw;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) s_acc[(wave * DT + dt) * 64 + lane] = acc[mt][dt];
+    __syncthreads();
+    float mw[NW];
+    float M = NEG_INF;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) {
+      mw[w2] = s_m[w2 * 16 + col];
+      M = fmaxf(M, mw[w2]);
+    }
+    float scw[NW];
+    float Lrow = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2) {
+      scw[w2] = (mw[w2] == NEG_INF) ? 0.f : exp2f(mw[w2] - M);
+      Lrow += s_l[w2 * 16 + col] * scw[w2];
+    }
+#pragma unroll
+    for (int i = 0; i < DTW; ++i) {
+      const int dt = wave + NW * i;
+      f32x4_t tot = s_acc[dt * 64 + lane] * scw[0];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) tot += s_acc[(w2 * DT + dt) * 64 + lane] * scw[w2];
+      if (r < R) {
+        if (n_active == 1) {
+          const int t = r / G, hq = r % G;
+          uint16_t *dst = out + (size_t)(b * T + t) * nq * D + (size_t)(kvh * G + hq) * D;
+          uint2 o;
+          o.x = pack2(tot[0] / Lrow, tot[1] / Lrow);
+          o.y = pack2(tot[2] / Lrow, tot[3] / Lrow);
+          st8<COH>(dst + dt * 16 + grp * 4, o);
+        } else {
+          store_coherent4(part + (size_t)r * D + dt * 16 + grp * 4, tot);
+        }
+      }
+    }
+    if (n_active > 1 && wave == 0 && grp == 0 && r < R) {
+      store_coherent(part + (size_t)R * D + r, M);
+      store_coherent(part + (size_t)R * D + R + r, Lrow);
+    }
+  }
+  if (n_active == 1) return;
+  if (!arrive_last(p.counters + (size_t)b * nkv + kvh, (uint32_t)n_active, s_flag)) return;
+
+  // Merge chunks 0..n_active-1 in order (chunks a row cannot see have
+  // m = -inf and are skipped).  The first CB chunks are loaded in one batch.
+  constexpr int CB = 8;
+#pragma unroll
+  for (int mt = 0; mt < MTQ; ++mt) {
+    const int r = mt * 16 + col;
+    if (r >= R) continue;
+    float mc[CB], lc[CB];
+    f32x4_t av[DTW][CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const float *pr = part_b + (size_t)min(j, n_active - 1) * cstride;
+      mc[j] = load_coherent(pr + (size_t)R * D + r);
+      lc[j] = load_coherent(pr + (size_t)R * D + R + r);
+#pragma unroll
+      for (int i = 0; i < DTW; ++i) av[i][j] = load_coherent4(pr + (size_t)r * D + (wave + NW * i) * 16 + grp * 4);
+    }
+    float mmax = NEG_INF;
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      if (j < n_active) mmax = fmaxf(mmax, mc[j]);
+    for (int ch = CB; ch < n_active; ++ch)
+      mmax = fmaxf(mmax, load_coherent(part_b + (size_t)ch * cstride + (size_t)R * D + r));
+    float lsum = 0.f;
+    f32x4_t o[DTW];
+#pragma unroll
+    for (int i = 0; i < DTW; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      if (j >= n_active || mc[j] == NEG_INF) continue;
+      const float w = exp2f(mc[j] - mmax);
+      lsum += lc[j] * w;
+#pragma unroll
+      for (int i = 0; i < DTW; ++i) o[i] += av[i][j] * w;
+    }
+    for (int ch = CB; ch < n_active; ++ch) {
+      const float *pr = part_b + (size_t)ch * cstride;
+      const float m = load_coherent(pr + (size_t)R * D + r);
+      if (m == NEG_INF) continue;
+      const float w = exp2f(m - mmax);
+      lsum += load_coherent(pr + (size_t)R * D + R + r) * w;
+#pragma unroll
+      for (int i = 0; i < DTW; ++i) o[i] += load_coherent4(pr + (size_t)r * D + (wave + NW * i) * 16 + grp * 4) * w;
+    }
+    const int t = r / G, hq = r % G;
+    uint16_t *dst = out + (size_t)(b * T + t) * nq * D + (size_t)(kvh * G + hq) * D;
+#pragma unroll
+    for (int i = 0; i < DTW; ++i) {
+      uint2 ov;
+      ov.x = pack2(o[i][0] / lsum, o[i][1] / lsum);
+      ov.y = pack2(o[i][2] / lsum, o[i][3] / lsum);
+      st8<COH>(dst + (wave + NW * i) * 16 + grp * 4, ov);
+    }
+  }
+}
+
+}  // namespace qdec

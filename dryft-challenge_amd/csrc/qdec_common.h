@@ -17,13 +17,17 @@ constexpr int kTileK = 32;   // k per MFMA step
 constexpr int kBlockElems = kTileN * kTileK;  // 512 bf16 = 1 KiB
 
 // ---------------------------------------------------------------- bf16 math
-// Round-to-nearest-even float -> bf16, the rounding torch's .to(bfloat16)
-// performs; NaN maps to the canonical quiet NaN.
+// float -> bf16 with round-to-nearest-even, the rounding torch's
+// .to(bfloat16) performs, in one gfx950 instruction (v_cvt_pk_bf16_f32, two
+// values at a time).  NaN stays NaN (torch writes the canonical 0x7fc0; no
+// NaN reaches a comparison in this library).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
 }
 __device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
 // Value of f after a round trip through bf16.
@@ -37,9 +41,6 @@ __device__ __forceinline__ void unpack8(const uint4 &v, float f[8]) {
   f[2] = lo16(v.y); f[3] = hi16(v.y);
   f[4] = lo16(v.z); f[5] = hi16(v.z);
   f[6] = lo16(v.w); f[7] = hi16(v.w);
-}
-__device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return f2bf(a) | (f2bf(b) << 16);
 }
 __device__ __forceinline__ uint4 pack8(const float f[8]) {
   uint4 v;
@@ -68,13 +69,66 @@ __device__ __forceinline__ float load_coherent(const float *p) {
 __device__ __forceinline__ void store_coherent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// 16-byte versions: volatile vector accesses compile to cache-bypassing
-// (system-scope) loads/stores, so several can be in flight at once.
+// Activation accesses, parameterised on coherence.  Inside one launch of the
+// persistent step kernel (step.hip) activations pass between workgroups on
+// different XCDs, whose L2s are not coherent with each other: there every
+// activation store and load is a device-scope access, performed at the
+// device's point of coherence (COH = true).  Separate kernel launches get
+// coherence from the launch boundaries (COH = false).  Device-scope 64-bit
+// relaxed atomics compile to plain global_load/store_dwordx2 with the sc1
+// (device scope) cache policy, so they pipeline like ordinary loads.
+__device__ __forceinline__ uint64_t ld64_dev(const void *p) {
+  return __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st64_dev(void *p, uint64_t v) {
+  __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool COH>
+__device__ __forceinline__ uint4 ld16(const void *p) {
+  if constexpr (COH) {
+    const uint64_t a = ld64_dev(p), b = ld64_dev(reinterpret_cast<const uint64_t *>(p) + 1);
+    return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+template <bool COH>
+__device__ __forceinline__ uint2 ld8(const void *p) {
+  if constexpr (COH) {
+    const uint64_t a = ld64_dev(p);
+    return make_uint2((uint32_t)a, (uint32_t)(a >> 32));
+  } else {
+    return *reinterpret_cast<const uint2 *>(p);
+  }
+}
+template <bool COH>
+__device__ __forceinline__ uint32_t ld4(const void *p) {
+  if constexpr (COH) return __hip_atomic_load(reinterpret_cast<const uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else return *reinterpret_cast<const uint32_t *>(p);
+}
+template <bool COH>
+__device__ __forceinline__ void st8(void *p, uint2 v) {
+  if constexpr (COH) st64_dev(p, (uint64_t)v.x | ((uint64_t)v.y << 32));
+  else *reinterpret_cast<uint2 *>(p) = v;
+}
+template <bool COH>
+__device__ __forceinline__ void st16(void *p, uint4 v) {
+  if constexpr (COH) {
+    st64_dev(p, (uint64_t)v.x | ((uint64_t)v.y << 32));
+    st64_dev(reinterpret_cast<uint64_t *>(p) + 1, (uint64_t)v.z | ((uint64_t)v.w << 32));
+  } else {
+    *reinterpret_cast<uint4 *>(p) = v;
+  }
+}
+
+// 16-byte fp32 partials handed between workgroups (device scope).
 __device__ __forceinline__ f32x4_t load_coherent4(const float *p) {
-  return *reinterpret_cast<volatile const f32x4_t *>(p);
+  const uint4 v = ld16<true>(p);
+  return f32x4_t{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
 }
 __device__ __forceinline__ void store_coherent4(float *p, f32x4_t v) {
-  *reinterpret_cast<volatile f32x4_t *>(p) = v;
+  st16<true>(p, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                           __float_as_uint(v[3])));
 }
 __device__ __forceinline__ int load_coherent_i(const int *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

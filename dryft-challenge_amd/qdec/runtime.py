@@ -96,14 +96,10 @@ def role_plan(n, k, role):
     ntiles = n // 16
     waves = 4
     ksplit = 1
-    if role == "o":
-        # 160 tiles x 8 waves of 16 k steps measured faster than any k split.
-        waves = 8
-    elif role == "down":
-        # Aim for >= 512 workgroups while keeping >= 8 k steps per wave.
-        for cand in (2, 4, 8):
-            if ks % (cand * waves) == 0 and ks // (cand * waves) >= 8 and ntiles * ksplit < 512:
-                ksplit = cand
+    # O and down (N = hidden, 160 tiles) stream k in several register passes
+    # per wave instead of splitting it across workgroups: a pure streaming
+    # read of the same bytes is as fast with 160 x 4 long waves as with 4x
+    # more short ones, and no cross-workgroup reduction sits on the tail.
     while (ks // ksplit) % waves:
         waves //= 2
     tiles = 1
@@ -236,6 +232,10 @@ class DecodeState:
         self.attn_counters = torch.zeros((max(ac, 4) // 4 + 4,), dtype=torch.int32, device=dev)
         self._gemm_cache = {}
         self._attn_cache = {}
+        # persistent step kernel: barrier state + cached phase tables
+        self.step_ctl = torch.zeros((4,), dtype=torch.int32, device=dev)
+        self._tables = {}
+        self.use_step_kernel = True
 
     # ----------------------------------------------------------- arguments
     def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None):
@@ -331,6 +331,69 @@ class DecodeState:
             a = self._attn_args(layer, t_rows)
             self._attn_cache[key] = a
         return a
+
+    # ---------------------------------------------- persistent step kernel
+    def _step_table(self, t_rows, lm_head, ids_out, advance):
+        """Phase table of one forward (the same calls run_step issues) in
+        device memory, cached per shape of the call."""
+        key = (t_rows, lm_head, None if ids_out is None else ids_out.data_ptr(), advance)
+        tab = self._tables.get(key)
+        if tab is not None:
+            return tab
+        import ctypes
+        lib, m, c = self.lib, self.model, self.model.cfg
+        rows = self.batch * t_rows
+        pb = lib.step_phase_bytes()
+        nph = 1 + 5 * c.n_layers + (1 if lm_head else 0)
+        host = (ctypes.c_ubyte * (pb * nph))()
+        base = ctypes.addressof(host)
+        lds = 0
+        e = capi.EmbedArgs()
+        e.ids, e.emb, e.h = self.ids.data_ptr(), m.emb.data_ptr(), self.h.data_ptr()
+        e.rows, e.hidden, e.vocab = rows, c.hidden, c.vocab
+        lib.step_encode_embed(e, base)
+        i = 1
+        for layer in range(c.n_layers):
+            for role in ("qkv", None, "o", "gate_up", "down"):
+                if role is None:
+                    lds = max(lds, lib.step_encode_attn(self._cached_attn(layer, t_rows), base + i * pb))
+                else:
+                    lds = max(lds, lib.step_encode_gemm(self._cached_gemm(role, layer, rows), base + i * pb))
+                i += 1
+        if lm_head:
+            a = self._gemm_args("lm", 0, rows, ids_out=ids_out,
+                                lens_inc=self.lens if (advance and t_rows == 1) else None)
+            lds = max(lds, lib.step_encode_gemm(a, base + i * pb))
+            i += 1
+        dev_tab = torch.frombuffer(bytearray(host), dtype=torch.uint8).to(self.model.device)
+        args = capi.StepArgs()
+        args.phases, args.nphases, args.spin_limit = dev_tab.data_ptr(), nph, 0
+        args.ctl = self.step_ctl.data_ptr()
+        args.max_rows, args.t_rows, args.lds_bytes, args.workgroups = rows, t_rows, lds, 0
+        tab = (dev_tab, args)
+        self._tables[key] = tab
+        return tab
+
+    def run_step_persistent(self, t_rows=1, lm_head=True, ids_out=None, advance=True, stream=None):
+        """``run_step`` as one launch of the persistent step kernel (same
+        phases, same per-block code, bit-identical results)."""
+        if t_rows < 1 or t_rows > self.max_t:
+            raise ValueError(f"t_rows {t_rows} not in [1, {self.max_t}]")
+        if advance and lm_head and t_rows != 1:
+            raise ValueError("advance needs t_rows == 1")
+        _, args = self._step_table(t_rows, lm_head, ids_out, advance)
+        s = (stream or torch.cuda.current_stream(self.model.device)).cuda_stream
+        self.lib.step_run(args, s)
+
+    def step(self, t_rows=1, lm_head=True, ids_out=None, advance=True, stream=None):
+        """One forward through the persistent step kernel or the per-op
+        launches (``use_step_kernel``); the two give identical bits."""
+        fn = self.run_step_persistent if self.use_step_kernel else self.run_step
+        fn(t_rows=t_rows, lm_head=lm_head, ids_out=ids_out, advance=advance, stream=stream)
+
+    def step_error(self):
+        """Error word of the step kernel's barrier (0 = fine)."""
+        return int(self.step_ctl[2].item())
 
     # ------------------------------------------------------------- prefill
     def prefill(self, prompt, stream=None):

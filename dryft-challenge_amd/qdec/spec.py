@@ -57,7 +57,7 @@ class SpecDecoder:
                                           self.draft.data_ptr())
         d.batch, d.cap, d.primary, d.backoff, d.k = B, st.cap, self.primary, self.backoff, self.k
         lib.ngram_draft(d, s)
-        st.run_step(t_rows=self.T, lm_head=True, ids_out=st.out_tok, advance=False)
+        st.step(t_rows=self.T, lm_head=True, ids_out=st.out_tok, advance=False)
         a = capi.AcceptArgs()
         a.out_tok, a.draft, a.hist, a.lens, a.naccept = (st.out_tok.data_ptr(), self.draft.data_ptr(),
                                                          self.hist.data_ptr(), st.lens.data_ptr(),

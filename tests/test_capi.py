@@ -104,7 +104,7 @@ def _attn(**kw):
 
 @pytest.mark.parametrize("kw,code", [
     (dict(head_dim=64), -3), (dict(nq=16), -3), (dict(t_rows=17), -1), (dict(cap=100), -1),
-    (dict(chunk=48), -1), (dict(waves=5), -1), (dict(out=None), -1), (dict(partial=None), -1), (dict(qkv=8), -2),
+    (dict(chunk=48), -1), (dict(waves=5), -1), (dict(waves=2), -1), (dict(out=None), -1), (dict(partial=None), -1), (dict(qkv=8), -2),
 ])
 def test_attn_validation(qlib, kw, code):
     assert qlib.so.qdec_attn(ctypes.byref(_attn(**kw)), None) == code
@@ -135,7 +135,11 @@ def test_role_plans_do_not_depend_on_rows():
         ks, w, t = role_plan(n, k, role)
         assert (k // 32) % (ks * w) == 0
         assert (n // 16) % t == 0
-    assert role_plan(2560, 9728, "down")[0] > 1 and role_plan(2560, 4096, "o")[1] == 8
+    assert role_plan(2560, 9728, "down")[0] == 1 and role_plan(2560, 4096, "o")[0] == 1
+    # every role runs 4 waves: the persistent step kernel executes the same plans
+    assert all(role_plan(n, k, r)[1] == 4 for r, n, k in (("qkv", 6144, 2560), ("o", 2560, 4096),
+                                                          ("gate_up", 9728, 2560), ("down", 2560, 9728),
+                                                          ("lm", 151936, 2560)))
     for b, cap in ((1, 800), (4, 1568), (32, 4384)):
         c = attn_chunk(b, 8, cap)
         assert c % 32 == 0 and 64 <= c <= cap
