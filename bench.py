@@ -138,8 +138,6 @@ def main():
     ap.add_argument("--ckpt", default=os.environ.get("QDEC_BENCH_CKPT", "/tmp/qdec_qwen3_4b_seed0"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-prompt", type=int, default=64)
-    ap.add_argument("--path", default="launch", choices=("step", "launch"),
-                    help="persistent step kernel (one launch per step) or one launch per op")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (every box has one MI355X); "
@@ -157,7 +155,7 @@ def main():
     ensure_checkpoint(args.ckpt, cfg, seed=0)
     log(f"checkpoint ready at {args.ckpt} ({time.perf_counter() - t0:.1f}s)")
     t0 = time.perf_counter()
-    eng = Engine(args.ckpt, step_kernel=(args.path == "step"))
+    eng = Engine(args.ckpt)
     log(f"engine loaded ({time.perf_counter() - t0:.1f}s)")
     mc = eng.model.cfg
     wbytes = eng.model.weight_bytes()

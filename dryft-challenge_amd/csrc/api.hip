@@ -97,6 +97,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->lds_x_off = (int)(head + red_bytes);
   p->lds_bytes = head + red_bytes + (size_t)a->rows * p->xstride * 2;
   p->xfast = gemm_fast_path(*p, f) ? 1 : 0;
+  p->rw = gemm_window(*p, f);
   if (p->lds_bytes > (size_t)kGemmLdsX)
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: rows %d x waves %d needs %zu B of LDS", a->rows, a->waves,
                      p->lds_bytes);
@@ -220,93 +221,6 @@ int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream) {
   const int rc = plan_attn(a, &p, true);
   if (rc != QDEC_OK) return rc;
   return launch_status(launch_attn(p, (hipStream_t)stream), "qdec_attn");
-}
-
-size_t qdec_step_phase_bytes(void) { return sizeof(StepPhase); }
-
-int qdec_step_encode_embed(const qdec_embed_args *a, void *phase) {
-  if (!a || !a->ids || !a->emb || !a->h || !phase) return set_error(QDEC_EINVAL, "qdec_step_encode_embed: null pointer");
-  if (a->rows < 1 || a->hidden <= 0 || a->hidden % 32 || a->vocab <= 0 || a->vocab % 16)
-    return set_error(QDEC_EINVAL, "qdec_step_encode_embed: rows %d hidden %d vocab %d", a->rows, a->hidden, a->vocab);
-  if (!aligned16(a->emb) || !aligned16(a->h)) return set_error(QDEC_EALIGN, "qdec_step_encode_embed: emb and h must be 16-byte aligned");
-  StepPhase ph = {};
-  ph.kind = kPhaseEmbed;
-  ph.nblk = a->rows;
-  ph.rows = a->rows;
-  ph.e.ids = a->ids; ph.e.emb = a->emb; ph.e.h = a->h;
-  ph.e.rows = a->rows; ph.e.hidden = a->hidden; ph.e.vocab = a->vocab;
-  memcpy(phase, &ph, sizeof(ph));
-  return QDEC_OK;
-}
-
-int qdec_step_encode_gemm(const qdec_gemm_args *a, void *phase, size_t *lds_bytes) {
-  GemmParams p;
-  const int rc = plan_gemm(a, &p, true);
-  if (rc != QDEC_OK) return rc;
-  if (!phase) return set_error(QDEC_EINVAL, "qdec_step_encode_gemm: null phase");
-  if (a->waves != 4) return set_error(QDEC_EUNSUPPORTED, "qdec_step_encode_gemm: the step kernel runs 4 waves, not %d", a->waves);
-  StepPhase ph = {};
-  ph.kind = kPhaseGemm;
-  ph.flags = a->flags;
-  ph.nblk = (a->n / 16 / a->tiles_per_wg) * a->ksplit;
-  ph.rows = a->rows;
-  ph.g = p;
-  memcpy(phase, &ph, sizeof(ph));
-  if (lds_bytes) *lds_bytes = p.lds_bytes;
-  return QDEC_OK;
-}
-
-int qdec_step_encode_attn(const qdec_attn_args *a, void *phase, size_t *lds_bytes) {
-  AttnParams p;
-  const int rc = plan_attn(a, &p, true);
-  if (rc != QDEC_OK) return rc;
-  if (!phase) return set_error(QDEC_EINVAL, "qdec_step_encode_attn: null phase");
-  if (a->waves != 4) return set_error(QDEC_EUNSUPPORTED, "qdec_step_encode_attn: the step kernel runs 4 waves, not %d", a->waves);
-  StepPhase ph = {};
-  ph.kind = kPhaseAttn;
-  ph.nblk = a->batch * a->nkv * p.nchunks;
-  ph.rows = a->t_rows;
-  ph.a = p;
-  memcpy(phase, &ph, sizeof(ph));
-  if (lds_bytes) *lds_bytes = kAttnLds;
-  return QDEC_OK;
-}
-
-int qdec_step_workgroups(void) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  static int cached[64] = {0};
-  if (dev >= 0 && dev < 64 && cached[dev]) return cached[dev];
-  hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
-    (void)hipGetLastError();
-    return 0;
-  }
-  if (dev >= 0 && dev < 64) cached[dev] = prop.multiProcessorCount;
-  return prop.multiProcessorCount;
-}
-
-int qdec_step_run(const qdec_step_args *a, qdec_stream_t stream) {
-  if (!a || !a->phases || !a->ctl) return set_error(QDEC_EINVAL, "qdec_step_run: null pointer");
-  if (a->nphases < 1) return set_error(QDEC_EINVAL, "qdec_step_run: nphases %d", a->nphases);
-  if (a->max_rows < 1 || a->max_rows > 64) return set_error(QDEC_EINVAL, "qdec_step_run: max_rows %d", a->max_rows);
-  if (a->t_rows < 1 || a->t_rows > 16) return set_error(QDEC_EINVAL, "qdec_step_run: t_rows %d", a->t_rows);
-  if (a->lds_bytes < 0 || a->lds_bytes > kGemmLdsX) return set_error(QDEC_EINVAL, "qdec_step_run: lds_bytes %d", a->lds_bytes);
-  if (!aligned16(a->phases) || !aligned16(a->ctl)) return set_error(QDEC_EALIGN, "qdec_step_run: phases and ctl must be 16-byte aligned");
-  int nwg = a->workgroups;
-  if (nwg <= 0) nwg = qdec_step_workgroups();
-  if (nwg <= 0) return set_error(QDEC_ENODEV, "qdec_step_run: no HIP device");
-  const int mt = (a->max_rows + 15) / 16;
-  const int mtq = (a->t_rows * 4 + 15) / 16;
-  const uint32_t spin = a->spin_limit ? a->spin_limit : (1u << 22);
-  return launch_status(launch_step(reinterpret_cast<const StepPhase *>(a->phases), a->nphases,
-                                   reinterpret_cast<StepCtl *>(a->ctl), spin, mt, mtq, nwg,
-                                   (size_t)a->lds_bytes, reinterpret_cast<uint64_t *>(a->trace),
-                                   (hipStream_t)stream),
-                       "qdec_step_run");
 }
 
 int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream) {

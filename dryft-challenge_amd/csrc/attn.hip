@@ -35,7 +35,7 @@ namespace {
 template <int D, int G, int MTQ>
 __global__ void __launch_bounds__(256) attn_kernel(const AttnParams p) {
   __shared__ __align__(16) unsigned char smem[kAttnLds];
-  attn_block<D, G, MTQ, false>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+  attn_block<D, G, MTQ>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }
 
 }  // namespace

@@ -50,7 +50,7 @@ constexpr int kAttnFlagOff = kAttnLOff + kAttnWaves * 16 * 4;
 static_assert(64 * kAttnRowStride * 2 <= kAttnWaves * 8 * 64 * 16, "query rows fit the partials area");
 static_assert(kAttnLds == kAttnFlagOff + 16, "attention LDS size");
 
-template <int D, int G, int MTQ, bool COH>
+template <int D, int G, int MTQ>
 __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, const int kvh, const int b,
                                            unsigned char *smem) {
   static_assert(D == 128 && G == 4, "head_dim 128, 4 query heads per kv head");
@@ -126,7 +126,7 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   for (int i = 0; i < QPW; ++i) {
     const int r = min(wave + NW * i, R - 1);
     const int t = r / G, hq = r % G;
-    qraw[i] = ld4<COH>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + 2 * lane);
+    qraw[i] = *reinterpret_cast<const uint32_t *>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + 2 * lane);
     qcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
     qsin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
   }
@@ -138,8 +138,8 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
     for (int i = 0; i < KPW; ++i) {
       const int t = min(wave + NW * i, T - 1);
       const uint16_t *row = qkv + (size_t)(b * T + t) * width;
-      kraw[i] = ld4<COH>(row + (size_t)(nq + kvh) * D + 2 * lane);
-      vraw[i] = ld4<COH>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
+      kraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + kvh) * D + 2 * lane);
+      vraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
       kcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
       ksin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
     }
@@ -358,7 +358,7 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
           uint2 o;
           o.x = pack2(tot[0] / Lrow, tot[1] / Lrow);
           o.y = pack2(tot[2] / Lrow, tot[3] / Lrow);
-          st8<COH>(dst + dt * 16 + grp * 4, o);
+          *reinterpret_cast<uint2 *>(dst + dt * 16 + grp * 4) = o;
         } else {
           store_coherent4(part + (size_t)r * D + dt * 16 + grp * 4, tot);
         }
@@ -373,7 +373,8 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   if (!arrive_last(p.counters + (size_t)b * nkv + kvh, (uint32_t)n_active, s_flag)) return;
 
   // Merge chunks 0..n_active-1 in order (chunks a row cannot see have
-  // m = -inf and are skipped).  The first CB chunks are loaded in one batch.
+  // m = -inf and are skipped).  Up to CB chunks are loaded in one batch; more
+  // take one batch of maxima and one of partials per CB chunks.
   constexpr int CB = 8;
 #pragma unroll
   for (int mt = 0; mt < MTQ; ++mt) {
@@ -381,40 +382,44 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
     if (r >= R) continue;
     float mc[CB], lc[CB];
     f32x4_t av[DTW][CB];
+    auto load_group = [&](int cc) {
 #pragma unroll
-    for (int j = 0; j < CB; ++j) {
-      const float *pr = part_b + (size_t)min(j, n_active - 1) * cstride;
-      mc[j] = load_coherent(pr + (size_t)R * D + r);
-      lc[j] = load_coherent(pr + (size_t)R * D + R + r);
+      for (int j = 0; j < CB; ++j) {
+        const float *pr = part_b + (size_t)min(cc + j, n_active - 1) * cstride;
+        mc[j] = load_coherent(pr + (size_t)R * D + r);
+        lc[j] = load_coherent(pr + (size_t)R * D + R + r);
 #pragma unroll
-      for (int i = 0; i < DTW; ++i) av[i][j] = load_coherent4(pr + (size_t)r * D + (wave + NW * i) * 16 + grp * 4);
-    }
+        for (int i = 0; i < DTW; ++i) av[i][j] = load_coherent4(pr + (size_t)r * D + (wave + NW * i) * 16 + grp * 4);
+      }
+    };
+    load_group(0);
     float mmax = NEG_INF;
 #pragma unroll
     for (int j = 0; j < CB; ++j)
       if (j < n_active) mmax = fmaxf(mmax, mc[j]);
-    for (int ch = CB; ch < n_active; ++ch)
-      mmax = fmaxf(mmax, load_coherent(part_b + (size_t)ch * cstride + (size_t)R * D + r));
+    for (int cc = CB; cc < n_active; cc += CB) {
+      float mg[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        mg[j] = load_coherent(part_b + (size_t)min(cc + j, n_active - 1) * cstride + (size_t)R * D + r);
+#pragma unroll
+      for (int j = 0; j < CB; ++j)
+        if (cc + j < n_active) mmax = fmaxf(mmax, mg[j]);
+    }
     float lsum = 0.f;
     f32x4_t o[DTW];
 #pragma unroll
     for (int i = 0; i < DTW; ++i) o[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int cc = 0; cc < n_active; cc += CB) {
+      if (cc > 0) load_group(cc);
 #pragma unroll
-    for (int j = 0; j < CB; ++j) {
-      if (j >= n_active || mc[j] == NEG_INF) continue;
-      const float w = exp2f(mc[j] - mmax);
-      lsum += lc[j] * w;
+      for (int j = 0; j < CB; ++j) {
+        if (cc + j >= n_active || mc[j] == NEG_INF) continue;
+        const float w = exp2f(mc[j] - mmax);
+        lsum += lc[j] * w;
 #pragma unroll
-      for (int i = 0; i < DTW; ++i) o[i] += av[i][j] * w;
-    }
-    for (int ch = CB; ch < n_active; ++ch) {
-      const float *pr = part_b + (size_t)ch * cstride;
-      const float m = load_coherent(pr + (size_t)R * D + r);
-      if (m == NEG_INF) continue;
-      const float w = exp2f(m - mmax);
-      lsum += load_coherent(pr + (size_t)R * D + R + r) * w;
-#pragma unroll
-      for (int i = 0; i < DTW; ++i) o[i] += load_coherent4(pr + (size_t)r * D + (wave + NW * i) * 16 + grp * 4) * w;
+        for (int i = 0; i < DTW; ++i) o[i] += av[i][j] * w;
+      }
     }
     const int t = r / G, hq = r % G;
     uint16_t *dst = out + (size_t)(b * T + t) * nq * D + (size_t)(kvh * G + hq) * D;
@@ -423,7 +428,7 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
       uint2 ov;
       ov.x = pack2(o[i][0] / lsum, o[i][1] / lsum);
       ov.y = pack2(o[i][2] / lsum, o[i][3] / lsum);
-      st8<COH>(dst + (wave + NW * i) * 16 + grp * 4, ov);
+      *reinterpret_cast<uint2 *>(dst + (wave + NW * i) * 16 + grp * 4) = ov;
     }
   }
 }

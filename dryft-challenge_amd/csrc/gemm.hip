@@ -5,16 +5,23 @@
 // pieces.  Each wave streams its part of the tiled weight -- one 1 KiB block
 // per k step, one 16-byte load per lane -- straight into the A operand of
 // v_mfma_f32_16x16x32_bf16, while the activations (normalised on the way in
-// when NORM_IN) are staged once per workgroup in LDS and read as the B
-// operand.  The product is computed transposed (y^T = W . x'^T), so a lane
-// ends up holding 4 consecutive output columns of one row.
+// when NORM_IN) are staged in LDS and read as the B operand.  The product is
+// computed transposed (y^T = W . x'^T), so a lane ends up holding 4
+// consecutive output columns of one row.
 //
-// Latency: the first pass's weight loads are issued before anything else;
-// for small row counts the activations are then loaded once into registers
-// (statistics and LDS staging come from those registers), so the norm
-// prologue overlaps the weight stream instead of preceding it.  With several
-// tiles per workgroup the next tile's weights are requested before the
-// current tile's epilogue.
+// Two ways of streaming the weights:
+//  * window (up to 16 rows, the workgroup's whole k range of x in LDS): a
+//    ring of RW weight registers per wave.  The block consumed at ring slot r
+//    is immediately replaced by the block RW steps further along the wave's
+//    sequence (k steps of its tile, then of its next tile), so RW loads stay
+//    in flight from the first MFMA to the last and the stream never drains
+//    between passes or tiles.  RW divides the wave's k steps per tile, which
+//    keeps slot r on k step r (mod RW) in every tile.
+//  * passes (everything else): up to 20 blocks per wave per pass, activations
+//    staged per pass when the whole range does not fit LDS.
+// In both, the activations are loaded before the first weights: they are
+// cache hits, and the statistics and LDS staging computed from them overlap
+// the weight stream (loads complete in issue order).
 //
 // Summation order of an output element: MFMA chain over the wave's k steps in
 // increasing order, then waves 0..W-1 added in order, then k splits 0..S-1
@@ -22,54 +29,515 @@
 // of a row is summed by thread t over the row's 16-byte vectors t, t+T, ...
 // and then across lanes and waves in a fixed tree, whatever the path.  None
 // of it depends on the number of rows, which is what lets a verify pass over
-// B*T rows reproduce the plain B-row step bit for bit.
+// B*T rows reproduce the plain B-row step bit for bit.  (The path is chosen
+// per role from (n, k) and the row count's M tiles; rows 1..16 share one.)
 //
 // Reference behaviour replaced: engine/kernels/fused.py:33-235 (_gemv_kernel,
 // _gemv_vec_kernel, _gemv_splitk_kernel + reduce) and the lm_head + argmax of
 // engine/engine.py:492-498, 542-545.
-#include "gemm_dev.h"
+#include "qdec_common.h"
+#include "qdec_kernels.h"
 
 namespace qdec {
 
 namespace {
 
-template <int MT, uint32_t FLAGS>
+// Weight registers a wave holds per pass: 20 blocks, or 2 x 10 with GLU.
+constexpr int kWbuf = 20;
+static_assert(kGemmKpMax == kWbuf && 2 * kGemmKpMaxGlu == kWbuf, "pass register budget");
+
+// Activations from registers: up to kFastRows rows, 2 vectors per thread per row.
+constexpr int kFastRows = 4;
+constexpr int kFastVec = 2;
+
+// Sum one fp32 value per thread of the workgroup for up to 8 rows in a fixed
+// order (lane tree, then waves in order); thread m < nrows gets row m's total.
+__device__ __forceinline__ void block_row_sums(float (&ss)[8], float *s_red, int nrows, float *dst_rstd, int m0,
+                                               int k, float eps) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float v = ss[j];
+    v += shfl_xor(v, 32);
+    v += shfl_xor(v, 16);
+    v += shfl_xor(v, 8);
+    v += shfl_xor(v, 4);
+    v += shfl_xor(v, 2);
+    v += shfl_xor(v, 1);
+    if (lane == 0) s_red[wave * 8 + j] = v;
+  }
+  __syncthreads();
+  if (tid < 8 && tid < nrows) {
+    float t = 0.f;
+    for (int w2 = 0; w2 < (int)(blockDim.x >> 6); ++w2) t += s_red[w2 * 8 + tid];
+    dst_rstd[m0 + tid] = 1.0f / sqrtf(t / (float)k + eps);
+  }
+  __syncthreads();
+}
+
+// x' = norm_w * bf16(x * rstd) of 8 consecutive elements (one 16-byte vector).
+__device__ __forceinline__ uint4 norm8(const uint4 &xv, const uint4 &nv, float rs) {
+  float f[8], g[8];
+  unpack8(xv, f);
+  unpack8(nv, g);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = g[e] * rbf(f[e] * rs);
+  return pack8(f);
+}
+
+template <int MT, uint32_t FLAGS, int RW>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
-  uint4 wbuf[kWbuf];
-  gemm_block<MT, FLAGS, false>(p, blockIdx.x, gridDim.x, smem, wbuf, false);
+  constexpr bool NORM = (FLAGS & QDEC_NORM_IN) != 0;
+  constexpr bool GLU = (FLAGS & QDEC_GLU) != 0;
+  constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
+  constexpr bool ARG = (FLAGS & QDEC_ARGMAX) != 0;
+  constexpr int NACC = GLU ? 2 : 1;
+  constexpr bool WIN = RW > 0;
+  static_assert(!WIN || MT == 1, "the window path serves one M tile");
+  constexpr int NB = WIN ? RW : (GLU ? kGemmKpMaxGlu : kGemmKpMax);  // weight registers per accumulator
+
+  float *s_rstd = reinterpret_cast<float *>(smem);              // [64]
+  uint32_t *s_flag = reinterpret_cast<uint32_t *>(smem + 256);  // [4]
+  float *s_red = reinterpret_cast<float *>(smem + 272);         // [64 floats]
+  uint16_t *s_x = reinterpret_cast<uint16_t *>(smem + p.lds_x_off);  // [rows][xstride]
+
+  const int blk = blockIdx.x, nblk = gridDim.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nthr = blockDim.x;
+  const int nw = nthr >> 6;
+  const int rows = p.rows;
+  const int col = lane & 15;  // row of x inside an M tile
+  const int grp = lane >> 4;  // k group / output column group
+
+  const int tg = blk / p.ksplit;                // tile group
+  const int split = blk - tg * p.ksplit;
+  const int ks_wg = split * (p.KS / p.ksplit);  // first k step of this workgroup
+  const int ks_wave = ks_wg + wave * p.ksw;     // first k step of this wave
+  const int xstride = p.xstride;
+  const uint4 *__restrict__ W = reinterpret_cast<const uint4 *>(p.w);
+  const uint16_t *__restrict__ X = reinterpret_cast<const uint16_t *>(p.x);
+  const size_t up_off = (size_t)p.up_tiles * p.KS * 64;
+  const int tile0 = tg * p.tiles_per_wg;
+
+  uint4 wb[NACC][NB];
+  // Weight block of k step i (relative to the wave's range) of `tile`.
+  auto wptr = [&](int tile, int i) { return W + ((size_t)tile * p.KS + ks_wave + i) * 64 + lane; };
+  // Passes: straight-line loads of one pass; indices past the pass are clamped
+  // to its last block (a redundant, cache-served load) instead of branched
+  // around, so all of them stay in flight together.
+  auto issue_pass = [&](int tile, int kbeg, int kcnt) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const uint4 *q = wptr(tile, kbeg + min(i, kcnt - 1));
+      wb[0][i] = q[0];
+      if constexpr (GLU) wb[1][i] = q[up_off];
+    }
+  };
+  // Window: the first RW k steps of the first tile (RW divides ksw).
+  auto issue_first = [&]() {
+    if constexpr (WIN) {
+      const uint4 *q = wptr(tile0, 0);
+#pragma unroll
+      for (int r = 0; r < NB; ++r) {
+        wb[0][r] = q[r * 64];
+        if constexpr (GLU) wb[1][r] = q[r * 64 + up_off];
+      }
+    } else {
+      issue_pass(tile0, 0, min(p.kp, p.ksw));
+    }
+  };
+
+  // ---- activations.
+  const int lds_steps = p.lds_all ? p.ksw : p.kp;  // LDS columns per wave
+  bool staged = false;
+  if (p.xfast) {
+    // Row m, vectors vr = tid + j*nthr of the workgroup's k range (per_row
+    // of them), loaded into registers before the first weights.
+    const int per_row = p.ksw * nw * 4;
+    uint4 xr[kFastRows][kFastVec];
+#pragma unroll
+    for (int m = 0; m < kFastRows; ++m)
+#pragma unroll
+      for (int j = 0; j < kFastVec; ++j) {
+        const int vr = tid + j * nthr;
+        const bool ok = m < rows && vr < per_row;
+        const int mm = ok ? m : 0, vv = ok ? vr : 0;
+        const uint4 v = *reinterpret_cast<const uint4 *>(X + (size_t)mm * p.k + ks_wg * 32 + 8 * vv);
+        xr[m][j] = ok ? v : zero4();
+      }
+    issue_first();
+    if constexpr (NORM) {
+      float ss[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss[j] = 0.f;
+#pragma unroll
+      for (int m = 0; m < kFastRows; ++m)
+#pragma unroll
+        for (int j = 0; j < kFastVec; ++j) {
+          float f[8];
+          unpack8(xr[m][j], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss[m] += f[e] * f[e];
+        }
+      block_row_sums(ss, s_red, rows, s_rstd, 0, p.k, p.eps);
+    }
+#pragma unroll
+    for (int m = 0; m < kFastRows; ++m)
+#pragma unroll
+      for (int j = 0; j < kFastVec; ++j) {
+        const int vr = tid + j * nthr;
+        if (m < rows && vr < per_row) {
+          uint4 xv = xr[m][j];
+          if constexpr (NORM)
+            xv = norm8(xv, *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p.norm_w) + ks_wg * 32 + 8 * vr),
+                       s_rstd[m]);
+          *reinterpret_cast<uint4 *>(s_x + (size_t)m * xstride + 8 * vr) = xv;
+        }
+      }
+    __syncthreads();
+    staged = true;
+  } else {
+    issue_first();
+    if constexpr (NORM) {
+      // Whole-row statistics, same per-thread vector assignment and order.
+      const int nvec = p.k >> 3;
+      for (int m0 = 0; m0 < rows; m0 += 8) {
+        float ss[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss[j] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int m = m0 + j;
+          if (m < rows) {
+            const uint16_t *xrow = X + (size_t)m * p.k;
+            for (int v = tid; v < nvec; v += nthr) {
+              float f[8];
+              unpack8(*reinterpret_cast<const uint4 *>(xrow + 8 * v), f);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) ss[j] += f[e] * f[e];
+            }
+          }
+        }
+        block_row_sums(ss, s_red, rows - m0, s_rstd, m0, p.k, p.eps);
+      }
+    }
+    if (p.lds_all) {
+      // The whole k range of the workgroup fits in LDS: stage it once.
+      const int per_row = nw * p.ksw * 4;  // 16-byte vectors per row
+      const int tot = rows * per_row;
+      for (int v = tid; v < tot; v += nthr) {
+        const int m = v / per_row;
+        const int vr = v - m * per_row;
+        const int kg = ks_wg * 32 + 8 * vr;
+        uint4 xv = *reinterpret_cast<const uint4 *>(X + (size_t)m * p.k + kg);
+        if constexpr (NORM)
+          xv = norm8(xv, *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p.norm_w) + kg), s_rstd[m]);
+        *reinterpret_cast<uint4 *>(s_x + (size_t)m * xstride + 8 * vr) = xv;
+      }
+      __syncthreads();
+      staged = true;
+    }
+  }
+
+  // ARGMAX running best per M tile (lane-local, rows = mt*16 + col).
+  float best_v[MT];
+  int best_i[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    best_v[mt] = -__builtin_huge_valf();
+    best_i[mt] = 0x7fffffff;
+  }
+
+  bool have_w = true;  // wb holds the next pass's weights already (pass path)
+  for (int tt = 0; tt < p.tiles_per_wg; ++tt) {
+    const int tile = tile0 + tt;
+    f32x4_t acc[NACC][MT];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[a][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    if constexpr (WIN) {
+      // B operand rows: lane col < rows reads its row, the others read row 0
+      // and use zeros.
+      const bool xrow_ok = col < rows;
+      const uint16_t *xs = s_x + (size_t)(xrow_ok ? col : 0) * xstride + wave * p.ksw * 32 + grp * 8;
+      // Refills: k step i0 + r + RW of this tile while it exists, then the
+      // same offset into the next tile; none past the wave's last tile.
+      const bool more_tiles = tt + 1 < p.tiles_per_wg;
+      for (int i0 = 0; i0 < p.ksw; i0 += RW) {
+        const bool same_tile = i0 + RW < p.ksw;
+        const bool refill = same_tile || more_tiles;
+        const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + 1, i0 + RW - p.ksw);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const uint4 bx = *reinterpret_cast<const uint4 *>(xs + (i0 + r) * 32);
+          const uint4 b = xrow_ok ? bx : zero4();
+#pragma unroll
+          for (int a = 0; a < NACC; ++a) acc[a][0] = mfma16x16x32(wb[a][r], b, acc[a][0]);
+          if (refill) {
+            wb[0][r] = qn[r * 64];
+            if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
+          }
+        }
+      }
+    } else {
+      for (int pass = 0; pass < p.npass; ++pass) {
+        const int kbeg = pass * p.kp;
+        const int kcnt = min(p.kp, p.ksw - kbeg);
+        if (!have_w) issue_pass(tile, kbeg, kcnt);
+        have_w = false;
+        if (!staged) {
+          if (pass > 0 || tt > 0) __syncthreads();  // previous readers are done
+          const int per_row = nw * kcnt * 4;        // 16-byte vectors per row in this pass
+          const int tot = rows * per_row;
+          for (int v = tid; v < tot; v += nthr) {
+            const int m = v / per_row;
+            int r = v - m * per_row;
+            const int w2 = r / (kcnt * 4);
+            r -= w2 * (kcnt * 4);
+            const int i = r >> 2;
+            const int q = r & 3;
+            const int kg = (ks_wg + w2 * p.ksw + kbeg + i) * 32 + q * 8;
+            uint4 xv = *reinterpret_cast<const uint4 *>(X + (size_t)m * p.k + kg);
+            if constexpr (NORM)
+              xv = norm8(xv, *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p.norm_w) + kg),
+                         s_rstd[m]);
+            *reinterpret_cast<uint4 *>(s_x + (size_t)m * xstride + (w2 * p.kp + i) * 32 + q * 8) = xv;
+          }
+          __syncthreads();
+          staged = p.npass == 1;  // several passes restage per pass
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+          if (i < kcnt) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const int m = mt * 16 + col;
+              uint4 b = zero4();
+              if (m < rows)
+                b = *reinterpret_cast<const uint4 *>(s_x + (size_t)m * xstride +
+                                                     (wave * lds_steps + (p.lds_all ? kbeg : 0) + i) * 32 + grp * 8);
+#pragma unroll
+              for (int a = 0; a < NACC; ++a) acc[a][mt] = mfma16x16x32(wb[a][i], b, acc[a][mt]);
+            }
+          }
+        }
+      }
+      // Request the next tile's weights before this tile's epilogue.
+      if (p.npass == 1 && tt + 1 < p.tiles_per_wg) {
+        issue_pass(tile + 1, 0, min(p.kp, p.ksw));
+        have_w = true;
+      }
+    }
+
+    // ---- merge the waves of the workgroup in wave order.
+    if (nw > 1) {
+      __syncthreads();
+      float4 *red = reinterpret_cast<float4 *>(smem + p.lds_red_off);
+      if (wave > 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            red[(((wave - 1) * NACC + a) * MT + mt) * 64 + lane] =
+                make_float4(acc[a][mt][0], acc[a][mt][1], acc[a][mt][2], acc[a][mt][3]);
+      }
+      __syncthreads();
+      if (wave == 0) {
+        for (int w2 = 1; w2 < nw; ++w2) {
+#pragma unroll
+          for (int a = 0; a < NACC; ++a)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const float4 r = red[(((w2 - 1) * NACC + a) * MT + mt) * 64 + lane];
+              acc[a][mt][0] += r.x;
+              acc[a][mt][1] += r.y;
+              acc[a][mt][2] += r.z;
+              acc[a][mt][3] += r.w;
+            }
+        }
+      }
+    }
+
+    const int n0 = tile * 16 + grp * 4;  // first of this lane's 4 output columns
+
+    // ---- k split across workgroups: partials, last arrival sums them.
+    if (p.ksplit > 1) {
+      if (wave == 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + col;
+            if (m < rows) store_coherent4(p.partial + ((size_t)(a * p.ksplit + split) * rows + m) * p.n + n0, acc[a][mt]);
+          }
+      }
+      if (!arrive_last(p.counters + tile, (uint32_t)p.ksplit, s_flag)) return;
+      if (wave == 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + col;
+            if (m < rows) {
+              f32x4_t t = load_coherent4(p.partial + ((size_t)(a * p.ksplit) * rows + m) * p.n + n0);
+              for (int s = 1; s < p.ksplit; ++s)
+                t += load_coherent4(p.partial + ((size_t)(a * p.ksplit + s) * rows + m) * p.n + n0);
+              acc[a][mt] = t;
+            }
+          }
+      }
+    }
+
+    // ---- epilogues (wave 0 holds the finished tile).
+    if (wave == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + col;
+        if (m >= rows) continue;
+        if constexpr (ARG) {
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = rbf(acc[0][mt][i]);
+          if (p.out) {
+            uint2 o;
+            o.x = pack2(v[0], v[1]);
+            o.y = pack2(v[2], v[3]);
+            *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (v[i] > best_v[mt]) {
+              best_v[mt] = v[i];
+              best_i[mt] = n0 + i;
+            }
+        } else if constexpr (RES) {
+          uint16_t *rp = reinterpret_cast<uint16_t *>(p.res) + (size_t)m * p.n + n0;
+          const uint2 r = *reinterpret_cast<const uint2 *>(rp);
+          uint2 o;
+          o.x = pack2(lo16(r.x) + rbf(acc[0][mt][0]), hi16(r.x) + rbf(acc[0][mt][1]));
+          o.y = pack2(lo16(r.y) + rbf(acc[0][mt][2]), hi16(r.y) + rbf(acc[0][mt][3]));
+          *reinterpret_cast<uint2 *>(rp) = o;
+        } else if constexpr (GLU) {
+          float o4[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float g = rbf(acc[0][mt][i]);
+            const float u = rbf(acc[1][mt][i]);
+            const float s = rbf(g / (1.0f + expf(-g)));
+            o4[i] = s * u;
+          }
+          uint2 o;
+          o.x = pack2(o4[0], o4[1]);
+          o.y = pack2(o4[2], o4[3]);
+          *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+        } else {
+          uint2 o;
+          o.x = pack2(acc[0][mt][0], acc[0][mt][1]);
+          o.y = pack2(acc[0][mt][2], acc[0][mt][3]);
+          *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+        }
+      }
+    }
+  }
+
+  if constexpr (ARG) {
+    // Reduce the 4 column groups of each row, lowest index on equal values.
+    float *pv = p.partial;                                          // [G][rows]
+    int *pi = reinterpret_cast<int *>(p.partial + (size_t)nblk * rows);  // [G][rows]
+    if (wave == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1) {
+          const float ov = shfl_xor(best_v[mt], off);
+          const int oi = __shfl_xor(best_i[mt], off, kWave);
+          if (ov > best_v[mt] || (ov == best_v[mt] && oi < best_i[mt])) {
+            best_v[mt] = ov;
+            best_i[mt] = oi;
+          }
+        }
+        const int m = mt * 16 + col;
+        if (grp == 0 && m < rows) {
+          store_coherent(pv + (size_t)blk * rows + m, best_v[mt]);
+          store_coherent_i(pi + (size_t)blk * rows + m, best_i[mt]);
+        }
+      }
+    }
+    if (!arrive_last(p.counters, (uint32_t)nblk, s_flag)) return;
+    float *sv = s_red;                             // [waves]
+    int *si = reinterpret_cast<int *>(s_red + 8);  // [waves]
+    for (int m = 0; m < rows; ++m) {
+      float bv = -__builtin_huge_valf();
+      int bi = 0x7fffffff;
+      for (int g = tid; g < nblk; g += nthr) {
+        const float v = load_coherent(pv + (size_t)g * rows + m);
+        const int i = load_coherent_i(pi + (size_t)g * rows + m);
+        if (v > bv || (v == bv && i < bi)) {
+          bv = v;
+          bi = i;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = shfl_xor(bv, off);
+        const int oi = __shfl_xor(bi, off, kWave);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        for (int w2 = 1; w2 < nw; ++w2)
+          if (sv[w2] > bv || (sv[w2] == bv && si[w2] < bi)) {
+            bv = sv[w2];
+            bi = si[w2];
+          }
+        p.ids_out[m] = (int64_t)bi;
+        if (p.lens_inc) p.lens_inc[m] += 1;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+template <int MT, int RW>
+hipError_t launch_flags(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  switch (flags) {
+    case 0u: hipLaunchKernelGGL((gemm_kernel<MT, 0u, RW>), grid, block, lds, s, p); break;
+    case QDEC_NORM_IN: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN, RW>), grid, block, lds, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT, RW>), grid, block, lds, s, p); break;
+    case QDEC_NORM_IN | QDEC_ARGMAX:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_ARGMAX, RW>), grid, block, lds, s, p);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipSuccess;
 }
 
 template <int MT>
-hipError_t launch_mt(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds,
-                     hipStream_t s) {
-  switch (flags) {
-    case 0:
-      hipLaunchKernelGGL((gemm_kernel<MT, 0u>), grid, block, lds, s, p);
-      break;
-    case QDEC_NORM_IN:
-      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN>), grid, block, lds, s, p);
-      break;
-    case QDEC_NORM_IN | QDEC_GLU:
-      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_GLU>), grid, block, lds, s, p);
-      break;
-    case QDEC_RES_OUT:
-      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT>), grid, block, lds, s, p);
-      break;
-    case QDEC_NORM_IN | QDEC_ARGMAX:
-      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_ARGMAX>), grid, block, lds, s, p);
-      break;
-    default:
-      return hipErrorInvalidValue;
+hipError_t launch_pass(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  if (flags == (QDEC_NORM_IN | QDEC_GLU)) {
+    hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_GLU, 0>), grid, block, lds, s, p);
+    return hipSuccess;
   }
-  return hipSuccess;
+  return launch_flags<MT, 0>(p, flags, grid, block, lds, s);
 }
 
 }  // namespace
 
 bool gemm_flags_supported(uint32_t flags) {
-  return flags == 0u || flags == QDEC_NORM_IN || flags == (QDEC_NORM_IN | QDEC_GLU) ||
-         flags == QDEC_RES_OUT || flags == (QDEC_NORM_IN | QDEC_ARGMAX);
+  return flags == 0u || flags == QDEC_NORM_IN || flags == (QDEC_NORM_IN | QDEC_GLU) || flags == QDEC_RES_OUT ||
+         flags == (QDEC_NORM_IN | QDEC_ARGMAX);
 }
 
 bool gemm_fast_path(const GemmParams &p, uint32_t flags) {
@@ -78,17 +546,40 @@ bool gemm_fast_path(const GemmParams &p, uint32_t flags) {
          (!(flags & QDEC_NORM_IN) || p.ksplit == 1);
 }
 
+int gemm_window(const GemmParams &p, uint32_t flags) {
+  if (!p.lds_all || p.rows > 16) return 0;
+  if (flags & QDEC_GLU) return p.ksw % 10 == 0 ? 10 : 0;
+  // 20 and 16 measured faster than passes on MI355X; a 19-register ring
+  // (k = 9728 with 4 waves) was slower than 20-block passes.
+  for (const int rw : {20, 16})
+    if (p.ksw % rw == 0) return rw;
+  return 0;
+}
+
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   const int mt = (p.rows + 15) / 16;
   const int ntiles = p.n / 16;
   dim3 grid((ntiles / p.tiles_per_wg) * p.ksplit);
   dim3 block(64 * p.waves);
   const size_t lds = p.lds_bytes;
+  if (p.rw > 0) {
+    if (mt != 1) return hipErrorInvalidValue;
+    if (flags == (QDEC_NORM_IN | QDEC_GLU)) {
+      if (p.rw != 10) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_GLU, 10>), grid, block, lds, s, p);
+      return hipSuccess;
+    }
+    switch (p.rw) {
+      case 16: return launch_flags<1, 16>(p, flags, grid, block, lds, s);
+      case 20: return launch_flags<1, 20>(p, flags, grid, block, lds, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (mt) {
-    case 1: return launch_mt<1>(p, flags, grid, block, lds, s);
-    case 2: return launch_mt<2>(p, flags, grid, block, lds, s);
-    case 3: return launch_mt<3>(p, flags, grid, block, lds, s);
-    case 4: return launch_mt<4>(p, flags, grid, block, lds, s);
+    case 1: return launch_pass<1>(p, flags, grid, block, lds, s);
+    case 2: return launch_pass<2>(p, flags, grid, block, lds, s);
+    case 3: return launch_pass<3>(p, flags, grid, block, lds, s);
+    case 4: return launch_pass<4>(p, flags, grid, block, lds, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -69,66 +69,24 @@ __device__ __forceinline__ float load_coherent(const float *p) {
 __device__ __forceinline__ void store_coherent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Activation accesses, parameterised on coherence.  Inside one launch of the
-// persistent step kernel (step.hip) activations pass between workgroups on
-// different XCDs, whose L2s are not coherent with each other: there every
-// activation store and load is a device-scope access, performed at the
-// device's point of coherence (COH = true).  Separate kernel launches get
-// coherence from the launch boundaries (COH = false).  Device-scope 64-bit
-// relaxed atomics compile to plain global_load/store_dwordx2 with the sc1
-// (device scope) cache policy, so they pipeline like ordinary loads.
+// Device-scope 64-bit relaxed atomics compile to plain global_load/store_dwordx2
+// with the device-scope cache policy, so they pipeline like ordinary loads.
 __device__ __forceinline__ uint64_t ld64_dev(const void *p) {
   return __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st64_dev(void *p, uint64_t v) {
   __hip_atomic_store(reinterpret_cast<uint64_t *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-template <bool COH>
-__device__ __forceinline__ uint4 ld16(const void *p) {
-  if constexpr (COH) {
-    const uint64_t a = ld64_dev(p), b = ld64_dev(reinterpret_cast<const uint64_t *>(p) + 1);
-    return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
-  } else {
-    return *reinterpret_cast<const uint4 *>(p);
-  }
-}
-template <bool COH>
-__device__ __forceinline__ uint2 ld8(const void *p) {
-  if constexpr (COH) {
-    const uint64_t a = ld64_dev(p);
-    return make_uint2((uint32_t)a, (uint32_t)(a >> 32));
-  } else {
-    return *reinterpret_cast<const uint2 *>(p);
-  }
-}
-template <bool COH>
-__device__ __forceinline__ uint32_t ld4(const void *p) {
-  if constexpr (COH) return __hip_atomic_load(reinterpret_cast<const uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else return *reinterpret_cast<const uint32_t *>(p);
-}
-template <bool COH>
-__device__ __forceinline__ void st8(void *p, uint2 v) {
-  if constexpr (COH) st64_dev(p, (uint64_t)v.x | ((uint64_t)v.y << 32));
-  else *reinterpret_cast<uint2 *>(p) = v;
-}
-template <bool COH>
-__device__ __forceinline__ void st16(void *p, uint4 v) {
-  if constexpr (COH) {
-    st64_dev(p, (uint64_t)v.x | ((uint64_t)v.y << 32));
-    st64_dev(reinterpret_cast<uint64_t *>(p) + 1, (uint64_t)v.z | ((uint64_t)v.w << 32));
-  } else {
-    *reinterpret_cast<uint4 *>(p) = v;
-  }
-}
 
 // 16-byte fp32 partials handed between workgroups (device scope).
 __device__ __forceinline__ f32x4_t load_coherent4(const float *p) {
-  const uint4 v = ld16<true>(p);
-  return f32x4_t{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+  const uint64_t a = ld64_dev(p), b = ld64_dev(p + 2);
+  return f32x4_t{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+                 __uint_as_float((uint32_t)(b >> 32))};
 }
 __device__ __forceinline__ void store_coherent4(float *p, f32x4_t v) {
-  st16<true>(p, make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
-                           __float_as_uint(v[3])));
+  st64_dev(p, (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32));
+  st64_dev(p + 2, (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32));
 }
 __device__ __forceinline__ int load_coherent_i(const int *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -34,10 +34,12 @@ struct GemmParams {
   int lds_red_off, lds_x_off;
   int xfast;     // activations staged from registers (see gemm.hip)
   int lds_all;   // the workgroup's whole k range of x is staged in LDS once
+  int rw;        // weight ring registers per wave (window path), 0 = passes
   size_t lds_bytes;
 };
 bool gemm_flags_supported(uint32_t flags);
 bool gemm_fast_path(const GemmParams &p, uint32_t flags);
+int gemm_window(const GemmParams &p, uint32_t flags);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 
 struct AttnParams {
@@ -63,32 +65,6 @@ hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 // partials 4 x 8 x 64 f32x4, wave maxima and sums 2 x 4 x 16 f32, a flag.
 constexpr int kAttnLds = 16 * 136 * 2 + 3 * 128 * 8 * 2 + 4 * 8 * 64 * 16 + 2 * 4 * 16 * 4 + 16;
 
-// Persistent step kernel (step.hip): a table of phases in device memory.
-constexpr int kPhaseEmbed = 0;
-constexpr int kPhaseGemm = 1;
-constexpr int kPhaseAttn = 2;
-struct StepEmbed {
-  const int64_t *ids;
-  const void *emb;
-  void *h;
-  int rows, hidden, vocab;
-};
-struct StepPhase {
-  int kind;
-  uint32_t flags;  // gemm flags
-  int nblk;        // blocks of the phase
-  int rows;        // gemm rows / attention query rows per sequence (guard)
-  GemmParams g;
-  AttnParams a;
-  StepEmbed e;
-};
-struct StepCtl {
-  uint64_t ticket;  // arrivals at grid barriers since the buffer was zeroed
-  uint32_t err;     // nonzero: a barrier wait timed out (results are invalid)
-  uint32_t pad;
-};
-hipError_t launch_step(const StepPhase *phases, int nphases, StepCtl *ctl, uint32_t spin_limit, int mt,
-                       int mtq, int nwg, size_t lds, uint64_t *trace, hipStream_t s);
 
 hipError_t launch_embed(const int64_t *ids, const void *emb, void *h, int rows, int hidden,
                         int vocab, hipStream_t s);

@@ -14,10 +14,6 @@ Public surface (the reference's engine/engine.py:215-241, 1024-1063):
   the O projection with the residual add, gate/up with the post-attention
   norm and SwiGLU, down with the residual add; the tied lm_head with the
   final norm and the greedy argmax.  5 launches per layer, 182 per step.
-* By default the whole step is ONE launch of the persistent step kernel (one
-  workgroup per CU walking the same 182 operations, with grid barriers and
-  cross-operation weight prefetch; bit-identical to the launch-per-op path,
-  ``step_kernel=False``).
 * A step reads its token ids and cache lengths from device buffers and writes
   the next ids and lengths itself, so it is captured once per shape as a
   hipGraph and replayed; up to LOOKAHEAD replays are queued ahead of the
@@ -74,40 +70,37 @@ class _Shape:
         self.state = DecodeState(engine.model, batch, self.capacity, max_t=max_t)
         self.graph = None
         self.spec_graph = None
-        self.state.use_step_kernel = engine.step_kernel
         self.host = torch.empty((new_tokens, batch), dtype=torch.int64, pin_memory=True)
-        self.host_err = torch.zeros((new_tokens,), dtype=torch.int32, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(new_tokens)]
 
 
 class Engine:
-    def __init__(self, model_path: str, speculate: bool = False, step_kernel: bool = False) -> None:
+    def __init__(self, model_path: str, speculate: bool = False) -> None:
         """Load the checkpoint at ``model_path`` (HF layout, local files only)."""
         start = time.perf_counter()
         if not torch.cuda.is_available():
             raise RuntimeError("Engine needs a HIP device (torch.cuda.is_available() is False)")
         cfg = load_config(model_path)
         tensors = load_tensors(model_path)
-        self._setup(cfg, tensors, speculate, step_kernel=step_kernel)
+        self._setup(cfg, tensors, speculate)
         del tensors
         _log(f"engine ready in {time.perf_counter() - start:.1f}s "
              f"({self.model.weight_bytes() / 1e9:.2f} GB of packed weights)")
 
     @classmethod
-    def from_tensors(cls, cfg, tensors, speculate=False, use_graphs=True, step_kernel=False):
+    def from_tensors(cls, cfg, tensors, speculate=False, use_graphs=True):
         """Build around in-memory HF-named tensors (tests)."""
         self = cls.__new__(cls)
-        self._setup(cfg, tensors, speculate, use_graphs, step_kernel)
+        self._setup(cfg, tensors, speculate, use_graphs)
         return self
 
-    def _setup(self, cfg, tensors, speculate, use_graphs=True, step_kernel=False):
+    def _setup(self, cfg, tensors, speculate, use_graphs=True):
         self.device = torch.device("cuda:0")
         torch.cuda.set_device(self.device)
         self.lib = capi.lib()
         self.model = DeviceModel(cfg, tensors, self.device)
         self.speculate = bool(speculate)
         self.use_graphs = use_graphs
-        self.step_kernel = bool(step_kernel)
         self.shape = None
         self.stats = {}
 
@@ -125,7 +118,6 @@ class Engine:
         self.shape = sh
         _log(f"shape B={batch} S={prompt_len} N={new_tokens}: capacity {sh.state.cap}, "
              f"attention chunk {sh.state.chunk}, graph={'yes' if sh.graph else 'no'}, "
-             f"step={'persistent' if self.step_kernel else 'per-op launches'}, "
              f"setup {time.perf_counter() - start:.2f}s")
         return sh
 
@@ -153,13 +145,10 @@ class Engine:
 
     def _publish(self, sh, step):
         sh.host[step].copy_(sh.state.ids[:sh.batch], non_blocking=True)
-        sh.host_err[step:step + 1].copy_(sh.state.step_ctl[2:3], non_blocking=True)
         sh.events[step].record()
 
     def _fetch(self, sh, step):
         sh.events[step].synchronize()
-        if int(sh.host_err[step]) != 0:
-            raise RuntimeError("step kernel barrier timed out; the decode results are invalid")
         return sh.host[step].tolist()
 
     def generate(self, input_ids: list[list[int]], max_new_tokens: int):

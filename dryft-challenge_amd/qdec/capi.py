@@ -48,12 +48,6 @@ class AttnArgs(ctypes.Structure):
                 ("waves", I32)]
 
 
-class StepArgs(ctypes.Structure):
-    _fields_ = [("phases", P), ("nphases", I32), ("spin_limit", ctypes.c_uint32), ("ctl", P),
-                ("max_rows", I32), ("t_rows", I32), ("lds_bytes", I32), ("workgroups", I32),
-                ("trace", P)]
-
-
 class DraftArgs(ctypes.Structure):
     _fields_ = [("hist", P), ("lens", P), ("ids", P), ("draft", P), ("batch", I32), ("cap", I32),
                 ("primary", I32), ("backoff", I32), ("k", I32)]
@@ -94,16 +88,6 @@ class Lib:
             fn = getattr(so, name)
             fn.argtypes = [ctypes.POINTER(st), P]
             fn.restype = ctypes.c_int
-        so.qdec_step_phase_bytes.restype = ctypes.c_size_t
-        so.qdec_step_workgroups.restype = ctypes.c_int
-        so.qdec_step_encode_embed.argtypes = [ctypes.POINTER(EmbedArgs), P]
-        so.qdec_step_encode_embed.restype = ctypes.c_int
-        for name, st in (("qdec_step_encode_gemm", GemmArgs), ("qdec_step_encode_attn", AttnArgs)):
-            fn = getattr(so, name)
-            fn.argtypes = [ctypes.POINTER(st), P, ctypes.POINTER(ctypes.c_size_t)]
-            fn.restype = ctypes.c_int
-        so.qdec_step_run.argtypes = [ctypes.POINTER(StepArgs), P]
-        so.qdec_step_run.restype = ctypes.c_int
         for name, st in (("qdec_gemm_workspace", GemmArgs), ("qdec_attn_workspace", AttnArgs)):
             fn = getattr(so, name)
             fn.argtypes = [ctypes.POINTER(st), ctypes.POINTER(ctypes.c_size_t),
@@ -143,30 +127,6 @@ class Lib:
 
     def spec_accept(self, args, stream):
         self._check("qdec_spec_accept", self.so.qdec_spec_accept(ctypes.byref(args), stream))
-
-    def step_phase_bytes(self):
-        return self.so.qdec_step_phase_bytes()
-
-    def step_workgroups(self):
-        return self.so.qdec_step_workgroups()
-
-    def step_encode_embed(self, args, buf):
-        self._check("qdec_step_encode_embed", self.so.qdec_step_encode_embed(ctypes.byref(args), buf))
-
-    def step_encode_gemm(self, args, buf):
-        lds = ctypes.c_size_t()
-        self._check("qdec_step_encode_gemm",
-                    self.so.qdec_step_encode_gemm(ctypes.byref(args), buf, ctypes.byref(lds)))
-        return lds.value
-
-    def step_encode_attn(self, args, buf):
-        lds = ctypes.c_size_t()
-        self._check("qdec_step_encode_attn",
-                    self.so.qdec_step_encode_attn(ctypes.byref(args), buf, ctypes.byref(lds)))
-        return lds.value
-
-    def step_run(self, args, stream):
-        self._check("qdec_step_run", self.so.qdec_step_run(ctypes.byref(args), stream))
 
     def gemm_workspace(self, args):
         pb, cb = ctypes.c_size_t(), ctypes.c_size_t()

@@ -113,14 +113,19 @@ def role_plan(n, k, role):
 
 def attn_chunk(batch, nkv, cap):
     """Slots per attention workgroup (a multiple of 32; absolute-slot
-    chunking).  Measured on MI355X with 4-wave workgroups: once batch x kv
-    heads fills half the CUs one chunk per sequence is fastest (no merge);
-    below that, 512-slot chunks (256 at batch 1) trade the cross-workgroup
-    merge against parallelism."""
+    chunking).  Measured on MI355X with 4-wave workgroups (graph-replayed,
+    36 layers): once batch x kv heads fills half the CUs one chunk per
+    sequence is fastest (no merge); below that, smaller chunks trade the
+    cross-workgroup merge against parallelism -- 512 slots at batch 8, 256 at
+    batch 2..7 and at batch 1 with long caches, 128 at batch 1 up to 1024
+    slots (10.4 us vs 12.0 us at 256 for 640 cached slots; 21.5 vs 17.1 us
+    at 4000)."""
     cap = round_up(cap, 32)
     if batch * nkv >= 128:
         return cap
-    return min(cap, 512 if batch >= 4 else 256)
+    if batch >= 8:
+        return min(cap, 512)
+    return min(cap, 128 if batch == 1 and cap <= 1024 else 256)
 
 
 class DeviceModel:
@@ -232,10 +237,6 @@ class DecodeState:
         self.attn_counters = torch.zeros((max(ac, 4) // 4 + 4,), dtype=torch.int32, device=dev)
         self._gemm_cache = {}
         self._attn_cache = {}
-        # persistent step kernel: barrier state + cached phase tables
-        self.step_ctl = torch.zeros((4,), dtype=torch.int32, device=dev)
-        self._tables = {}
-        self.use_step_kernel = True
 
     # ----------------------------------------------------------- arguments
     def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None):
@@ -332,68 +333,9 @@ class DecodeState:
             self._attn_cache[key] = a
         return a
 
-    # ---------------------------------------------- persistent step kernel
-    def _step_table(self, t_rows, lm_head, ids_out, advance):
-        """Phase table of one forward (the same calls run_step issues) in
-        device memory, cached per shape of the call."""
-        key = (t_rows, lm_head, None if ids_out is None else ids_out.data_ptr(), advance)
-        tab = self._tables.get(key)
-        if tab is not None:
-            return tab
-        import ctypes
-        lib, m, c = self.lib, self.model, self.model.cfg
-        rows = self.batch * t_rows
-        pb = lib.step_phase_bytes()
-        nph = 1 + 5 * c.n_layers + (1 if lm_head else 0)
-        host = (ctypes.c_ubyte * (pb * nph))()
-        base = ctypes.addressof(host)
-        lds = 0
-        e = capi.EmbedArgs()
-        e.ids, e.emb, e.h = self.ids.data_ptr(), m.emb.data_ptr(), self.h.data_ptr()
-        e.rows, e.hidden, e.vocab = rows, c.hidden, c.vocab
-        lib.step_encode_embed(e, base)
-        i = 1
-        for layer in range(c.n_layers):
-            for role in ("qkv", None, "o", "gate_up", "down"):
-                if role is None:
-                    lds = max(lds, lib.step_encode_attn(self._cached_attn(layer, t_rows), base + i * pb))
-                else:
-                    lds = max(lds, lib.step_encode_gemm(self._cached_gemm(role, layer, rows), base + i * pb))
-                i += 1
-        if lm_head:
-            a = self._gemm_args("lm", 0, rows, ids_out=ids_out,
-                                lens_inc=self.lens if (advance and t_rows == 1) else None)
-            lds = max(lds, lib.step_encode_gemm(a, base + i * pb))
-            i += 1
-        dev_tab = torch.frombuffer(bytearray(host), dtype=torch.uint8).to(self.model.device)
-        args = capi.StepArgs()
-        args.phases, args.nphases, args.spin_limit = dev_tab.data_ptr(), nph, 0
-        args.ctl = self.step_ctl.data_ptr()
-        args.max_rows, args.t_rows, args.lds_bytes, args.workgroups = rows, t_rows, lds, 0
-        tab = (dev_tab, args)
-        self._tables[key] = tab
-        return tab
-
-    def run_step_persistent(self, t_rows=1, lm_head=True, ids_out=None, advance=True, stream=None):
-        """``run_step`` as one launch of the persistent step kernel (same
-        phases, same per-block code, bit-identical results)."""
-        if t_rows < 1 or t_rows > self.max_t:
-            raise ValueError(f"t_rows {t_rows} not in [1, {self.max_t}]")
-        if advance and lm_head and t_rows != 1:
-            raise ValueError("advance needs t_rows == 1")
-        _, args = self._step_table(t_rows, lm_head, ids_out, advance)
-        s = (stream or torch.cuda.current_stream(self.model.device)).cuda_stream
-        self.lib.step_run(args, s)
-
     def step(self, t_rows=1, lm_head=True, ids_out=None, advance=True, stream=None):
-        """One forward through the persistent step kernel or the per-op
-        launches (``use_step_kernel``); the two give identical bits."""
-        fn = self.run_step_persistent if self.use_step_kernel else self.run_step
-        fn(t_rows=t_rows, lm_head=lm_head, ids_out=ids_out, advance=advance, stream=stream)
-
-    def step_error(self):
-        """Error word of the step kernel's barrier (0 = fine)."""
-        return int(self.step_ctl[2].item())
+        """One forward (``run_step``); the name every caller captures."""
+        self.run_step(t_rows=t_rows, lm_head=lm_head, ids_out=ids_out, advance=advance, stream=stream)
 
     # ------------------------------------------------------------- prefill
     def prefill(self, prompt, stream=None):

@@ -188,49 +188,6 @@ int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream);
 int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,
                         size_t *counter_bytes);
 
-/* ------------------------------------------- persistent step kernel */
-
-/* A whole forward as ONE launch: one workgroup per CU walks a table of
- * phases (embed, each projection, each attention, lm_head + argmax).  Each
- * phase runs the same per-block code as the standalone entry point it was
- * encoded from, so the results are bit-identical to issuing those calls one
- * by one; between phases the workgroups meet at a grid barrier, and each
- * issues the weight loads of its next block before it waits.
- *
- * Build the table on the host: every phase is qdec_step_phase_bytes() bytes,
- * written by one qdec_step_encode_* call from the same argument struct the
- * standalone call would take (gemm and attention calls must use waves == 4,
- * the step kernel's workgroup size).  Copy the table to device memory once;
- * per-step values (ids, lens) stay device pointers inside it, so the launch
- * can be captured and replayed.  `ctl` is 16 bytes of zeroed device memory
- * (64-bit barrier ticket, error word), reused across launches of one grid
- * size.  If a barrier wait exceeds `spin_limit` polls the kernel records 1 in
- * the error word (uint32 at ctl + 8), stops waiting and runs to the end; the
- * results of that launch are invalid and the caller must check the word (and
- * re-zero ctl before reusing it).
- * Replaces the per-step launch graph of engine/engine.py:517-546 and the
- * disabled one-launch layer kernel of engine/kernels/layer.py:46-285. */
-typedef struct {
-  const void *phases;  /* device copy of the phase table */
-  int32_t nphases;
-  uint32_t spin_limit; /* barrier polls before giving up; 0 = 1 << 22 */
-  void *ctl;           /* 16 zeroed bytes of device memory */
-  int32_t max_rows;    /* largest gemm row count in the table (1..64) */
-  int32_t t_rows;      /* attention query rows per sequence (1..16) */
-  int32_t lds_bytes;   /* largest LDS size reported by the encode calls */
-  int32_t workgroups;  /* 0 = one per CU of the current device */
-  void *trace;         /* NULL, or uint64[workgroups][nphases][2]: device
-                          real-time clock (100 MHz) at each phase's start and
-                          at its barrier arrival, for profiling */
-} qdec_step_args;
-size_t qdec_step_phase_bytes(void);
-int qdec_step_encode_embed(const qdec_embed_args *a, void *phase);
-int qdec_step_encode_gemm(const qdec_gemm_args *a, void *phase, size_t *lds_bytes);
-int qdec_step_encode_attn(const qdec_attn_args *a, void *phase, size_t *lds_bytes);
-int qdec_step_run(const qdec_step_args *a, qdec_stream_t stream);
-/* Compute units of the current device (0 without a device). */
-int qdec_step_workgroups(void);
-
 /* ------------------------------------------------ n-gram speculation */
 
 /* Suffix-match drafter over each sequence's own history hist[b, 0..lens[b]]

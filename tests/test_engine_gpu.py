@@ -133,26 +133,3 @@ def test_speculative_equals_plain_greedy(ckpt, engine):
         print(f"spec B={B} S={S} n={n}: {stats}")
         assert stats["iterations"] <= n - 1
 
-
-def test_step_kernel_matches_launch_path(engine):
-    """One persistent launch per step reproduces the 182-launch step bit for
-    bit (same per-block code and plans), and its barrier reports no error."""
-    from qdec.runtime import DecodeState
-    B, S, n = 2, 40, 8
-    prompt = prompts(B, S, 11).to(engine.device)
-    out = []
-    for persistent in (False, True):
-        st = DecodeState(engine.model, B, S + n + 18, max_t=16, keep_logits=True)
-        st.prefill(prompt)
-        logits, ids = [], []
-        for _ in range(n):
-            (st.run_step_persistent if persistent else st.run_step)(t_rows=1)
-            logits.append(st.logits[:B].clone())
-            ids.append(st.ids[:B].clone())
-        torch.cuda.synchronize()
-        if persistent:
-            assert st.step_error() == 0
-        out.append((torch.stack(logits).cpu(), torch.stack(ids).cpu(), st.lens.cpu()))
-    (l0, i0, n0), (l1, i1, n1) = out
-    assert torch.equal(i0, i1) and torch.equal(n0, n1)
-    assert torch.equal(l0.view(torch.int16), l1.view(torch.int16))
