@@ -19,7 +19,13 @@ Printed JSON fields beyond the driver contract:
                 with HIP events on the engine's stream;
   cpu_baseline  the Transformers CPU greedy loop on the same checkpoint
                 (the reference's own oracle path), on a bounded sample;
-  step_hbm      algorithmic bytes per step (weights + KV read/write) / step time.
+  step_hbm      algorithmic bytes per step (weights + KV read/write) / step time;
+  speculation   BASELINE.json configs[4] through the same engine: batch 4,
+                1024-token prompts tiling a seeded 64-token motif with 10%
+                random substitutions, 512 new tokens, n-gram drafter (n=3,
+                backoff 2, up to 8 drafts); plain and speculative generate()
+                timed from the first emitted token to the last, tokens
+                compared for identity (skip with --no-spec).
 """
 
 import argparse
@@ -75,6 +81,59 @@ def time_gemm_role(engine, state, role, reps=5):
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / 1e3 / (reps * len(args))
+
+
+def motif_prompts(batch, length, vocab, seed, motif=64, subst=0.10):
+    """Each sequence tiles its own seeded random ``motif``-token pattern to
+    ``length`` tokens, then replaces a ``subst`` fraction of positions with
+    uniform random tokens."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(batch):
+        pat = torch.randint(0, vocab, (motif,), generator=g)
+        seq = pat.repeat((length + motif - 1) // motif)[:length].clone()
+        mask = torch.rand(length, generator=g) < subst
+        seq[mask] = torch.randint(0, vocab, (int(mask.sum()),), generator=g)
+        out.append(seq.tolist())
+    return out
+
+
+def spec_bench(eng, vocab, batch=4, prompt_len=1024, new_tokens=512, seed=5):
+    """Plain vs speculative greedy decode of the same prompts (decode phase
+    only: first emitted token to last), and whether the tokens agree."""
+    import torch
+    prompts = motif_prompts(batch, prompt_len, vocab, seed)
+    res = {}
+    for spec in (False, True):
+        eng.speculate = spec
+        for _ in range(2):  # the first call captures the graphs
+            toks, t_first = [], None
+            for i, step in enumerate(eng.generate(prompts, new_tokens)):
+                if i == 0:
+                    t_first = time.perf_counter()
+                toks.append(step)
+            dt = time.perf_counter() - t_first
+        res[spec] = (toks, dt)
+        log(f"{'speculative' if spec else 'plain'} B={batch} S={prompt_len} N={new_tokens}: "
+            f"{dt * 1e3:.1f} ms for {new_tokens - 1} decode steps")
+    stats = dict(eng.stats.get("spec", {}))
+    n_draft = eng.shape.spec_k if eng.shape is not None else None
+    eng.speculate = False
+    torch.cuda.empty_cache()
+    n_tok = batch * (new_tokens - 1)
+    plain_tps, spec_tps = n_tok / res[False][1], n_tok / res[True][1]
+    return {"workload": f"qwen3-4b bf16 bs{batch} motif prompt{prompt_len} new{new_tokens}, drafter n=3/2 k<=8",
+            "plain_tok_s": round(plain_tps, 2), "spec_tok_s": round(spec_tps, 2),
+            "speedup": round(spec_tps / plain_tps, 3),
+            "mean_accept_len": round(stats.get("mean_accept_len", float("nan")), 3),
+            "tokens_per_verify": round(stats.get("tokens_per_verify", float("nan")), 3),
+            "iterations": stats.get("iterations"),
+            "verify_iterations": stats.get("verify_iterations"),
+            "plain_iterations": stats.get("plain_iterations"),
+            "verify_cost_ratio": stats.get("cost_ratio"),
+            "drafts_per_verify": n_draft,
+            "token_identical": res[False][0] == res[True][0]}
 
 
 def cpu_baseline(ckpt, cfg, prompt_len, budget_s=25.0):
@@ -137,6 +196,7 @@ def main():
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--ckpt", default=os.environ.get("QDEC_BENCH_CKPT", "/tmp/qdec_qwen3_4b_seed0"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-spec", action="store_true")
     ap.add_argument("--cpu-prompt", type=int, default=64)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -214,9 +274,17 @@ def main():
         roles[role] = round(time_gemm_role(eng, st, role) * 1e6, 2)
     log(f"other roles us/launch: {roles}")
 
+    spec = None
+    if not args.no_spec:
+        del sh, st, graph
+        eng.shape = None
+        torch.cuda.empty_cache()
+        spec = spec_bench(eng, mc.vocab)
+        log(f"speculation: {spec}")
+
     cpu = None
     if not args.no_cpu_baseline:
-        del eng, sh, st, graph
+        del eng
         torch.cuda.empty_cache()
         try:
             cpu = cpu_baseline(args.ckpt, cfg, args.cpu_prompt)
@@ -248,6 +316,7 @@ def main():
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
         "role_us_per_launch": roles,
+        "speculation": spec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -36,6 +36,29 @@ static int launch_status(hipError_t e, const char *what) {
   return check_launch(what);
 }
 
+// Workspace of a planned GEMM call: fp32 k-split partials or the argmax
+// partials, then (direct activations with NORM_IN) the normalised rows.
+static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *partial_bytes,
+                         size_t *counter_bytes, size_t *xn_off) {
+  const int ntiles = a->n / 16;
+  size_t pb = 0, cb = 0;
+  if (a->flags & QDEC_ARGMAX) {
+    pb = 2 * sizeof(float) * (size_t)(ntiles / a->tiles_per_wg) * a->rows;
+    cb = sizeof(uint32_t);
+  } else if (a->ksplit > 1) {
+    pb = sizeof(float) * (size_t)a->ksplit * a->rows * a->n * ((a->flags & QDEC_GLU) ? 2 : 1);
+    cb = sizeof(uint32_t) * (size_t)ntiles;
+  }
+  size_t off = 0;
+  if (p.xd && (a->flags & QDEC_NORM_IN)) {
+    off = (pb + 255) & ~(size_t)255;
+    pb = off + sizeof(uint16_t) * (size_t)a->rows * a->k;
+  }
+  *partial_bytes = pb;
+  *counter_bytes = cb;
+  *xn_off = off;
+}
+
 // Derive the launch plan of a GEMM call; returns QDEC_OK or an error code.
 static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) {
   if (!a) return set_error(QDEC_EINVAL, "qdec_gemm: null args");
@@ -97,7 +120,29 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->lds_x_off = (int)(head + red_bytes);
   p->lds_bytes = head + red_bytes + (size_t)a->rows * p->xstride * 2;
   p->xfast = gemm_fast_path(*p, f) ? 1 : 0;
-  p->rw = gemm_window(*p, f);
+  // Weight ring: x staged in LDS when it fits; otherwise (up to 16 rows, no
+  // k split) B fragments straight from x, with NORM_IN's normalised rows
+  // written to the workspace by a pre-pass.
+  p->rw = 0;
+  p->xd = 0;
+  p->xn = nullptr;
+  if (a->rows <= 16) {
+    const int rw = gemm_ring(p->ksw, f);
+    if (rw && lds_all) {
+      p->rw = rw;
+    } else if (rw && a->ksplit == 1) {
+      p->rw = rw;
+      p->xd = 1;
+      p->xfast = 0;
+      p->lds_all = 0;
+      p->lds_bytes = head + red_bytes;
+    }
+  }
+  size_t pb = 0, cb = 0, xn_off = 0;
+  gemm_scratch(a, *p, &pb, &cb, &xn_off);
+  if (need_scratch && pb && !a->partial) return set_error(QDEC_EINVAL, "qdec_gemm: this call needs a partial workspace");
+  if (p->xd && (f & QDEC_NORM_IN) && a->partial)
+    p->xn = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(a->partial) + xn_off);
   if (p->lds_bytes > (size_t)kGemmLdsX)
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: rows %d x waves %d needs %zu B of LDS", a->rows, a->waves,
                      p->lds_bytes);
@@ -184,15 +229,8 @@ int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes, size_t *
   GemmParams p;
   const int rc = plan_gemm(a, &p, false);
   if (rc != QDEC_OK) return rc;
-  const int ntiles = a->n / 16;
-  size_t pb = 0, cb = 0;
-  if (a->flags & QDEC_ARGMAX) {
-    pb = 2 * sizeof(float) * (size_t)(ntiles / a->tiles_per_wg) * a->rows;
-    cb = sizeof(uint32_t);
-  } else if (a->ksplit > 1) {
-    pb = sizeof(float) * (size_t)a->ksplit * a->rows * a->n * ((a->flags & QDEC_GLU) ? 2 : 1);
-    cb = sizeof(uint32_t) * (size_t)ntiles;
-  }
+  size_t pb = 0, cb = 0, xn_off = 0;
+  gemm_scratch(a, p, &pb, &cb, &xn_off);
   if (partial_bytes) *partial_bytes = pb;
   if (counter_bytes) *counter_bytes = cb;
   return QDEC_OK;
@@ -225,7 +263,7 @@ int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream) {
 
 int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream) {
   if (!a || !a->hist || !a->lens || !a->ids || !a->draft) return set_error(QDEC_EINVAL, "qdec_ngram_draft: null pointer");
-  if (a->batch < 1 || a->cap < 1 || a->k < 1 || a->primary < 1 || a->backoff < 1)
+  if (a->batch < 1 || a->cap < 1 || a->k < 0 || a->primary < 1 || a->backoff < 1)
     return set_error(QDEC_EINVAL, "qdec_ngram_draft: batch %d cap %d k %d primary %d backoff %d", a->batch, a->cap,
                      a->k, a->primary, a->backoff);
   return launch_status(
@@ -237,7 +275,7 @@ int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream) {
 int qdec_spec_accept(const qdec_accept_args *a, qdec_stream_t stream) {
   if (!a || !a->out_tok || !a->draft || !a->hist || !a->lens || !a->naccept)
     return set_error(QDEC_EINVAL, "qdec_spec_accept: null pointer");
-  if (a->batch < 1 || a->cap < 1 || a->k < 1)
+  if (a->batch < 1 || a->cap < 1 || a->k < 0)
     return set_error(QDEC_EINVAL, "qdec_spec_accept: batch %d cap %d k %d", a->batch, a->cap, a->k);
   return launch_status(launch_accept(a->out_tok, a->draft, a->hist, a->lens, a->naccept, a->batch, a->cap, a->k,
                                      a->stop_len, (hipStream_t)stream),

@@ -85,7 +85,7 @@ __device__ __forceinline__ uint4 norm8(const uint4 &xv, const uint4 &nv, float r
   return pack8(f);
 }
 
-template <int MT, uint32_t FLAGS, int RW>
+template <int MT, uint32_t FLAGS, int RW, bool XD>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr bool NORM = (FLAGS & QDEC_NORM_IN) != 0;
@@ -95,6 +95,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   constexpr int NACC = GLU ? 2 : 1;
   constexpr bool WIN = RW > 0;
   static_assert(!WIN || MT == 1, "the window path serves one M tile");
+  static_assert(!XD || (WIN && !NORM), "direct activations: window path, x already normalised");
   constexpr int NB = WIN ? RW : (GLU ? kGemmKpMaxGlu : kGemmKpMax);  // weight registers per accumulator
 
   float *s_rstd = reinterpret_cast<float *>(smem);              // [64]
@@ -123,6 +124,11 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   const int tile0 = tg * p.tiles_per_wg;
 
   uint4 wb[NACC][NB];
+  // Direct activations: the B fragment of ring slot r, loaded from global
+  // (cache-resident x) right behind the slot's weight block.
+  uint4 xb[XD ? NB : 1];
+  const bool xrow_ok = col < rows;  // lanes past the last row read row 0 and use zeros
+  const uint16_t *xg = X + (size_t)(xrow_ok ? col : 0) * p.k + (size_t)ks_wave * 32 + grp * 8;
   // Weight block of k step i (relative to the wave's range) of `tile`.
   auto wptr = [&](int tile, int i) { return W + ((size_t)tile * p.KS + ks_wave + i) * 64 + lane; };
   // Passes: straight-line loads of one pass; indices past the pass are clamped
@@ -144,6 +150,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       for (int r = 0; r < NB; ++r) {
         wb[0][r] = q[r * 64];
         if constexpr (GLU) wb[1][r] = q[r * 64 + up_off];
+        if constexpr (XD) xb[r] = *reinterpret_cast<const uint4 *>(xg + r * 32);
       }
     } else {
       issue_pass(tile0, 0, min(p.kp, p.ksw));
@@ -153,7 +160,9 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   // ---- activations.
   const int lds_steps = p.lds_all ? p.ksw : p.kp;  // LDS columns per wave
   bool staged = false;
-  if (p.xfast) {
+  if constexpr (XD) {
+    issue_first();
+  } else if (p.xfast) {
     // Row m, vectors vr = tid + j*nthr of the workgroup's k range (per_row
     // of them), loaded into registers before the first weights.
     const int per_row = p.ksw * nw * 4;
@@ -263,7 +272,6 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
     if constexpr (WIN) {
       // B operand rows: lane col < rows reads its row, the others read row 0
       // and use zeros.
-      const bool xrow_ok = col < rows;
       const uint16_t *xs = s_x + (size_t)(xrow_ok ? col : 0) * xstride + wave * p.ksw * 32 + grp * 8;
       // Refills: k step i0 + r + RW of this tile while it exists, then the
       // same offset into the next tile; none past the wave's last tile.
@@ -274,13 +282,17 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + 1, i0 + RW - p.ksw);
 #pragma unroll
         for (int r = 0; r < RW; ++r) {
-          const uint4 bx = *reinterpret_cast<const uint4 *>(xs + (i0 + r) * 32);
+          uint4 bx;
+          if constexpr (XD) bx = xb[r];
+          else bx = *reinterpret_cast<const uint4 *>(xs + (i0 + r) * 32);
           const uint4 b = xrow_ok ? bx : zero4();
 #pragma unroll
           for (int a = 0; a < NACC; ++a) acc[a][0] = mfma16x16x32(wb[a][r], b, acc[a][0]);
           if (refill) {
             wb[0][r] = qn[r * 64];
             if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
+            // every tile of the workgroup spans the same k range of x
+            if constexpr (XD) xb[r] = *reinterpret_cast<const uint4 *>(xg + ((i0 + RW + r) % p.ksw) * 32);
           }
         }
       }
@@ -510,14 +522,41 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   }
 }
 
+// x' = norm_w * bf16(x * rstd) of one row per workgroup, written to xn: the
+// same statistic (thread t sums vectors t, t+T, ..., then block_row_sums)
+// and the same rounding as the GEMM's own staging, so a row comes out
+// bit-identical whichever path stages it.
+__global__ void __launch_bounds__(512) rownorm_kernel(const uint16_t *__restrict__ X, const uint16_t *__restrict__ norm_w,
+                                                       uint16_t *__restrict__ xn, int k, float eps) {
+  __shared__ float s_red[8 * 8];
+  __shared__ float s_rstd[8];
+  const int m = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
+  const uint16_t *xrow = X + (size_t)m * k;
+  const int nvec = k >> 3;
+  float ss[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss[j] = 0.f;
+  for (int v = tid; v < nvec; v += nthr) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4 *>(xrow + 8 * v), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss[0] += f[e] * f[e];
+  }
+  block_row_sums(ss, s_red, 1, s_rstd, 0, k, eps);
+  const float rs = s_rstd[0];
+  for (int v = tid; v < nvec; v += nthr)
+    *reinterpret_cast<uint4 *>(xn + (size_t)m * k + 8 * v) =
+        norm8(*reinterpret_cast<const uint4 *>(xrow + 8 * v), *reinterpret_cast<const uint4 *>(norm_w + 8 * v), rs);
+}
+
 template <int MT, int RW>
 hipError_t launch_flags(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   switch (flags) {
-    case 0u: hipLaunchKernelGGL((gemm_kernel<MT, 0u, RW>), grid, block, lds, s, p); break;
-    case QDEC_NORM_IN: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN, RW>), grid, block, lds, s, p); break;
-    case QDEC_RES_OUT: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT, RW>), grid, block, lds, s, p); break;
+    case 0u: hipLaunchKernelGGL((gemm_kernel<MT, 0u, RW, false>), grid, block, lds, s, p); break;
+    case QDEC_NORM_IN: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN, RW, false>), grid, block, lds, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT, RW, false>), grid, block, lds, s, p); break;
     case QDEC_NORM_IN | QDEC_ARGMAX:
-      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_ARGMAX, RW>), grid, block, lds, s, p);
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_ARGMAX, RW, false>), grid, block, lds, s, p);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -527,7 +566,7 @@ hipError_t launch_flags(const GemmParams &p, uint32_t flags, dim3 grid, dim3 blo
 template <int MT>
 hipError_t launch_pass(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   if (flags == (QDEC_NORM_IN | QDEC_GLU)) {
-    hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_GLU, 0>), grid, block, lds, s, p);
+    hipLaunchKernelGGL((gemm_kernel<MT, QDEC_NORM_IN | QDEC_GLU, 0, false>), grid, block, lds, s, p);
     return hipSuccess;
   }
   return launch_flags<MT, 0>(p, flags, grid, block, lds, s);
@@ -546,14 +585,24 @@ bool gemm_fast_path(const GemmParams &p, uint32_t flags) {
          (!(flags & QDEC_NORM_IN) || p.ksplit == 1);
 }
 
-int gemm_window(const GemmParams &p, uint32_t flags) {
-  if (!p.lds_all || p.rows > 16) return 0;
-  if (flags & QDEC_GLU) return p.ksw % 10 == 0 ? 10 : 0;
+int gemm_ring(int ksw, uint32_t flags) {
+  if (flags & QDEC_GLU) return ksw % 10 == 0 ? 10 : 0;
   // 20 and 16 measured faster than passes on MI355X; a 19-register ring
   // (k = 9728 with 4 waves) was slower than 20-block passes.
   for (const int rw : {20, 16})
-    if (p.ksw % rw == 0) return rw;
+    if (ksw % rw == 0) return rw;
   return 0;
+}
+
+template <int RW>
+hipError_t launch_direct(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  switch (flags & ~QDEC_NORM_IN) {
+    case 0u: hipLaunchKernelGGL((gemm_kernel<1, 0u, RW, true>), grid, block, lds, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL((gemm_kernel<1, QDEC_RES_OUT, RW, true>), grid, block, lds, s, p); break;
+    case QDEC_ARGMAX: hipLaunchKernelGGL((gemm_kernel<1, QDEC_ARGMAX, RW, true>), grid, block, lds, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
@@ -562,11 +611,30 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   dim3 grid((ntiles / p.tiles_per_wg) * p.ksplit);
   dim3 block(64 * p.waves);
   const size_t lds = p.lds_bytes;
+  if (p.xd) {
+    if (mt != 1) return hipErrorInvalidValue;
+    GemmParams q = p;
+    if (flags & QDEC_NORM_IN) {
+      hipLaunchKernelGGL(rownorm_kernel, dim3(p.rows), block, 0, s, reinterpret_cast<const uint16_t *>(p.x),
+                         reinterpret_cast<const uint16_t *>(p.norm_w), p.xn, p.k, p.eps);
+      q.x = p.xn;
+    }
+    if (flags & QDEC_GLU) {
+      if (p.rw != 10) return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gemm_kernel<1, QDEC_GLU, 10, true>), grid, block, lds, s, q);
+      return hipSuccess;
+    }
+    switch (p.rw) {
+      case 16: return launch_direct<16>(q, flags, grid, block, lds, s);
+      case 20: return launch_direct<20>(q, flags, grid, block, lds, s);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (p.rw > 0) {
     if (mt != 1) return hipErrorInvalidValue;
     if (flags == (QDEC_NORM_IN | QDEC_GLU)) {
       if (p.rw != 10) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_GLU, 10>), grid, block, lds, s, p);
+      hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_GLU, 10, false>), grid, block, lds, s, p);
       return hipSuccess;
     }
     switch (p.rw) {

@@ -56,8 +56,8 @@ __global__ void draft_kernel(const int64_t *__restrict__ hist, const int32_t *__
   if (L < 0) L = 0;
   if (L >= cap) L = cap - 1;  // a frozen or corrupt length never reads out of the row
   const int ngram[2] = {primary, backoff};
-  int best[2];
-  for (int which = 0; which < 2; ++which) {
+  int best[2] = {-1, -1};
+  for (int which = 0; which < 2 && K > 0; ++which) {  // k = 0: feed the current token only
     const int n = ngram[which];
     const int limit = min(L - n - K + 2, cap);
     int mine = -1;

@@ -35,11 +35,13 @@ struct GemmParams {
   int xfast;     // activations staged from registers (see gemm.hip)
   int lds_all;   // the workgroup's whole k range of x is staged in LDS once
   int rw;        // weight ring registers per wave (window path), 0 = passes
+  int xd;        // window path with B fragments loaded straight from x (no LDS staging)
+  uint16_t *xn;  // NORM_IN with xd: normalised copy of x (workspace)
   size_t lds_bytes;
 };
 bool gemm_flags_supported(uint32_t flags);
 bool gemm_fast_path(const GemmParams &p, uint32_t flags);
-int gemm_window(const GemmParams &p, uint32_t flags);
+int gemm_ring(int ksw, uint32_t flags);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 
 struct AttnParams {

@@ -48,7 +48,15 @@ LOOKAHEAD = 3
 # n-gram drafter settings of speculative decoding (notes/v10/spec.py:13-16).
 SPEC_PRIMARY = 3
 SPEC_BACKOFF = 2
-SPEC_K = 8
+SPEC_K_MAX = 8
+
+
+def spec_k(batch):
+    """Drafts per sequence per verify iteration: up to SPEC_K_MAX, and few
+    enough that the batch's verify rows fit one 16-row MFMA tile (the GEMMs'
+    fast path), so a verify iteration costs about a plain step.  0 = no
+    speculation at this batch size."""
+    return max(0, min(SPEC_K_MAX, 16 // batch - 1))
 
 
 def _log(message):
@@ -64,9 +72,10 @@ class _Shape:
         # The verify slack is reserved in both modes: attention chunking is a
         # function of (batch, capacity), and plain and speculative runs of one
         # shape must chunk alike to produce the same bits.
-        slack = 2 * (SPEC_K + 1)
+        self.spec_k = spec_k(batch)
+        slack = 2 * (self.spec_k + 1)
         self.capacity = prompt_len + new_tokens + slack
-        max_t = (SPEC_K + 1) if speculate else 16
+        max_t = (self.spec_k + 1) if (speculate and self.spec_k) else 16
         self.state = DecodeState(engine.model, batch, self.capacity, max_t=max_t)
         self.graph = None
         self.spec_graph = None
@@ -100,6 +109,7 @@ class Engine:
         self.lib = capi.lib()
         self.model = DeviceModel(cfg, tensors, self.device)
         self.speculate = bool(speculate)
+        self.spec_gate = True  # speculation falls back to plain steps when drafts do not pay
         self.use_graphs = use_graphs
         self.shape = None
         self.stats = {}
@@ -169,6 +179,9 @@ class Engine:
             yield from self._generate_spec(ids, steps)
             return
         sh = self._shape_for(batch, prompt_len, steps)
+        yield from self._generate_plain(sh, ids, steps)
+
+    def _generate_plain(self, sh, ids, steps):
         sh.state.prefill(ids.to(self.device, non_blocking=True))
         self._publish(sh, 0)
         ahead = LOOKAHEAD if sh.graph is not None else 1
@@ -186,8 +199,12 @@ class Engine:
 
         batch, prompt_len = ids.shape
         sh = self._shape_for(batch, prompt_len, steps)
+        if sh.spec_k == 0:  # no room for drafts at this batch size
+            yield from self._generate_plain(sh, ids, steps)
+            self.stats["spec"] = {"iterations": steps - 1, "verify_iterations": 0, "plain_iterations": steps - 1}
+            return
         dec = getattr(sh, "spec", None)
         if dec is None:
-            dec = sh.spec = SpecDecoder(self, sh.state, SPEC_PRIMARY, SPEC_BACKOFF, SPEC_K)
-        yield from dec.generate(ids, steps)
+            dec = sh.spec = SpecDecoder(self, sh.state, SPEC_PRIMARY, SPEC_BACKOFF, sh.spec_k)
+        yield from dec.generate(ids, steps, gate=self.spec_gate)
         self.stats["spec"] = dec.last_stats

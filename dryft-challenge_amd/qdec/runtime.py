@@ -227,9 +227,10 @@ class DecodeState:
         gw = 0
         gc = 1
         for role in ("qkv", "o", "gate_up", "down", "lm"):
-            a = self._gemm_args(role, 0, R)
-            pb, cb = self.lib.gemm_workspace(a)
-            gw, gc = max(gw, pb), max(gc, cb)
+            for t in range(1, self.max_t + 1):  # the plan (and its workspace) depends on the row count
+                a = self._gemm_args(role, 0, batch * t)
+                pb, cb = self.lib.gemm_workspace(a)
+                gw, gc = max(gw, pb), max(gc, cb)
         self.gemm_partial = torch.zeros((max(gw, 16) // 4 + 4,), dtype=torch.float32, device=dev)
         self.gemm_counters = torch.zeros((max(gc, 4) // 4 + 4,), dtype=torch.int32, device=dev)
         aw, ac = self.lib.attn_workspace(self._attn_args(0, self.max_t))

@@ -195,7 +195,9 @@ int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,
  * tokens; the most recent earlier occurrence whose k-token continuation lies
  * inside the history wins; otherwise the same with `backoff` tokens;
  * otherwise the draft is all zeros.  Writes ids[b*(k+1)] = hist[b, lens[b]],
- * ids[b*(k+1) + 1 + t] = draft[b*k + t].
+ * ids[b*(k+1) + 1 + t] = draft[b*k + t].  k = 0 only feeds the current token
+ * (a plain step that keeps the history: what the acceptance gate falls back
+ * to); draft must still be a valid pointer.
  * Replaces notes/v10/spec.py:36-108 (_ngram_draft_kernel / ngram_draft). */
 typedef struct {
   const int64_t *hist; /* [batch, cap] */

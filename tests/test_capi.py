@@ -122,7 +122,7 @@ def test_other_validation(qlib):
     assert qlib.so.qdec_pack_tiles(16, 16, 17, 32, None) == -1
     e = capi.EmbedArgs(ids=16, emb=16, h=16, rows=1, hidden=100, vocab=16)
     assert qlib.so.qdec_embed(ctypes.byref(e), None) == -1
-    d = capi.DraftArgs(hist=16, lens=16, ids=16, draft=16, batch=1, cap=8, primary=3, backoff=2, k=0)
+    d = capi.DraftArgs(hist=16, lens=16, ids=16, draft=16, batch=1, cap=8, primary=3, backoff=2, k=-1)
     assert qlib.so.qdec_ngram_draft(ctypes.byref(d), None) == -1
     a = capi.AcceptArgs(out_tok=16, draft=16, hist=16, lens=16, naccept=None, batch=1, cap=8, k=1, stop_len=1)
     assert qlib.so.qdec_spec_accept(ctypes.byref(a), None) == -1

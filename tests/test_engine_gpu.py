@@ -124,12 +124,16 @@ def motif_prompts(B, S, seed, vocab=151936, motif=64, noise=0.1):
 def test_speculative_equals_plain_greedy(ckpt, engine):
     from engine import Engine
     spec = Engine.from_tensors(engine.model.cfg.raw, load_tensors(ckpt[0]), speculate=True)
-    for B, S, n, seed in ((4, 200, 40, 7), (2, 64, 25, 8), (1, 30, 17, 9)):
+    for B, S, n, seed in ((4, 200, 40, 7), (2, 64, 25, 8), (1, 30, 17, 9), (16, 40, 9, 10)):
         prompt = motif_prompts(B, S, seed)
         plain = list(engine.generate(prompt.tolist(), n))
-        fast = list(spec.generate(prompt.tolist(), n))
-        assert fast == plain, (B, S, n)
-        stats = spec.stats["spec"]
-        print(f"spec B={B} S={S} n={n}: {stats}")
-        assert stats["iterations"] <= n - 1
+        for gate in (False, True):  # always verify / acceptance gate
+            spec.spec_gate = gate
+            fast = list(spec.generate(prompt.tolist(), n))
+            assert fast == plain, (B, S, n, gate)
+            stats = spec.stats["spec"]
+            print(f"spec B={B} S={S} n={n} gate={gate}: {stats}")
+            assert stats["iterations"] <= n - 1
+            if not gate and B < 16:
+                assert stats["plain_iterations"] == 0
 

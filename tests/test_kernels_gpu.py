@@ -9,6 +9,7 @@ checked bit for bit: it is what makes speculative decoding lossless.
 """
 
 import math
+import zlib
 
 import pytest
 import torch
@@ -117,7 +118,7 @@ def test_embed_gather_exact(lib):
 
 # ------------------------------------------------------------------- GEMM
 
-@pytest.mark.parametrize("rows", [1, 4, 17, 36, 64])
+@pytest.mark.parametrize("rows", [1, 4, 9, 16, 17, 36, 64])
 @pytest.mark.parametrize("role", ["qkv", "o", "gate_up", "down"])
 def test_gemm_roles_vs_oracle(lib, role, rows):
     from qdec import capi
@@ -125,7 +126,7 @@ def test_gemm_roles_vs_oracle(lib, role, rows):
     n, k, flags = {"qkv": (6144, H, capi.NORM_IN), "o": (H, 4096, capi.RES_OUT),
                    "gate_up": (I, H, capi.NORM_IN | capi.GLU), "down": (H, I, capi.RES_OUT)}[role]
     ks, waves, _ = role_plan(n, k, role)
-    seed = hash((role, rows)) % 1000
+    seed = (zlib.crc32(role.encode()) + 7 * rows) % 1000  # stable across processes
     x = rnd(rows, k, scale=3.0, seed=seed)
     wn = 2 * n if flags & capi.GLU else n
     W = rnd(wn, k, scale=0.02, seed=seed + 1)
@@ -150,13 +151,17 @@ def test_gemm_roles_vs_oracle(lib, role, rows):
         out = torch.zeros(rows, n, dtype=torch.bfloat16, device=DEV)
         g(xd, Wt, out=out, norm_w=nw.to(DEV))
         ref = linear(xin, W.float())
-    agree(out, ref)
+    # bf16 outputs agree bit for bit except where the fp32 sums straddle a
+    # rounding boundary (summation order differs from torch's); SwiGLU
+    # rounds three times, so more of its outputs straddle one.
+    agree(out, ref, min_exact=0.97 if flags & capi.GLU else 0.98)
 
 
 @pytest.mark.parametrize("role", ["qkv", "o", "gate_up", "down"])
 def test_gemm_row_invariance_bitexact(lib, role):
     """A row's output bits do not depend on how many rows share the call or
-    where the row sits (MFMA column, M tile, LDS pass)."""
+    where the row sits (MFMA column, M tile, LDS pass, activations staged in
+    LDS or read directly after the normalisation pre-pass)."""
     from qdec import capi
     from qdec.runtime import role_plan
     n, k, flags = {"qkv": (6144, H, capi.NORM_IN), "o": (H, 4096, capi.RES_OUT),
@@ -180,7 +185,8 @@ def test_gemm_row_invariance_bitexact(lib, role):
         return o
 
     full = run(list(range(big)))
-    for rows_idx in ([5], [0, 1, 2, 3], list(range(36)), [63, 9, 40], list(range(17, 34))):
+    for rows_idx in ([5], [0, 1, 2, 3], list(range(36)), [63, 9, 40], list(range(17, 34)), list(range(16)),
+                     list(range(40, 49)), [7] * 12):
         part = run(rows_idx)
         assert torch.equal(part.view(torch.int16), full[rows_idx].view(torch.int16)), rows_idx
 
@@ -343,11 +349,14 @@ def attn_case_from(lib, c9, B, T, t, lens, cap, chunk):
 
 # ---------------------------------------------------------- speculation
 
-def test_draft_and_accept_vs_oracle(lib):
+@pytest.mark.parametrize("K", [6, 0])
+def test_draft_and_accept_vs_oracle(lib, K):
+    """k = 0 is the plain step of the acceptance gate: only the current
+    token is fed and one pick is appended."""
     from qdec import capi
     import random
-    rng = random.Random(3)
-    B, cap, K = 5, 96, 6
+    rng = random.Random(3 + K)
+    B, cap = 5, 96
     T = K + 1
     for trial in range(20):
         hist = [[rng.randint(0, 4) for _ in range(cap)] for _ in range(B)]
@@ -355,7 +364,7 @@ def test_draft_and_accept_vs_oracle(lib):
         dh = torch.tensor(hist, dtype=torch.int64, device=DEV)
         dl = torch.tensor(lens, dtype=torch.int32, device=DEV)
         ids = torch.zeros(B * T, dtype=torch.int64, device=DEV)
-        dr = torch.zeros(B * K, dtype=torch.int64, device=DEV)
+        dr = torch.zeros(max(B * K, 1), dtype=torch.int64, device=DEV)
         d = capi.DraftArgs(hist=dh.data_ptr(), lens=dl.data_ptr(), ids=ids.data_ptr(), draft=dr.data_ptr(),
                            batch=B, cap=cap, primary=3, backoff=2, k=K)
         lib.ngram_draft(d, stream())
@@ -365,7 +374,7 @@ def test_draft_and_accept_vs_oracle(lib):
             i, dd = draft_ref(hist[b], lens[b], 3, 2, K)
             exp_ids += i
             exp_dr += dd
-        assert ids.cpu().tolist() == exp_ids and dr.cpu().tolist() == exp_dr
+        assert ids.cpu().tolist() == exp_ids and dr.cpu().tolist()[:B * K] == exp_dr
         # accept with model outputs that agree with the draft for a random prefix
         out_tok = []
         for b in range(B):
