@@ -120,23 +120,22 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->lds_x_off = (int)(head + red_bytes);
   p->lds_bytes = head + red_bytes + (size_t)a->rows * p->xstride * 2;
   p->xfast = gemm_fast_path(*p, f) ? 1 : 0;
-  // Weight ring: x staged in LDS when it fits; otherwise (up to 16 rows, no
-  // k split) B fragments straight from x, with NORM_IN's normalised rows
-  // written to the workspace by a pre-pass.
+  // Weight ring: x staged in LDS when it fits (one M tile); otherwise (no k
+  // split) B fragments straight from x, with NORM_IN's normalised rows
+  // written to the workspace by a pre-pass; passes only when neither fits.
   p->rw = 0;
   p->xd = 0;
   p->xn = nullptr;
-  if (a->rows <= 16) {
-    const int rw = gemm_ring(p->ksw, f);
-    if (rw && lds_all) {
-      p->rw = rw;
-    } else if (rw && a->ksplit == 1) {
-      p->rw = rw;
-      p->xd = 1;
-      p->xfast = 0;
-      p->lds_all = 0;
-      p->lds_bytes = head + red_bytes;
-    }
+  const int ring = gemm_ring(p->ksw, f);
+  const int ring_d = gemm_ring_direct(mt, f);
+  if (mt == 1 && lds_all && ring) {
+    p->rw = ring;
+  } else if (a->ksplit == 1 && ring_d && (a->tiles_per_wg == 1 || p->ksw % ring_d == 0)) {
+    p->rw = ring_d;
+    p->xd = 1;
+    p->xfast = 0;
+    p->lds_all = 0;
+    p->lds_bytes = head + red_bytes;
   }
   size_t pb = 0, cb = 0, xn_off = 0;
   gemm_scratch(a, *p, &pb, &cb, &xn_off);

@@ -94,7 +94,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   constexpr bool ARG = (FLAGS & QDEC_ARGMAX) != 0;
   constexpr int NACC = GLU ? 2 : 1;
   constexpr bool WIN = RW > 0;
-  static_assert(!WIN || MT == 1, "the window path serves one M tile");
+  static_assert(!WIN || MT == 1 || XD, "LDS-staged windows serve one M tile");
   static_assert(!XD || (WIN && !NORM), "direct activations: window path, x already normalised");
   constexpr int NB = WIN ? RW : (GLU ? kGemmKpMaxGlu : kGemmKpMax);  // weight registers per accumulator
 
@@ -126,9 +126,14 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   uint4 wb[NACC][NB];
   // Direct activations: the B fragment of ring slot r, loaded from global
   // (cache-resident x) right behind the slot's weight block.
-  uint4 xb[XD ? NB : 1];
+  uint4 xb[XD ? MT : 1][XD ? NB : 1];
   const bool xrow_ok = col < rows;  // lanes past the last row read row 0 and use zeros
-  const uint16_t *xg = X + (size_t)(xrow_ok ? col : 0) * p.k + (size_t)ks_wave * 32 + grp * 8;
+  const uint16_t *xg[MT];           // row mt*16 + col of x at the wave's first k step
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + col;
+    xg[mt] = X + (size_t)(m < rows ? m : 0) * p.k + (size_t)ks_wave * 32 + grp * 8;
+  }
   // Weight block of k step i (relative to the wave's range) of `tile`.
   auto wptr = [&](int tile, int i) { return W + ((size_t)tile * p.KS + ks_wave + i) * 64 + lane; };
   // Passes: straight-line loads of one pass; indices past the pass are clamped
@@ -148,9 +153,14 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       const uint4 *q = wptr(tile0, 0);
 #pragma unroll
       for (int r = 0; r < NB; ++r) {
-        wb[0][r] = q[r * 64];
-        if constexpr (GLU) wb[1][r] = q[r * 64 + up_off];
-        if constexpr (XD) xb[r] = *reinterpret_cast<const uint4 *>(xg + r * 32);
+        const int rr = min(r, p.ksw - 1);  // a range shorter than the ring repeats its last block
+        wb[0][r] = q[rr * 64];
+        if constexpr (GLU) wb[1][r] = q[rr * 64 + up_off];
+        if constexpr (XD) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + min(r, p.ksw - 1) * 32);
+        }
       }
     } else {
       issue_pass(tile0, 0, min(p.kp, p.ksw));
@@ -273,26 +283,52 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       // B operand rows: lane col < rows reads its row, the others read row 0
       // and use zeros.
       const uint16_t *xs = s_x + (size_t)(xrow_ok ? col : 0) * xstride + wave * p.ksw * 32 + grp * 8;
-      // Refills: k step i0 + r + RW of this tile while it exists, then the
-      // same offset into the next tile; none past the wave's last tile.
       const bool more_tiles = tt + 1 < p.tiles_per_wg;
-      for (int i0 = 0; i0 < p.ksw; i0 += RW) {
-        const bool same_tile = i0 + RW < p.ksw;
-        const bool refill = same_tile || more_tiles;
-        const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + 1, i0 + RW - p.ksw);
+      if constexpr (!XD) {
+        // Slot r always holds k step r (mod RW): refill with k step i + RW of
+        // this tile while it exists, else the same offset into the next tile;
+        // none past the last tile.
+        for (int i0 = 0; i0 < p.ksw; i0 += RW) {
+          const bool same_tile = i0 + RW < p.ksw;
+          const bool refill = same_tile || more_tiles;
+          const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + 1, i0 + RW - p.ksw);
 #pragma unroll
-        for (int r = 0; r < RW; ++r) {
-          uint4 bx;
-          if constexpr (XD) bx = xb[r];
-          else bx = *reinterpret_cast<const uint4 *>(xs + (i0 + r) * 32);
-          const uint4 b = xrow_ok ? bx : zero4();
+          for (int r = 0; r < RW; ++r) {
+            const uint4 bx = *reinterpret_cast<const uint4 *>(xs + (i0 + r) * 32);
+            const uint4 b = xrow_ok ? bx : zero4();
 #pragma unroll
-          for (int a = 0; a < NACC; ++a) acc[a][0] = mfma16x16x32(wb[a][r], b, acc[a][0]);
-          if (refill) {
-            wb[0][r] = qn[r * 64];
-            if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
-            // every tile of the workgroup spans the same k range of x
-            if constexpr (XD) xb[r] = *reinterpret_cast<const uint4 *>(xg + ((i0 + RW + r) % p.ksw) * 32);
+            for (int a = 0; a < NACC; ++a) acc[a][0] = mfma16x16x32(wb[a][r], b, acc[a][0]);
+            if (refill) {
+              wb[0][r] = qn[r * 64];
+              if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
+            }
+          }
+        }
+      } else {
+        // Direct activations: the same ring, and a ragged last chunk when RW
+        // does not divide the range (one tile per workgroup then).  Every tile
+        // spans the same k range of x.
+        for (int i0 = 0; i0 < p.ksw; i0 += RW) {
+          const bool same_tile = i0 + RW < p.ksw;
+          const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + 1, i0 + RW - p.ksw);
+#pragma unroll
+          for (int r = 0; r < RW; ++r) {
+            const int i = i0 + r;
+            if (i < p.ksw) {
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt) {
+                const uint4 b = (mt * 16 + col < rows) ? xb[mt][r] : zero4();
+#pragma unroll
+                for (int a = 0; a < NACC; ++a) acc[a][mt] = mfma16x16x32(wb[a][r], b, acc[a][mt]);
+              }
+              if (i + RW < p.ksw || (!same_tile && more_tiles)) {
+                wb[0][r] = qn[r * 64];
+                if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                  xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + ((i + RW) % p.ksw) * 32);
+              }
+            }
           }
         }
       }
@@ -594,15 +630,43 @@ int gemm_ring(int ksw, uint32_t flags) {
   return 0;
 }
 
-template <int RW>
+namespace {
+
+template <int MT, int RW>
 hipError_t launch_direct(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   switch (flags & ~QDEC_NORM_IN) {
-    case 0u: hipLaunchKernelGGL((gemm_kernel<1, 0u, RW, true>), grid, block, lds, s, p); break;
-    case QDEC_RES_OUT: hipLaunchKernelGGL((gemm_kernel<1, QDEC_RES_OUT, RW, true>), grid, block, lds, s, p); break;
-    case QDEC_ARGMAX: hipLaunchKernelGGL((gemm_kernel<1, QDEC_ARGMAX, RW, true>), grid, block, lds, s, p); break;
+    case 0u: hipLaunchKernelGGL((gemm_kernel<MT, 0u, RW, true>), grid, block, lds, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT, RW, true>), grid, block, lds, s, p); break;
+    case QDEC_ARGMAX: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_ARGMAX, RW, true>), grid, block, lds, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;
+}
+
+template <int MT, int RW, int RWG>
+hipError_t launch_direct_mt(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  if (flags & QDEC_GLU) {
+    if (p.rw != RWG) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemm_kernel<MT, QDEC_GLU, RWG, true>), grid, block, lds, s, p);
+    return hipSuccess;
+  }
+  if (p.rw != RW) return hipErrorInvalidValue;
+  return launch_direct<MT, RW>(p, flags, grid, block, lds, s);
+}
+
+}  // namespace
+
+int gemm_ring_direct(int mt, uint32_t flags) {
+  // (weights + mt activation fragments) x 4 registers per ring slot stays
+  // near 128 registers.
+  const bool glu = (flags & QDEC_GLU) != 0;
+  switch (mt) {
+    case 1: return glu ? 10 : 20;
+    case 2: return glu ? 8 : 10;
+    case 3: return glu ? 6 : 8;
+    case 4: return glu ? 4 : 8;
+    default: return 0;
+  }
 }
 
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
@@ -612,21 +676,17 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   dim3 block(64 * p.waves);
   const size_t lds = p.lds_bytes;
   if (p.xd) {
-    if (mt != 1) return hipErrorInvalidValue;
     GemmParams q = p;
     if (flags & QDEC_NORM_IN) {
       hipLaunchKernelGGL(rownorm_kernel, dim3(p.rows), block, 0, s, reinterpret_cast<const uint16_t *>(p.x),
                          reinterpret_cast<const uint16_t *>(p.norm_w), p.xn, p.k, p.eps);
       q.x = p.xn;
     }
-    if (flags & QDEC_GLU) {
-      if (p.rw != 10) return hipErrorInvalidValue;
-      hipLaunchKernelGGL((gemm_kernel<1, QDEC_GLU, 10, true>), grid, block, lds, s, q);
-      return hipSuccess;
-    }
-    switch (p.rw) {
-      case 16: return launch_direct<16>(q, flags, grid, block, lds, s);
-      case 20: return launch_direct<20>(q, flags, grid, block, lds, s);
+    switch (mt) {
+      case 1: return launch_direct_mt<1, 20, 10>(q, flags, grid, block, lds, s);
+      case 2: return launch_direct_mt<2, 10, 8>(q, flags, grid, block, lds, s);
+      case 3: return launch_direct_mt<3, 8, 6>(q, flags, grid, block, lds, s);
+      case 4: return launch_direct_mt<4, 8, 4>(q, flags, grid, block, lds, s);
       default: return hipErrorInvalidValue;
     }
   }

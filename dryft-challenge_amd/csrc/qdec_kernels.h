@@ -42,6 +42,7 @@ struct GemmParams {
 bool gemm_flags_supported(uint32_t flags);
 bool gemm_fast_path(const GemmParams &p, uint32_t flags);
 int gemm_ring(int ksw, uint32_t flags);
+int gemm_ring_direct(int mt, uint32_t flags);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 
 struct AttnParams {
