@@ -20,6 +20,9 @@ Printed JSON fields beyond the driver contract:
   cpu_baseline  the Transformers CPU greedy loop on the same checkpoint
                 (the reference's own oracle path), on a bounded sample;
   step_hbm      algorithmic bytes per step (weights + KV read/write) / step time;
+  batched       decode tok/s of configs[2] (batch 8, 1024 cached) and configs[3]
+                (batch 32, 4096 cached) on synthetic cache contents (skip
+                with --no-batched);
   speculation   BASELINE.json configs[4] through the same engine: batch 4,
                 1024-token prompts tiling a seeded 64-token motif with 10%
                 random substitutions, 512 new tokens, n-gram drafter (n=3,
@@ -136,6 +139,54 @@ def spec_bench(eng, vocab, batch=4, prompt_len=1024, new_tokens=512, seed=5):
             "token_identical": res[False][0] == res[True][0]}
 
 
+def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):
+    """Decode throughput of a batched configuration with synthetic cache
+    contents: the shape's KV cache is filled with random bf16 values (the
+    step's cost does not depend on them) instead of a real prefill, every
+    sequence sits at ``prompt_len`` cached tokens, and the timed replays walk
+    the workload's positions like the headline measurement."""
+    import torch
+    mc = eng.model.cfg
+    sh = eng._shape_for(batch, prompt_len, new_tokens)
+    st = sh.state
+    g = torch.Generator(device=eng.device).manual_seed(seed)
+    for cache in (st.k_cache, st.v_cache):
+        for layer in range(cache.shape[0]):
+            cache[layer].normal_(0.0, 1.0, generator=g)
+    st.ids[:batch].random_(0, mc.vocab, generator=g)
+    st.lens.fill_(prompt_len)
+    last_pos = prompt_len + new_tokens - 2
+    span = last_pos - prompt_len + 1
+    done = [0]
+
+    def run(k):
+        for _ in range(k):
+            if done[0] % span == 0 and done[0]:
+                st.lens.fill_(prompt_len)
+            done[0] += 1
+            sh.graph.replay()
+
+    run(warmup)
+    done[0] = 0
+    st.lens.fill_(prompt_len)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    run(steps)
+    e1.record()
+    torch.cuda.synchronize()
+    elapsed = max(time.perf_counter() - t0, e0.elapsed_time(e1) / 1e3)
+    kv_bytes = 2 * mc.n_layers * batch * mc.nkv * st.cap * mc.head_dim * 2
+    res = {"workload": f"qwen3-4b bf16 bs{batch} prompt{prompt_len} new{new_tokens}",
+           "tok_s": round(batch * steps / elapsed, 2), "ms_per_step": round(1e3 * elapsed / steps, 4),
+           "steps": steps, "cache": f"synthetic random K/V, {kv_bytes / 1e9:.1f} GB allocated"}
+    eng.shape = None
+    del sh, st
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(ckpt, cfg, prompt_len, budget_s=25.0):
     """Transformers' greedy loop on the host CPU over the same checkpoint
     (bf16, sdpa), bounded: a short prefill, then decode steps until the
@@ -197,6 +248,10 @@ def main():
     ap.add_argument("--ckpt", default=os.environ.get("QDEC_BENCH_CKPT", "/tmp/qdec_qwen3_4b_seed0"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-spec", action="store_true")
+    ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--pmc-role", choices=("qkv", "o", "gate_up", "down", "lm"),
+                    help="only launch this role's GEMM over every layer (5 rounds), then a "
+                         "512 MiB device copy as the counter calibration, for rocprofv3 --pmc")
     ap.add_argument("--cpu-prompt", type=int, default=64)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -224,6 +279,16 @@ def main():
     prompt = torch.randint(0, mc.vocab, (B, S), generator=g)
     sh = eng._shape_for(B, S, N)
     st = sh.state
+    if args.pmc_role:
+        st.prefill(prompt.to(eng.device))
+        time_gemm_role(eng, st, args.pmc_role, reps=5)
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=eng.device)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"pmc: {args.pmc_role} x {mc.n_layers} layers x 6 rounds, then 6 copies of {src.numel()} bytes")
+        return
     t0 = time.perf_counter()
     st.prefill(prompt.to(eng.device))
     torch.cuda.synchronize()
@@ -274,9 +339,19 @@ def main():
         roles[role] = round(time_gemm_role(eng, st, role) * 1e6, 2)
     log(f"other roles us/launch: {roles}")
 
+    batched = {}
+    if not args.no_batched:
+        del sh, st, graph
+        eng.shape = None
+        torch.cuda.empty_cache()
+        for name, seed in (("c3", 2), ("c4", 3)):
+            bB, bS, bN, _ = CONFIGS[name]
+            batched[f"batch{bB}"] = r = batched_decode(eng, bB, bS, bN, max(10, args.steps // 4), 3, seed)
+            log(f"{name}: {r}")
+
     spec = None
     if not args.no_spec:
-        del sh, st, graph
+        sh = st = graph = None
         eng.shape = None
         torch.cuda.empty_cache()
         spec = spec_bench(eng, mc.vocab)
@@ -316,6 +391,7 @@ def main():
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
         "role_us_per_launch": roles,
+        "batched": batched or None,
         "speculation": spec,
         "cpu_baseline": cpu,
     }
