@@ -44,6 +44,10 @@ for _p in (PKG, REPO):
         sys.path.insert(0, _p)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per gate/up launch at batch 1 measured with rocprofv3 counters
+# (bench.py --pmc-role gate_up; FETCH_SIZE x 1.99994 + WRITE_SIZE, the scale
+# factors read off a 512 MiB device copy).
+GATE_UP_TRAFFIC_BYTES = 99_898_266
 
 CONFIGS = {
     # name: (batch, prompt, new tokens, description)
@@ -386,7 +390,9 @@ def main():
                      "frac": round(step_tbs * 1e3 / HBM_PEAK_GBS, 4),
                      "bytes_per_step_mean": int(total_bytes / len(positions))},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a "
+                                       "512 MiB copy (profiles/gate_up_hbm_traffic_bs1.md)",
                      "kernel": "gemm_kernel<1, NORM_IN|GLU> (gate/up, 9728x2x2560)",
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
