@@ -4,7 +4,8 @@
 // Grid (chunk, kv head, sequence); a workgroup of 4 wavefronts per cell.
 //   1. Every wave issues the K/V loads of its first two 32-slot blocks, then
 //      the raw loads of its share of the query rows (row r = G*t + g goes to
-//      wave r % 4) and of the new key/value rows (t % 4); a lane holds two
+//      wave r % 4) and of the new key/value rows (t % 4), all before the
+//      sequence length arrives (no address depends on it); a lane holds two
 //      channels of a row, so the head RMSNorm is one wave reduction and the
 //      rotate_half partner sits in lane ^ 32.  Normalised, rotated queries
 //      go to LDS; new keys go to LDS in row layout, new values in the
@@ -77,14 +78,8 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   const int grp = lane >> 4;
   const int T = p.t_rows;
   const int R = T * G;
-  const int L = p.lens[b];
-  const int last = L + T - 1;
   const int c0 = c * p.chunk;
-  if (L < 0 || last >= p.cap) return;  // never index outside the cache slab
-  if (c0 > last) return;
-  const int n_active = last / p.chunk + 1;
-  const int c1 = c0 + p.chunk;                        // exclusive end of this chunk
-  const int nb = (min(c1, last + 1) - c0 + 31) / 32;  // blocks in this chunk
+  const int c1 = c0 + p.chunk;  // exclusive end of this chunk
   const int nq = p.nq, nkv = p.nkv;
   const int width = (nq + 2 * nkv) * D;
   const uint16_t *qkv = reinterpret_cast<const uint16_t *>(p.qkv);
@@ -113,33 +108,52 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
     for (int dt = 0; dt < DT; ++dt)
       f.vf[dt] = *reinterpret_cast<const uint4 *>(vblk + (size_t)(dt * 16 + col) * 8);
   };
+  // The first two blocks of this wave and the raw query / new key / new
+  // value rows go out before the sequence length is known: none of their
+  // addresses depends on it (blocks are issued when they lie inside the
+  // chunk and the cache; the ones past the length are never used).
+  auto block_in = [&](int j) { return 32 * j < p.chunk && c0 + 32 * (j + 1) <= p.cap; };
   Frag f0, f1;
-  if (wave < nb) load_block(c0 + 32 * wave, f0);
+  if (block_in(wave)) load_block(c0 + 32 * wave, f0);
   if constexpr (DB) {
-    if (wave + NW < nb) load_block(c0 + 32 * (wave + NW), f1);
+    if (block_in(wave + NW)) load_block(c0 + 32 * (wave + NW), f1);
   }
-
-  // ---- 1. raw query / new key / new value rows (clamped, straight-line loads).
-  const bool overlap = c1 > L;  // this chunk holds some of the new slots
-  uint32_t qraw[QPW], qcos[QPW], qsin[QPW];
+  uint32_t qraw[QPW], kraw[KPW], vraw[KPW];
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
     const int r = min(wave + NW * i, R - 1);
     const int t = r / G, hq = r % G;
     qraw[i] = *reinterpret_cast<const uint32_t *>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + 2 * lane);
+  }
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    const uint16_t *row = qkv + (size_t)(b * T + min(wave + NW * i, T - 1)) * width;
+    kraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + kvh) * D + 2 * lane);
+    vraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
+  }
+  const uint32_t qw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + 2 * lane);
+  const uint32_t kw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + 2 * lane);
+
+  const int L = p.lens[b];
+  const int last = L + T - 1;
+  if (L < 0 || last >= p.cap) return;  // never index outside the cache slab
+  if (c0 > last) return;
+  const int n_active = last / p.chunk + 1;
+  const int nb = (min(c1, last + 1) - c0 + 31) / 32;  // blocks in this chunk
+
+  // ---- 1. rotation tables of the rows' positions.
+  const bool overlap = c1 > L;  // this chunk holds some of the new slots
+  uint32_t qcos[QPW], qsin[QPW], kcos[KPW], ksin[KPW];
+#pragma unroll
+  for (int i = 0; i < QPW; ++i) {
+    const int t = min(wave + NW * i, R - 1) / G;
     qcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
     qsin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
   }
-  const uint32_t qw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + 2 * lane);
-  uint32_t kraw[KPW], vraw[KPW], kcos[KPW], ksin[KPW], kw = 0u;
   if (overlap) {
-    kw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + 2 * lane);
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       const int t = min(wave + NW * i, T - 1);
-      const uint16_t *row = qkv + (size_t)(b * T + t) * width;
-      kraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + kvh) * D + 2 * lane);
-      vraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
       kcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
       ksin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
     }

@@ -89,22 +89,23 @@ def rope_tables(cap, head_dim, theta):
 def role_plan(n, k, role):
     """(ksplit, waves, tiles_per_wg) of one projection role.
 
-    Output tiles are 16 columns.  Roles with few tiles (N = hidden) split k
-    across workgroups so the grid covers all 256 CUs; the others keep one
-    workgroup per tile.  Only (n, k, role) decide it."""
+    Output tiles are 16 columns, one workgroup per tile (8 per workgroup for
+    the lm_head), no k split across workgroups: a split's cross-workgroup
+    reduction cost more than it won back on MI355X.  The roles with few
+    tiles (N = hidden: O and down, 160 tiles for 256 CUs) run 8 waves per
+    workgroup, which doubles the weight blocks each busy CU keeps in flight
+    (O 7.6 -> 7.0 us, down 14.2 -> 13.5 us at batch 1; lm_head 152 -> 143 us
+    with 8 tiles per workgroup).  Only (n, k, role) decide it, never the
+    row count."""
     ks = k // 32
     ntiles = n // 16
-    waves = 4
     ksplit = 1
-    # O and down (N = hidden, 160 tiles) stream k in several register passes
-    # per wave instead of splitting it across workgroups: a pure streaming
-    # read of the same bytes is as fast with 160 x 4 long waves as with 4x
-    # more short ones, and no cross-workgroup reduction sits on the tail.
-    while (ks // ksplit) % waves:
+    waves = 8 if ntiles <= 256 else 4
+    while ks % waves:
         waves //= 2
     tiles = 1
     if role == "lm":
-        for cand in (4, 2, 1):
+        for cand in (8, 4, 2, 1):
             if ntiles % cand == 0:
                 tiles = cand
                 break
