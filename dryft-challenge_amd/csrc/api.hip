@@ -77,7 +77,6 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   const bool glu = (f & QDEC_GLU) != 0;
   const int ntiles = a->n / 16;
   if (a->tiles_per_wg < 1) return set_error(QDEC_EINVAL, "qdec_gemm: tiles_per_wg %d < 1", a->tiles_per_wg);
-  if (!arg && a->tiles_per_wg != 1) return set_error(QDEC_EINVAL, "qdec_gemm: tiles_per_wg > 1 needs QDEC_ARGMAX");
   if (ntiles % a->tiles_per_wg) return set_error(QDEC_EINVAL, "qdec_gemm: n/16=%d not divisible by tiles_per_wg %d", ntiles, a->tiles_per_wg);
   if (arg && a->ksplit != 1) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: QDEC_ARGMAX needs ksplit 1");
   if (need_scratch && (!a->x || !a->w)) return set_error(QDEC_EINVAL, "qdec_gemm: null x or w");

@@ -68,7 +68,7 @@ def _gemm(**kw):
     (dict(ksplit=3), -1, "ksplit"),
     (dict(flags=capi.GLU), -3, "not supported"),
     (dict(flags=capi.ARGMAX | capi.NORM_IN, ksplit=2), -3, "ksplit 1"),
-    (dict(tiles_per_wg=2), -1, "tiles_per_wg"),
+    (dict(tiles_per_wg=3), -1, "tiles_per_wg"),
     (dict(x=8), -2, "aligned"),
     (dict(out=None), -1, "null out"),
 ])
