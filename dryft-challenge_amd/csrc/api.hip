@@ -79,7 +79,18 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   if (a->tiles_per_wg < 1) return set_error(QDEC_EINVAL, "qdec_gemm: tiles_per_wg %d < 1", a->tiles_per_wg);
   if (ntiles % a->tiles_per_wg) return set_error(QDEC_EINVAL, "qdec_gemm: n/16=%d not divisible by tiles_per_wg %d", ntiles, a->tiles_per_wg);
   if (arg && a->ksplit != 1) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: QDEC_ARGMAX needs ksplit 1");
-  if (need_scratch && (!a->x || !a->w)) return set_error(QDEC_EINVAL, "qdec_gemm: null x or w");
+  const qdec_attn_args *xa = a->x_attn;
+  if (xa) {
+    if (f & QDEC_NORM_IN) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_attn with NORM_IN");
+    if (!xa->out_partials) return set_error(QDEC_EINVAL, "qdec_gemm: x_attn call was not made with out_partials");
+    if (xa->head_dim != 128 || xa->nkv < 1 || xa->nq != 4 * xa->nkv || xa->chunk < 32 || xa->cap < 32 ||
+        xa->t_rows < 1 || xa->batch < 1)
+      return set_error(QDEC_EINVAL, "qdec_gemm: x_attn shape");
+    if (a->rows != xa->batch * xa->t_rows || a->k != xa->nq * xa->head_dim)
+      return set_error(QDEC_EINVAL, "qdec_gemm: x_attn rows %d / k %d do not match the attention call", a->rows, a->k);
+    if (need_scratch && (!xa->partial || !xa->lens)) return set_error(QDEC_EINVAL, "qdec_gemm: x_attn needs partial and lens");
+  }
+  if (need_scratch && ((!a->x && !xa) || !a->w)) return set_error(QDEC_EINVAL, "qdec_gemm: null x or w");
   if (need_scratch && (f & QDEC_NORM_IN) && !a->norm_w) return set_error(QDEC_EINVAL, "qdec_gemm: NORM_IN needs norm_w");
   if (need_scratch && (f & QDEC_RES_OUT) && !a->res) return set_error(QDEC_EINVAL, "qdec_gemm: RES_OUT needs res");
   if (need_scratch && !(f & (QDEC_RES_OUT | QDEC_ARGMAX)) && !a->out) return set_error(QDEC_EINVAL, "qdec_gemm: null out");
@@ -136,6 +147,20 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     p->lds_all = 0;
     p->lds_bytes = head + red_bytes;
   }
+  p->amerge = 0;
+  p->apart = nullptr;
+  p->alens = nullptr;
+  if (xa) {
+    if (!p->xfast || p->xd || a->ksplit != 1)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_attn needs activations staged from registers (rows %d)", a->rows);
+    p->amerge = 1;
+    p->apart = xa->partial;
+    p->alens = xa->lens;
+    p->a_t_rows = xa->t_rows;
+    p->a_nkv = xa->nkv;
+    p->a_chunk = xa->chunk;
+    p->a_nchunks = (xa->cap + xa->chunk - 1) / xa->chunk;
+  }
   size_t pb = 0, cb = 0, xn_off = 0;
   gemm_scratch(a, *p, &pb, &cb, &xn_off);
   if (need_scratch && pb && !a->partial) return set_error(QDEC_EINVAL, "qdec_gemm: this call needs a partial workspace");
@@ -157,13 +182,16 @@ static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) 
   if (a->cap < 32 || a->cap % 32) return set_error(QDEC_EINVAL, "qdec_attn: cap %d not a positive multiple of 32", a->cap);
   if (a->chunk < 32 || a->chunk % 32) return set_error(QDEC_EINVAL, "qdec_attn: chunk %d not a positive multiple of 32", a->chunk);
   if (a->waves != 4) return set_error(QDEC_EINVAL, "qdec_attn: waves %d (the kernel runs 4 wavefronts)", a->waves);
+  if (a->out_partials != 0 && a->out_partials != 1)
+    return set_error(QDEC_EINVAL, "qdec_attn: out_partials %d not 0 or 1", a->out_partials);
   const int nchunks = (a->cap + a->chunk - 1) / a->chunk;
   if (!need_scratch) goto fill;
   if (!a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->lens || !a->k_cache ||
       !a->v_cache || !a->out)
     return set_error(QDEC_EINVAL, "qdec_attn: null pointer argument");
-  if (nchunks > 1 && (!a->partial || !a->counters))
+  if (nchunks > 1 && !a->out_partials && (!a->partial || !a->counters))
     return set_error(QDEC_EINVAL, "qdec_attn: more than one chunk needs partial and counters");
+  if (a->out_partials && !a->partial) return set_error(QDEC_EINVAL, "qdec_attn: out_partials needs partial");
   if (!aligned16(a->qkv) || !aligned16(a->q_norm_w) || !aligned16(a->k_norm_w) || !aligned16(a->cos_tab) ||
       !aligned16(a->sin_tab) || !aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->out))
     return set_error(QDEC_EALIGN, "qdec_attn: tensor pointers must be 16-byte aligned");
@@ -176,6 +204,7 @@ fill:
   p->scale_log2 = a->sm_scale * 1.4426950408889634f;
   p->batch = a->batch; p->t_rows = a->t_rows; p->nq = a->nq; p->nkv = a->nkv;
   p->cap = a->cap; p->chunk = a->chunk; p->nchunks = nchunks; p->waves = a->waves;
+  p->out_partials = a->out_partials;
   return QDEC_OK;
 }
 
@@ -246,9 +275,10 @@ int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes, size_t *
   const int rc = plan_attn(a, &p, false);
   if (rc != QDEC_OK) return rc;
   const size_t R = (size_t)a->t_rows * (a->nq / a->nkv);
+  const bool parts = p.nchunks > 1 || a->out_partials;
   if (partial_bytes)
-    *partial_bytes = p.nchunks > 1 ? sizeof(float) * (size_t)a->batch * a->nkv * p.nchunks * R * (a->head_dim + 2) : 0;
-  if (counter_bytes) *counter_bytes = p.nchunks > 1 ? sizeof(uint32_t) * (size_t)a->batch * a->nkv : 0;
+    *partial_bytes = parts ? sizeof(float) * (size_t)a->batch * a->nkv * p.nchunks * R * (a->head_dim + 2) : 0;
+  if (counter_bytes) *counter_bytes = (p.nchunks > 1 && !a->out_partials) ? sizeof(uint32_t) * (size_t)a->batch * a->nkv : 0;
   return QDEC_OK;
 }
 

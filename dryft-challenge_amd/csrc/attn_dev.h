@@ -21,7 +21,9 @@
 //      from LDS with masks; slots past the last new one are zero.
 //   3. The waves merge in LDS in wave order; a sequence that needs one chunk
 //      is written out directly, otherwise the workgroup stores (acc, m, l) and
-//      the last chunk to arrive merges all chunks in chunk order.
+//      the last chunk to arrive merges all chunks in chunk order -- or, with
+//      out_partials, every chunk stores its partials and the consuming GEMM
+//      merges them (gemm.hip, attn_merge8) with the same arithmetic.
 // Block-to-wave dealing and chunk boundaries are keyed to absolute slot
 // numbers, and every row's arithmetic is the same whatever t_rows is, so
 // verify rows reproduce plain decode bit for bit.
@@ -328,6 +330,10 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   }
 
   // ---- 3. merge the waves (wave order), then output or chunk partials.
+  // A sequence that needs one chunk is written out directly, unless the
+  // caller asked for partials (a GEMM merging them in its prologue, with the
+  // arithmetic of the merge below: one chunk gives tot * 1 / (Lrow * 1)).
+  const bool direct = n_active == 1 && !p.out_partials;
   uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
   const size_t cstride = (size_t)R * (D + 2);  // floats per chunk partial: acc [R][D], m [R], l [R]
   float *part_b = p.partial + ((size_t)b * nkv + kvh) * p.nchunks * cstride;
@@ -366,7 +372,7 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
 #pragma unroll
       for (int w2 = 1; w2 < NW; ++w2) tot += s_acc[(w2 * DT + dt) * 64 + lane] * scw[w2];
       if (r < R) {
-        if (n_active == 1) {
+        if (direct) {
           const int t = r / G, hq = r % G;
           uint16_t *dst = out + (size_t)(b * T + t) * nq * D + (size_t)(kvh * G + hq) * D;
           uint2 o;
@@ -378,12 +384,12 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
         }
       }
     }
-    if (n_active > 1 && wave == 0 && grp == 0 && r < R) {
+    if (!direct && wave == 0 && grp == 0 && r < R) {
       store_coherent(part + (size_t)R * D + r, M);
       store_coherent(part + (size_t)R * D + R + r, Lrow);
     }
   }
-  if (n_active == 1) return;
+  if (direct || p.out_partials) return;  // done, or the consuming GEMM merges
   if (!arrive_last(p.counters + (size_t)b * nkv + kvh, (uint32_t)n_active, s_flag)) return;
 
   // Merge chunks 0..n_active-1 in order (chunks a row cannot see have

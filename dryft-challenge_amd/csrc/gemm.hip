@@ -85,6 +85,69 @@ __device__ __forceinline__ uint4 norm8(const uint4 &xv, const uint4 &nv, float r
   return pack8(f);
 }
 
+// Activation vector (8 consecutive elements from k index kk) of row m,
+// merged from the attention chunk partials the previous launch left with
+// out_partials (attn_dev.h: per (sequence, kv head, chunk) acc [R][128],
+// max [R], sum [R], R = t_rows * 4).  The same operations in the same order
+// as the attention's own chunk merge, so the bf16 result is bit-identical
+// to the output that call would have written.
+__device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk) {
+  constexpr int D = 128, G = 4, CB = 8;
+  const int T = p.a_t_rows, R = T * G;
+  const int b = m / T, t = m - b * T;
+  const int h = kk / D, d0 = kk - h * D;
+  const int kvh = h / G;
+  const int r = t * G + (h - kvh * G);
+  const size_t cstride = (size_t)R * (D + 2);
+  const float *part_b = p.apart + ((size_t)b * p.a_nkv + kvh) * p.a_nchunks * cstride;
+  const int n_active = (p.alens[b] + T - 1) / p.a_chunk + 1;
+  const float NEG_INF = -__builtin_huge_valf();
+  float mc[CB], lc[CB];
+  f32x4_t a0[CB], a1[CB];
+  auto load_group = [&](int cc) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const float *pr = part_b + (size_t)min(cc + j, n_active - 1) * cstride;
+      mc[j] = pr[(size_t)R * D + r];
+      lc[j] = pr[(size_t)R * D + R + r];
+      a0[j] = *reinterpret_cast<const f32x4_t *>(pr + (size_t)r * D + d0);
+      a1[j] = *reinterpret_cast<const f32x4_t *>(pr + (size_t)r * D + d0 + 4);
+    }
+  };
+  load_group(0);
+  float mmax = NEG_INF;
+#pragma unroll
+  for (int j = 0; j < CB; ++j)
+    if (j < n_active) mmax = fmaxf(mmax, mc[j]);
+  for (int cc = CB; cc < n_active; cc += CB) {
+    float mg[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) mg[j] = part_b[(size_t)min(cc + j, n_active - 1) * cstride + (size_t)R * D + r];
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+      if (cc + j < n_active) mmax = fmaxf(mmax, mg[j]);
+  }
+  float lsum = 0.f;
+  f32x4_t o0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, o1 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int cc = 0; cc < n_active; cc += CB) {
+    if (cc > 0) load_group(cc);
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      if (cc + j >= n_active || mc[j] == NEG_INF) continue;
+      const float w = exp2f(mc[j] - mmax);
+      lsum += lc[j] * w;
+      o0 += a0[j] * w;
+      o1 += a1[j] * w;
+    }
+  }
+  uint4 v;
+  v.x = pack2(o0[0] / lsum, o0[1] / lsum);
+  v.y = pack2(o0[2] / lsum, o0[3] / lsum);
+  v.z = pack2(o1[0] / lsum, o1[1] / lsum);
+  v.w = pack2(o1[2] / lsum, o1[3] / lsum);
+  return v;
+}
+
 template <int MT, uint32_t FLAGS, int RW, bool XD>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -184,8 +247,12 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         const int vr = tid + j * nthr;
         const bool ok = m < rows && vr < per_row;
         const int mm = ok ? m : 0, vv = ok ? vr : 0;
-        const uint4 v = *reinterpret_cast<const uint4 *>(X + (size_t)mm * p.k + ks_wg * 32 + 8 * vv);
-        xr[m][j] = ok ? v : zero4();
+        if (!XD && !NORM && p.amerge) {
+          xr[m][j] = ok ? attn_merge8(p, mm, ks_wg * 32 + 8 * vv) : zero4();
+        } else {
+          const uint4 v = *reinterpret_cast<const uint4 *>(X + (size_t)mm * p.k + ks_wg * 32 + 8 * vv);
+          xr[m][j] = ok ? v : zero4();
+        }
       }
     issue_first();
     if constexpr (NORM) {

@@ -37,6 +37,12 @@ struct GemmParams {
   int rw;        // weight ring registers per wave (window path), 0 = passes
   int xd;        // window path with B fragments loaded straight from x (no LDS staging)
   uint16_t *xn;  // NORM_IN with xd: normalised copy of x (workspace)
+  // Activations merged from attention chunk partials (x_attn): layout of
+  // attn_dev.h, head_dim 128, 4 query heads per kv head.
+  int amerge;
+  const float *apart;
+  const int32_t *alens;
+  int a_t_rows, a_nkv, a_chunk, a_nchunks;
   size_t lds_bytes;
 };
 bool gemm_flags_supported(uint32_t flags);
@@ -60,6 +66,7 @@ struct AttnParams {
   float eps;
   float scale_log2;  // log2(e) / sqrt(head_dim)
   int batch, t_rows, nq, nkv, cap, chunk, nchunks, waves;
+  int out_partials;
 };
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 

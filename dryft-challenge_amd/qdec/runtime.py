@@ -22,6 +22,7 @@ row count: that keeps every output element's summation order the same for a
 1-row and a 36-row call (the basis of lossless speculation).
 """
 
+import ctypes
 import math
 
 import torch
@@ -31,6 +32,8 @@ from . import capi
 GEMM_MAX_ROWS = 64
 ATTN_MAX_T = 16
 ATTN_WAVES = 4
+# Plain decode up to this batch merges attention chunks in the O projection.
+MERGE_IN_O_MAX_BATCH = 4
 # Loss-free speculation needs identical arithmetic in the plain and verify
 # steps, so attention chunking depends on (batch, capacity) only.
 
@@ -235,13 +238,20 @@ class DecodeState:
         self.gemm_partial = torch.zeros((max(gw, 16) // 4 + 4,), dtype=torch.float32, device=dev)
         self.gemm_counters = torch.zeros((max(gc, 4) // 4 + 4,), dtype=torch.int32, device=dev)
         aw, ac = self.lib.attn_workspace(self._attn_args(0, self.max_t))
+        aw = max(aw, self.lib.attn_workspace(self._attn_args(0, 1, partials=True))[0])
         self.attn_partial = torch.zeros((max(aw, 16) // 4 + 4,), dtype=torch.float32, device=dev)
         self.attn_counters = torch.zeros((max(ac, 4) // 4 + 4,), dtype=torch.int32, device=dev)
         self._gemm_cache = {}
         self._attn_cache = {}
 
     # ----------------------------------------------------------- arguments
-    def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None):
+    def _merge_in_o(self, t_rows):
+        """Plain decode of up to 4 sequences: the attention leaves its chunk
+        partials and the O projection merges them while staging its
+        activations (no arrival pass); bit-identical to the merged output."""
+        return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH
+
+    def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None, x_attn=None):
         m, c = self.model, self.model.cfg
         ksplit, waves, tiles = m.plans[role]
         a = capi.GemmArgs()
@@ -253,6 +263,9 @@ class DecodeState:
         elif role == "o":
             a.x, a.w, a.res = self.attn_out.data_ptr(), m.w_o[layer].data_ptr(), self.h.data_ptr()
             a.n, a.k, a.flags = c.hidden, c.nq * c.head_dim, capi.RES_OUT
+            if x_attn is not None:
+                a.x_attn = ctypes.addressof(x_attn)
+                a._x_attn = x_attn  # keeps the referenced struct alive
         elif role == "gate_up":
             a.x, a.w, a.out = self.h.data_ptr(), m.w_gu[layer].data_ptr(), self.act.data_ptr()
             a.norm_w = m.post_w[layer].data_ptr()
@@ -273,9 +286,10 @@ class DecodeState:
             a.counters = self.gemm_counters.data_ptr()
         return a
 
-    def _attn_args(self, layer, t_rows):
+    def _attn_args(self, layer, t_rows, partials=False):
         m, c = self.model, self.model.cfg
         a = capi.AttnArgs()
+        a.out_partials = 1 if partials else 0
         a.qkv, a.q_norm_w, a.k_norm_w = self.qkv.data_ptr(), m.q_norm[layer].data_ptr(), m.k_norm[layer].data_ptr()
         a.cos_tab, a.sin_tab, a.lens = self.cos.data_ptr(), self.sin.data_ptr(), self.lens.data_ptr()
         a.k_cache = self.k_cache[layer].data_ptr()
@@ -308,10 +322,11 @@ class DecodeState:
         e.ids, e.emb, e.h = self.ids.data_ptr(), m.emb.data_ptr(), self.h.data_ptr()
         e.rows, e.hidden, e.vocab = rows, c.hidden, c.vocab
         lib.embed(e, s)
+        pm = self._merge_in_o(t_rows)
         for i in range(c.n_layers):
             lib.gemm(self._cached_gemm("qkv", i, rows), s)
-            lib.attn(self._cached_attn(i, t_rows), s)
-            lib.gemm(self._cached_gemm("o", i, rows), s)
+            lib.attn(self._cached_attn(i, t_rows, pm), s)
+            lib.gemm(self._cached_gemm("o", i, rows, self._cached_attn(i, t_rows, pm) if pm else None), s)
             lib.gemm(self._cached_gemm("gate_up", i, rows), s)
             lib.gemm(self._cached_gemm("down", i, rows), s)
         if lm_head:
@@ -319,19 +334,19 @@ class DecodeState:
                                 lens_inc=self.lens if (advance and t_rows == 1) else None)
             lib.gemm(a, s)
 
-    def _cached_gemm(self, role, layer, rows):
-        key = (role, layer, rows)
+    def _cached_gemm(self, role, layer, rows, x_attn=None):
+        key = (role, layer, rows, x_attn is not None)
         a = self._gemm_cache.get(key)
         if a is None:
-            a = self._gemm_args(role, layer, rows)
+            a = self._gemm_args(role, layer, rows, x_attn=x_attn)
             self._gemm_cache[key] = a
         return a
 
-    def _cached_attn(self, layer, t_rows):
-        key = (layer, t_rows)
+    def _cached_attn(self, layer, t_rows, partials=False):
+        key = (layer, t_rows, partials)
         a = self._attn_cache.get(key)
         if a is None:
-            a = self._attn_args(layer, t_rows)
+            a = self._attn_args(layer, t_rows, partials)
             self._attn_cache[key] = a
         return a
 

@@ -103,6 +103,8 @@ int qdec_embed(const qdec_embed_args *a, qdec_stream_t stream);
 
 /* ------------------------------------------------------------ skinny GEMM */
 
+struct qdec_attn_args;  /* below: the attention call a GEMM may take its x from */
+
 /* y[m, n] = sum_k x'[m, k] * W[n, k] over the tiled weight, for m < rows
  * (1 <= rows <= 64), fp32 accumulation, one rounding to bf16, then:
  *   plain   : out = bf16(y)
@@ -135,7 +137,15 @@ typedef struct {
   uint32_t flags;
   int32_t ksplit;       /* workgroups sharing one output tile along k (>= 1) */
   int32_t waves;        /* wavefronts per workgroup, splitting its k range (1..8) */
-  int32_t tiles_per_wg; /* output tiles per workgroup, ARGMAX only (>= 1) */
+  int32_t tiles_per_wg; /* output tiles per workgroup (>= 1, divides n/16) */
+  /* NULL, or an attention call made with out_partials = 1: then x is not
+   * read; activation row m = b*t_rows + t is the merge of that call's chunk
+   * partials for sequence b, query row t (k = nq*head_dim, rows =
+   * batch*t_rows), bit-identical to what the attention would have written to
+   * its out.  Needs activations staged from registers (rows <= 4 and the
+   * workgroup's k range within 2 vectors per thread); QDEC_EUNSUPPORTED
+   * otherwise. */
+  const struct qdec_attn_args *x_attn;
 } qdec_gemm_args;
 int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream);
 /* Scratch sizes (bytes) a qdec_gemm call with these arguments needs. */
@@ -155,12 +165,13 @@ int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes,
  * Slots are processed in chunks of `chunk` slots keyed to absolute slot
  * numbers, one workgroup per (chunk, kv head, sequence); the last workgroup
  * of a (sequence, kv head) to finish merges the chunk partials in chunk
- * order.  A row's result therefore does not depend on t_rows (for a fixed
+ * order (or, with out_partials, the consuming GEMM merges them in the same
+ * order and arithmetic).  A row's result therefore does not depend on t_rows (for a fixed
  * chunk and waves).
  * Replaces fused.attention_fused (engine/kernels/fused.py:360-479),
  * ops.qkv_post + ops.DecodeAttention (engine/kernels/ops.py:84-431) and the
  * multi-row verify attention of notes/v10/spec.py:111-182. */
-typedef struct {
+typedef struct qdec_attn_args {
   const void *qkv;      /* [batch*t_rows, (nq + 2*nkv)*head_dim] bf16 */
   const void *q_norm_w; /* [head_dim] bf16 */
   const void *k_norm_w; /* [head_dim] bf16 */
@@ -183,6 +194,10 @@ typedef struct {
   int32_t chunk;        /* slots per workgroup, multiple of 32 */
   int32_t waves;        /* wavefronts per workgroup: must be 4; blocks of 32
                            slots are dealt to them round robin */
+  int32_t out_partials; /* 0: merged rows to out.  1: every chunk leaves its
+                           unnormalised (acc, max, sum) in partial, out is not
+                           written, and a qdec_gemm with x_attn = these
+                           arguments merges them (no arrival pass) */
 } qdec_attn_args;
 int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream);
 int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,

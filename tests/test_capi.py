@@ -26,7 +26,7 @@ def test_structs_match_header_fields():
     for cname, st in (("qdec_embed_args", capi.EmbedArgs), ("qdec_gemm_args", capi.GemmArgs),
                       ("qdec_attn_args", capi.AttnArgs), ("qdec_draft_args", capi.DraftArgs),
                       ("qdec_accept_args", capi.AcceptArgs)):
-        body = re.search(r"typedef struct \{([^{}]*)\}\s*" + cname + ";", text).group(1)
+        body = re.search(r"typedef struct (?:\w+ )?\{([^{}]*)\}\s*" + cname + ";", text).group(1)
         fields = re.findall(r"\*?\s*(\w+)\s*;", body)
         assert fields == [f[0] for f in st._fields_], cname
 

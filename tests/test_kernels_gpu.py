@@ -8,6 +8,7 @@ least 98% of the bf16 outputs bit-identical.  Row- and t_rows-invariance is
 checked bit for bit: it is what makes speculative decoding lossless.
 """
 
+import ctypes
 import math
 import zlib
 
@@ -263,6 +264,53 @@ def attn_case(lib, B, T, lens, cap, chunk, seed):
     assert int(cnt.abs().sum()) == 0
     return dict(qkv=qkv, qn=qn, kn=kn, kc=kc, vc=vc, cos=cos, sin=sin, lens=lens, out=out.cpu(),
                 k_after=dk.cpu(), v_after=dv.cpu())
+
+
+@pytest.mark.parametrize("B,lens,cap,chunk", [(1, [640], 800, 128), (1, [100], 800, 128), (3, [700, 31, 257], 800, 128),
+                                               (2, [200, 90], 256, 256), (1, [4000], 4384, 256)])
+def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chunk):
+    """Attention with out_partials + an O projection reading x_attn gives the
+    same bits as the attention's own merged output fed to the O projection
+    (one chunk and several; the attention's out buffer is left untouched)."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    g = torch.Generator().manual_seed(sum(lens) + B)
+    W = (NQ + 2 * NKV) * D
+    qkv = (torch.randn(B, W, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    qn = bf16(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    kn = bf16(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    kc0 = torch.randn(B, NKV, cap, D, generator=g).to(torch.bfloat16)
+    vc0 = v_layout(torch.randn(B, NKV, cap, D, generator=g).to(torch.bfloat16))
+    cos, sin = rope_tables(cap, D, 5e6, "bf16")
+    dcos, dsin = cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
+    dl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    Wo = pack(lib, rnd(H, NQ * D, scale=0.02, seed=5).to(DEV))
+    res0 = rnd(B, H, scale=2.0, seed=6).to(DEV)
+    ks, waves, _ = role_plan(H, NQ * D, "o")
+    results = []
+    for partials in (0, 1):
+        kc, vc = kc0.to(DEV), vc0.to(DEV)
+        out = torch.full((B, NQ * D), 7.0, dtype=torch.bfloat16, device=DEV)
+        a = capi.AttnArgs(qkv=qkv.data_ptr(), q_norm_w=qn.data_ptr(), k_norm_w=kn.data_ptr(), cos_tab=dcos.data_ptr(),
+                          sin_tab=dsin.data_ptr(), lens=dl.data_ptr(), k_cache=kc.data_ptr(), v_cache=vc.data_ptr(),
+                          out=out.data_ptr(), eps=1e-6, sm_scale=D ** -0.5, batch=B, t_rows=1, nq=NQ, nkv=NKV,
+                          head_dim=D, cap=cap, chunk=chunk, waves=4, out_partials=partials)
+        pb, cb = lib.attn_workspace(a)
+        part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
+        cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
+        a.partial, a.counters = part.data_ptr(), cnt.data_ptr()
+        lib.attn(a, stream())
+        res = res0.clone()
+        o = capi.GemmArgs(x=out.data_ptr(), w=Wo.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=B, n=H, k=NQ * D,
+                          flags=capi.RES_OUT, ksplit=ks, waves=waves, tiles_per_wg=1)
+        if partials:
+            o.x_attn = ctypes.addressof(a)
+        lib.gemm(o, stream())
+        torch.cuda.synchronize()
+        if partials:
+            assert bool((out == 7.0).all()), "out_partials must leave out untouched"
+        results.append(res.cpu())
+    assert torch.equal(results[0].view(torch.int16), results[1].view(torch.int16))
 
 
 def attn_oracle(c, B, T):
