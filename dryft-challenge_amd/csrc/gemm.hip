@@ -354,17 +354,22 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       if constexpr (!XD) {
         // Slot r always holds k step r (mod RW): refill with k step i + RW of
         // this tile while it exists, else the same offset into the next tile;
-        // none past the last tile.
+        // none past the last tile.  The chunk's LDS reads are all issued
+        // before its first MFMA, so their latency is paid once per chunk.
         for (int i0 = 0; i0 < p.ksw; i0 += RW) {
           const bool same_tile = i0 + RW < p.ksw;
           const bool refill = same_tile || more_tiles;
           const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + 1, i0 + RW - p.ksw);
+          uint4 bq[RW];
 #pragma unroll
           for (int r = 0; r < RW; ++r) {
             const uint4 bx = *reinterpret_cast<const uint4 *>(xs + (i0 + r) * 32);
-            const uint4 b = xrow_ok ? bx : zero4();
+            bq[r] = xrow_ok ? bx : zero4();
+          }
 #pragma unroll
-            for (int a = 0; a < NACC; ++a) acc[a][0] = mfma16x16x32(wb[a][r], b, acc[a][0]);
+          for (int r = 0; r < RW; ++r) {
+#pragma unroll
+            for (int a = 0; a < NACC; ++a) acc[a][0] = mfma16x16x32(wb[a][r], bq[r], acc[a][0]);
             if (refill) {
               wb[0][r] = qn[r * 64];
               if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
