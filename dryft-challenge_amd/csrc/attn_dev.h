@@ -102,13 +102,13 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
     const int slot_b = slot_a + 4;
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
-      f.ka[s] = *reinterpret_cast<const uint4 *>(kc + (size_t)slot_a * D + s * 32 + grp * 8);
-      f.kb[s] = *reinterpret_cast<const uint4 *>(kc + (size_t)slot_b * D + s * 32 + grp * 8);
+      f.ka[s] = ld_nt(kc + (size_t)slot_a * D + s * 32 + grp * 8);
+      f.kb[s] = ld_nt(kc + (size_t)slot_b * D + s * 32 + grp * 8);
     }
     const uint16_t *vblk = vc + ((size_t)((s0 >> 3) + grp) * D) * 8;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      f.vf[dt] = *reinterpret_cast<const uint4 *>(vblk + (size_t)(dt * 16 + col) * 8);
+      f.vf[dt] = ld_nt(vblk + (size_t)(dt * 16 + col) * 8);
   };
   // The first two blocks of this wave and the raw query / new key / new
   // value rows go out before the sequence length is known: none of their

