@@ -92,14 +92,15 @@ def rope_tables(cap, head_dim, theta):
 def role_plan(n, k, role):
     """(ksplit, waves, tiles_per_wg) of one projection role.
 
-    Output tiles are 16 columns, one workgroup per tile (8 per workgroup for
+    Output tiles are 16 columns, one workgroup per tile (4 per workgroup for
     the lm_head), no k split across workgroups: a split's cross-workgroup
     reduction cost more than it won back on MI355X.  The roles with few
     tiles (N = hidden: O and down, 160 tiles for 256 CUs) run 8 waves per
     workgroup, which doubles the weight blocks each busy CU keeps in flight
-    (O 7.6 -> 7.0 us, down 14.2 -> 13.5 us at batch 1; lm_head 152 -> 143 us
-    with 8 tiles per workgroup).  Only (n, k, role) decide it, never the
-    row count."""
+    (O 7.6 -> 7.0 us, down 14.2 -> 13.5 us at batch 1).  The lm_head runs 4
+    tiles per workgroup (137 us against 144 us with 8 and 146 us with 2,
+    non-temporal weight loads).  Only (n, k, role) decide it, never the row
+    count."""
     ks = k // 32
     ntiles = n // 16
     ksplit = 1
@@ -108,7 +109,7 @@ def role_plan(n, k, role):
         waves //= 2
     tiles = 1
     if role == "lm":
-        for cand in (8, 4, 2, 1):
+        for cand in (4, 2, 1):
             if ntiles % cand == 0:
                 tiles = cand
                 break
