@@ -501,7 +501,8 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
             if (m < rows) store_coherent4(p.partial + ((size_t)(a * p.ksplit + split) * rows + m) * p.n + n0, acc[a][mt]);
           }
       }
-      if (!arrive_last(p.counters + tile, (uint32_t)p.ksplit, s_flag)) return;
+      // Not the last split of this tile: go on with the workgroup's next tile.
+      if (!arrive_last(p.counters + tile, (uint32_t)p.ksplit, s_flag)) continue;
       if (wave == 0) {
 #pragma unroll
         for (int a = 0; a < NACC; ++a)

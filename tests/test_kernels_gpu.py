@@ -69,7 +69,7 @@ class Gemm:
         self.lib, self.capi = lib, capi
         self.flags, self.n, self.k = flags, n, k
         self.ksplit, self.waves, self.tiles = ksplit, waves, tiles
-        self.partial = torch.zeros(4 << 20, dtype=torch.float32, device=DEV)
+        self.partial = torch.zeros(8 << 20, dtype=torch.float32, device=DEV)
         self.counters = torch.zeros(16384, dtype=torch.int32, device=DEV)
 
     def __call__(self, x, w_tiled, out=None, res=None, norm_w=None, ids=None, lens=None):
@@ -190,6 +190,33 @@ def test_gemm_row_invariance_bitexact(lib, role):
                      list(range(40, 49)), [7] * 12):
         part = run(rows_idx)
         assert torch.equal(part.view(torch.int16), full[rows_idx].view(torch.int16)), rows_idx
+
+
+@pytest.mark.parametrize("rows", [3, 32])
+@pytest.mark.parametrize("role", ["gate_up", "down"])
+def test_gemm_split_multi_tile_vs_oracle(lib, role, rows):
+    """k split across workgroups that own several output tiles each: a
+    workgroup that is not the last split of one tile goes on to the next."""
+    from qdec import capi
+    n, k, flags = {"gate_up": (I, H, capi.NORM_IN | capi.GLU), "down": (H, I, capi.RES_OUT)}[role]
+    ks, waves, tiles = (4, 4, 8) if role == "gate_up" else (8, 2, 4)
+    seed = (zlib.crc32(role.encode()) + 13 * rows) % 1000
+    x = rnd(rows, k, scale=3.0, seed=seed)
+    W = rnd(2 * n if flags & capi.GLU else n, k, scale=0.02, seed=seed + 1)
+    nw = bf16(1 + 0.2 * torch.randn(k, generator=torch.Generator().manual_seed(seed + 2))).to(torch.bfloat16)
+    g = Gemm(lib, flags, n, k, ksplit=ks, waves=waves, tiles=tiles)
+    xd, Wt = x.to(DEV), pack(lib, W.to(DEV))
+    if flags & capi.GLU:
+        xin = rms_norm(x.float(), nw.float(), 1e-6)
+        out = torch.zeros(rows, n, dtype=torch.bfloat16, device=DEV)
+        g(xd, Wt, out=out, norm_w=nw.to(DEV))
+        ref = silu_mul(linear(xin, W[:n].float()), linear(xin, W[n:].float()))
+    else:
+        res0 = rnd(rows, n, scale=2.0, seed=seed + 3)
+        out = res0.to(DEV).clone()
+        g(xd, Wt, res=out)
+        ref = bf16(res0.float() + linear(x.float(), W.float()))
+    agree(out, ref, min_exact=0.97 if flags & capi.GLU else 0.98)
 
 
 def test_lmhead_argmax_and_ties(lib):
