@@ -50,9 +50,9 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
     cb = sizeof(uint32_t) * (size_t)ntiles;
   }
   size_t off = 0;
-  if (p.xd && (a->flags & QDEC_NORM_IN)) {
+  if (p.xd && ((a->flags & QDEC_NORM_IN) || p.xt)) {
     off = (pb + 255) & ~(size_t)255;
-    pb = off + sizeof(uint16_t) * (size_t)a->rows * a->k;
+    pb = off + sizeof(uint16_t) * (size_t)(p.xt ? p.xt * 16 : a->rows) * a->k;
   }
   *partial_bytes = pb;
   *counter_bytes = cb;
@@ -109,6 +109,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->eps = a->eps; p->rows = a->rows; p->n = a->n; p->k = a->k;
   p->ksplit = a->ksplit; p->waves = a->waves; p->tiles_per_wg = a->tiles_per_wg;
   p->KS = KS;
+  p->xt = 0;
   p->ksw = KS / a->ksplit / a->waves;
   p->up_tiles = ntiles;
   const int kpmax = glu ? kGemmKpMaxGlu : kGemmKpMax;
@@ -146,6 +147,9 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     p->xfast = 0;
     p->lds_all = 0;
     p->lds_bytes = head + red_bytes;
+    // The pre-pass writes x in fragment order (normalised under NORM_IN):
+    // row-major fragments would cost a cache access per lane.
+    if ((f & QDEC_NORM_IN) || a->rows >= kGemmRetileRows) p->xt = mt;
   }
   p->amerge = 0;
   p->apart = nullptr;
@@ -164,7 +168,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   size_t pb = 0, cb = 0, xn_off = 0;
   gemm_scratch(a, *p, &pb, &cb, &xn_off);
   if (need_scratch && pb && !a->partial) return set_error(QDEC_EINVAL, "qdec_gemm: this call needs a partial workspace");
-  if (p->xd && (f & QDEC_NORM_IN) && a->partial)
+  if (p->xd && ((f & QDEC_NORM_IN) || p->xt) && a->partial)
     p->xn = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(a->partial) + xn_off);
   if (p->lds_bytes > (size_t)kGemmLdsX)
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: rows %d x waves %d needs %zu B of LDS", a->rows, a->waves,

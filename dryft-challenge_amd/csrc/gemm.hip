@@ -196,11 +196,16 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   // (cache-resident x) right behind the slot's weight block.
   uint4 xb[XD ? MT : 1][XD ? NB : 1];
   const bool xrow_ok = col < rows;  // lanes past the last row read row 0 and use zeros
-  const uint16_t *xg[MT];           // row mt*16 + col of x at the wave's first k step
+  // Row mt*16 + col of x at the wave's first k step; with p.xt the
+  // normalisation pre-pass wrote x in fragment order (k step, M tile, lane),
+  // so a fragment load is one contiguous KiB instead of 16 row pieces.
+  const uint16_t *xg[MT];
+  const int xkstep = p.xt ? p.xt * 512 : 32;  // elements between k steps
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + col;
-    xg[mt] = X + (size_t)(m < rows ? m : 0) * p.k + (size_t)ks_wave * 32 + grp * 8;
+    xg[mt] = p.xt ? X + ((size_t)ks_wave * p.xt + mt) * 512 + lane * 8
+                  : X + (size_t)(m < rows ? m : 0) * p.k + (size_t)ks_wave * 32 + grp * 8;
   }
   // Weight block of k step i (relative to the wave's range) of `tile`.
   auto wptr = [&](int tile, int i) { return W + ((size_t)tile * p.KS + ks_wave + i) * 64 + lane; };
@@ -227,7 +232,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         if constexpr (XD) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
-            xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + min(r, p.ksw - 1) * 32);
+            xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + (size_t)min(r, p.ksw - 1) * xkstep);
         }
       }
     } else {
@@ -403,7 +408,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
                 if constexpr (GLU) wb[1][r] = ldw(qn + r * 64 + up_off);
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                  xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + ((i + RW) % p.ksw) * 32);
+                  xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + (size_t)((i + RW) % p.ksw) * xkstep);
               }
             }
           }
@@ -641,12 +646,27 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 // and the same rounding as the GEMM's own staging, so a row comes out
 // bit-identical whichever path stages it.
 __global__ void __launch_bounds__(512) rownorm_kernel(const uint16_t *__restrict__ X, const uint16_t *__restrict__ norm_w,
-                                                       uint16_t *__restrict__ xn, int k, float eps) {
+                                                       uint16_t *__restrict__ xn, int k, float eps, int rows, int nmt,
+                                                       int do_norm) {
   __shared__ float s_red[8 * 8];
   __shared__ float s_rstd[8];
   const int m = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
-  const uint16_t *xrow = X + (size_t)m * k;
   const int nvec = k >> 3;
+  // Fragment order (nmt > 0): vector v of row m goes to k step v/4, M tile
+  // m/16, lane (m%16) + 16*(v%4); rows past the last real one are zeros.
+  auto dst = [&](int v) -> uint16_t * {
+    if (nmt == 0) return xn + (size_t)m * k + 8 * v;
+    return xn + (((size_t)(v >> 2) * nmt + (m >> 4)) * 64 + (m & 15) + 16 * (v & 3)) * 8;
+  };
+  if (m >= rows) {
+    for (int v = tid; v < nvec; v += nthr) *reinterpret_cast<uint4 *>(dst(v)) = zero4();
+    return;
+  }
+  const uint16_t *xrow = X + (size_t)m * k;
+  if (!do_norm) {  // re-layout only
+    for (int v = tid; v < nvec; v += nthr) *reinterpret_cast<uint4 *>(dst(v)) = *reinterpret_cast<const uint4 *>(xrow + 8 * v);
+    return;
+  }
   float ss[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) ss[j] = 0.f;
@@ -659,7 +679,7 @@ __global__ void __launch_bounds__(512) rownorm_kernel(const uint16_t *__restrict
   block_row_sums(ss, s_red, 1, s_rstd, 0, k, eps);
   const float rs = s_rstd[0];
   for (int v = tid; v < nvec; v += nthr)
-    *reinterpret_cast<uint4 *>(xn + (size_t)m * k + 8 * v) =
+    *reinterpret_cast<uint4 *>(dst(v)) =
         norm8(*reinterpret_cast<const uint4 *>(xrow + 8 * v), *reinterpret_cast<const uint4 *>(norm_w + 8 * v), rs);
 }
 
@@ -747,6 +767,13 @@ int gemm_ring_direct(int mt, uint32_t flags) {
   }
 }
 
+hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStream_t s) {
+  const int nrow = p.xt ? p.xt * 16 : p.rows;
+  hipLaunchKernelGGL(rownorm_kernel, dim3(nrow), block, 0, s, reinterpret_cast<const uint16_t *>(p.x),
+                     reinterpret_cast<const uint16_t *>(p.norm_w), p.xn, p.k, p.eps, p.rows, p.xt, do_norm ? 1 : 0);
+  return hipSuccess;
+}
+
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   const int mt = (p.rows + 15) / 16;
   const int ntiles = p.n / 16;
@@ -755,9 +782,9 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   const size_t lds = p.lds_bytes;
   if (p.xd) {
     GemmParams q = p;
-    if (flags & QDEC_NORM_IN) {
-      hipLaunchKernelGGL(rownorm_kernel, dim3(p.rows), block, 0, s, reinterpret_cast<const uint16_t *>(p.x),
-                         reinterpret_cast<const uint16_t *>(p.norm_w), p.xn, p.k, p.eps);
+    if ((flags & QDEC_NORM_IN) || p.xt) {
+      const hipError_t e = launch_rownorm(p, block, (flags & QDEC_NORM_IN) != 0, s);
+      if (e != hipSuccess) return e;
       q.x = p.xn;
     }
     switch (mt) {

@@ -11,6 +11,10 @@ constexpr int kGemmKpMax = 20;
 constexpr int kGemmKpMaxGlu = 10;
 // LDS the GEMM may use for staged activations.
 constexpr int kGemmLdsX = 64 * 1024;
+// Direct path without NORM_IN: from this many rows (two M tiles) the
+// activations are first copied into fragment order; below it the extra
+// launch costs more than the uncoalesced fragment loads.
+constexpr int kGemmRetileRows = 17;
 
 struct GemmParams {
   const void *x;
@@ -36,7 +40,8 @@ struct GemmParams {
   int lds_all;   // the workgroup's whole k range of x is staged in LDS once
   int rw;        // weight ring registers per wave (window path), 0 = passes
   int xd;        // window path with B fragments loaded straight from x (no LDS staging)
-  uint16_t *xn;  // NORM_IN with xd: normalised copy of x (workspace)
+  uint16_t *xn;  // xd: pre-pass copy of x (normalised under NORM_IN) in the workspace
+  int xt;        // > 0: xd reads xn in fragment order with this many M tiles
   // Activations merged from attention chunk partials (x_attn): layout of
   // attn_dev.h, head_dim 128, 4 query heads per kv head.
   int amerge;
@@ -49,6 +54,7 @@ bool gemm_flags_supported(uint32_t flags);
 bool gemm_fast_path(const GemmParams &p, uint32_t flags);
 int gemm_ring(int ksw, uint32_t flags);
 int gemm_ring_direct(int mt, uint32_t flags);
+hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStream_t s);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 
 struct AttnParams {
