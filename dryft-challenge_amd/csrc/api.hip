@@ -50,7 +50,7 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
     cb = sizeof(uint32_t) * (size_t)ntiles;
   }
   size_t off = 0;
-  if (p.xd && ((a->flags & QDEC_NORM_IN) || p.xt)) {
+  if (p.xd && p.xpre) {
     off = (pb + 255) & ~(size_t)255;
     pb = off + sizeof(uint16_t) * (size_t)(p.xt ? p.xt * 16 : a->rows) * a->k;
   }
@@ -79,6 +79,12 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   if (a->tiles_per_wg < 1) return set_error(QDEC_EINVAL, "qdec_gemm: tiles_per_wg %d < 1", a->tiles_per_wg);
   if (ntiles % a->tiles_per_wg) return set_error(QDEC_EINVAL, "qdec_gemm: n/16=%d not divisible by tiles_per_wg %d", ntiles, a->tiles_per_wg);
   if (arg && a->ksplit != 1) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: QDEC_ARGMAX needs ksplit 1");
+  if ((a->x_frag != 0 && a->x_frag != 1) || (a->out_frag != 0 && a->out_frag != 1))
+    return set_error(QDEC_EINVAL, "qdec_gemm: x_frag %d / out_frag %d not 0 or 1", a->x_frag, a->out_frag);
+  if (a->out_frag && (f & (QDEC_RES_OUT | QDEC_ARGMAX)))
+    return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: out_frag with RES_OUT or ARGMAX");
+  if (a->x_frag && ((f & QDEC_NORM_IN) || a->x_attn || a->ksplit != 1))
+    return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_frag needs no NORM_IN, no x_attn and ksplit 1");
   const qdec_attn_args *xa = a->x_attn;
   if (xa) {
     if (f & QDEC_NORM_IN) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_attn with NORM_IN");
@@ -110,6 +116,8 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->ksplit = a->ksplit; p->waves = a->waves; p->tiles_per_wg = a->tiles_per_wg;
   p->KS = KS;
   p->xt = 0;
+  p->xpre = 0;
+  p->ofrag = a->out_frag ? (a->rows + 15) / 16 : 0;
   p->ksw = KS / a->ksplit / a->waves;
   p->up_tiles = ntiles;
   const int kpmax = glu ? kGemmKpMaxGlu : kGemmKpMax;
@@ -144,7 +152,17 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   // for the statistics and then again for staging (qkv at 8 rows 14.2 us
   // vs 15.6, gate/up 25.2 vs 27.6 on MI355X).
   const bool stage_norm = !(f & QDEC_NORM_IN) || a->rows < kGemmDirectNormRows;
-  if (mt == 1 && lds_all && ring && stage_norm) {
+  if (a->x_frag) {
+    // x already in fragment order: the direct path reads it as it is.
+    if (!ring_d || (a->tiles_per_wg != 1 && p->ksw % ring_d))
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_frag: no direct ring for rows %d", a->rows);
+    p->rw = ring_d;
+    p->xd = 1;
+    p->xt = mt;
+    p->xfast = 0;
+    p->lds_all = 0;
+    p->lds_bytes = head + red_bytes;
+  } else if (mt == 1 && lds_all && ring && stage_norm) {
     p->rw = ring;
   } else if (a->ksplit == 1 && ring_d && (a->tiles_per_wg == 1 || p->ksw % ring_d == 0)) {
     p->rw = ring_d;
@@ -154,7 +172,10 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     p->lds_bytes = head + red_bytes;
     // The pre-pass writes x in fragment order (normalised under NORM_IN):
     // row-major fragments would cost a cache access per lane.
-    if ((f & QDEC_NORM_IN) || a->rows >= kGemmRetileRows) p->xt = mt;
+    if ((f & QDEC_NORM_IN) || a->rows >= kGemmRetileRows) {
+      p->xt = mt;
+      p->xpre = 1;
+    }
   }
   p->amerge = 0;
   p->apart = nullptr;
@@ -173,7 +194,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   size_t pb = 0, cb = 0, xn_off = 0;
   gemm_scratch(a, *p, &pb, &cb, &xn_off);
   if (need_scratch && pb && !a->partial) return set_error(QDEC_EINVAL, "qdec_gemm: this call needs a partial workspace");
-  if (p->xd && ((f & QDEC_NORM_IN) || p->xt) && a->partial)
+  if (p->xd && p->xpre && a->partial)
     p->xn = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(a->partial) + xn_off);
   if (p->lds_bytes > (size_t)kGemmLdsX)
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: rows %d x waves %d needs %zu B of LDS", a->rows, a->waves,
@@ -193,6 +214,7 @@ static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) 
   if (a->waves != 4) return set_error(QDEC_EINVAL, "qdec_attn: waves %d (the kernel runs 4 wavefronts)", a->waves);
   if (a->out_partials != 0 && a->out_partials != 1)
     return set_error(QDEC_EINVAL, "qdec_attn: out_partials %d not 0 or 1", a->out_partials);
+  if (a->out_frag != 0 && a->out_frag != 1) return set_error(QDEC_EINVAL, "qdec_attn: out_frag %d not 0 or 1", a->out_frag);
   const int nchunks = (a->cap + a->chunk - 1) / a->chunk;
   if (!need_scratch) goto fill;
   if (!a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->lens || !a->k_cache ||
@@ -214,6 +236,7 @@ fill:
   p->batch = a->batch; p->t_rows = a->t_rows; p->nq = a->nq; p->nkv = a->nkv;
   p->cap = a->cap; p->chunk = a->chunk; p->nchunks = nchunks; p->waves = a->waves;
   p->out_partials = a->out_partials;
+  p->ofrag = (a->out_frag && !a->out_partials) ? (a->batch * a->t_rows + 15) / 16 : 0;
   return QDEC_OK;
 }
 

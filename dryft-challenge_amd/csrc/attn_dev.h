@@ -335,6 +335,8 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   // arithmetic of the merge below: one chunk gives tot * 1 / (Lrow * 1)).
   const bool direct = n_active == 1 && !p.out_partials;
   uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
+  // Output row m, column k (row-major, or fragment order for a direct GEMM).
+  auto out_at = [&](int m, int k) { return p.ofrag ? out + frag_off(m, k, p.ofrag) : out + (size_t)m * nq * D + k; };
   const size_t cstride = (size_t)R * (D + 2);  // floats per chunk partial: acc [R][D], m [R], l [R]
   float *part_b = p.partial + ((size_t)b * nkv + kvh) * p.nchunks * cstride;
   float *part = part_b + (size_t)c * cstride;
@@ -374,11 +376,10 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
       if (r < R) {
         if (direct) {
           const int t = r / G, hq = r % G;
-          uint16_t *dst = out + (size_t)(b * T + t) * nq * D + (size_t)(kvh * G + hq) * D;
           uint2 o;
           o.x = pack2(tot[0] / Lrow, tot[1] / Lrow);
           o.y = pack2(tot[2] / Lrow, tot[3] / Lrow);
-          *reinterpret_cast<uint2 *>(dst + dt * 16 + grp * 4) = o;
+          *reinterpret_cast<uint2 *>(out_at(b * T + t, (kvh * G + hq) * D + dt * 16 + grp * 4)) = o;
         } else {
           store_coherent4(part + (size_t)r * D + dt * 16 + grp * 4, tot);
         }
@@ -442,13 +443,12 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
       }
     }
     const int t = r / G, hq = r % G;
-    uint16_t *dst = out + (size_t)(b * T + t) * nq * D + (size_t)(kvh * G + hq) * D;
 #pragma unroll
     for (int i = 0; i < DTW; ++i) {
       uint2 ov;
       ov.x = pack2(o[i][0] / lsum, o[i][1] / lsum);
       ov.y = pack2(o[i][2] / lsum, o[i][3] / lsum);
-      *reinterpret_cast<uint2 *>(dst + (wave + NW * i) * 16 + grp * 4) = ov;
+      *reinterpret_cast<uint2 *>(out_at(b * T + t, (kvh * G + hq) * D + (wave + NW * i) * 16 + grp * 4)) = ov;
     }
   }
 }

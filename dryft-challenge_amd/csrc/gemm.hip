@@ -494,6 +494,10 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
     }
 
     const int n0 = tile * 16 + grp * 4;  // first of this lane's 4 output columns
+    auto out_at = [&](int m, int n) {
+      uint16_t *o = reinterpret_cast<uint16_t *>(p.out);
+      return p.ofrag ? o + frag_off(m, n, p.ofrag) : o + (size_t)m * p.n + n;
+    };
 
     // ---- k split across workgroups: partials, last arrival sums them.
     if (p.ksplit > 1) {
@@ -565,12 +569,12 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
           uint2 o;
           o.x = pack2(o4[0], o4[1]);
           o.y = pack2(o4[2], o4[3]);
-          *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+          *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
         } else {
           uint2 o;
           o.x = pack2(acc[0][mt][0], acc[0][mt][1]);
           o.y = pack2(acc[0][mt][2], acc[0][mt][3]);
-          *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
+          *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
         }
       }
     }
@@ -782,7 +786,7 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   const size_t lds = p.lds_bytes;
   if (p.xd) {
     GemmParams q = p;
-    if ((flags & QDEC_NORM_IN) || p.xt) {
+    if (p.xpre) {
       const hipError_t e = launch_rownorm(p, block, (flags & QDEC_NORM_IN) != 0, s);
       if (e != hipSuccess) return e;
       q.x = p.xn;

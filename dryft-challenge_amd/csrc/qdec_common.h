@@ -61,6 +61,16 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const uint4 &a, const uint4 &b, 
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
+// Activations in MFMA fragment order: element (m, k) of a [rows, K] matrix
+// with nmt = ceil(rows / 16) M tiles lives in the 1 KiB block of (k step
+// k/32, M tile m/16), lane (m % 16) + 16 * ((k % 32) / 8), element k % 8 --
+// exactly the B fragment a lane of a 16x16x32 MFMA loads, so one fragment
+// load is one contiguous KiB.  4 consecutive k from a multiple of 4 stay
+// contiguous.
+__device__ __forceinline__ size_t frag_off(int m, int k, int nmt) {
+  return (((size_t)(k >> 5) * nmt + (m >> 4)) * 64 + (m & 15) + 16 * ((k >> 3) & 3)) * 8 + (k & 7);
+}
+
 // 16-byte load with the non-temporal hint, for data read once per step
 // (weights, cached keys and values).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));

@@ -43,7 +43,9 @@ struct GemmParams {
   int rw;        // weight ring registers per wave (window path), 0 = passes
   int xd;        // window path with B fragments loaded straight from x (no LDS staging)
   uint16_t *xn;  // xd: pre-pass copy of x (normalised under NORM_IN) in the workspace
-  int xt;        // > 0: xd reads xn in fragment order with this many M tiles
+  int xt;        // > 0: xd reads x (or xn) in fragment order with this many M tiles
+  int xpre;      // xd: run the pre-pass into xn first
+  int ofrag;     // > 0: out is written in fragment order with this many M tiles
   // Activations merged from attention chunk partials (x_attn): layout of
   // attn_dev.h, head_dim 128, 4 query heads per kv head.
   int amerge;
@@ -75,6 +77,7 @@ struct AttnParams {
   float scale_log2;  // log2(e) / sqrt(head_dim)
   int batch, t_rows, nq, nkv, cap, chunk, nchunks, waves;
   int out_partials;
+  int ofrag;  // > 0: out is written in fragment order with this many M tiles
 };
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 

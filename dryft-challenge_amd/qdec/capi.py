@@ -37,7 +37,7 @@ class GemmArgs(ctypes.Structure):
     _fields_ = [("x", P), ("w", P), ("out", P), ("res", P), ("norm_w", P), ("partial", P),
                 ("counters", P), ("ids_out", P), ("lens_inc", P), ("eps", F32), ("rows", I32),
                 ("n", I32), ("k", I32), ("flags", ctypes.c_uint32), ("ksplit", I32), ("waves", I32),
-                ("tiles_per_wg", I32), ("x_attn", P)]
+                ("tiles_per_wg", I32), ("x_attn", P), ("x_frag", I32), ("out_frag", I32)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -45,7 +45,7 @@ class AttnArgs(ctypes.Structure):
                 ("lens", P), ("k_cache", P), ("v_cache", P), ("out", P), ("partial", P),
                 ("counters", P), ("eps", F32), ("sm_scale", F32), ("batch", I32), ("t_rows", I32),
                 ("nq", I32), ("nkv", I32), ("head_dim", I32), ("cap", I32), ("chunk", I32),
-                ("waves", I32), ("out_partials", I32)]
+                ("waves", I32), ("out_partials", I32), ("out_frag", I32)]
 
 
 class DraftArgs(ctypes.Structure):

@@ -146,6 +146,18 @@ typedef struct {
    * workgroup's k range within 2 vectors per thread); QDEC_EUNSUPPORTED
    * otherwise. */
   const struct qdec_attn_args *x_attn;
+  /* Activation layouts for batched calls (0 = row-major [rows, k] / [rows, n]).
+   * Fragment order, nmt = ceil(rows / 16) M tiles: element (m, c) of a matrix
+   * with C columns sits at ((c/32 * nmt + m/16) * 64 + m%16 + 16*(c%32/8)) * 8
+   * + c%8 -- the operand order of the kernels' 16x16x32 MFMA, so a direct
+   * call loads each fragment as one contiguous KiB; rows past `rows` in the
+   * last M tile are ignored.
+   * x_frag = 1: x is in fragment order (as a call with out_frag = 1 or an
+   * attention call with out_frag = 1 over the same rows wrote it).  Not with
+   * NORM_IN or x_attn; needs ksplit 1 (the call takes the direct path).
+   * out_frag = 1: out is written in fragment order (plain or GLU only). */
+  int32_t x_frag;
+  int32_t out_frag;
 } qdec_gemm_args;
 int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream);
 /* Scratch sizes (bytes) a qdec_gemm call with these arguments needs. */
@@ -198,6 +210,8 @@ typedef struct qdec_attn_args {
                            unnormalised (acc, max, sum) in partial, out is not
                            written, and a qdec_gemm with x_attn = these
                            arguments merges them (no arrival pass) */
+  int32_t out_frag;     /* 1: out in the fragment order of qdec_gemm_args
+                           (rows = batch*t_rows, columns nq*head_dim) */
 } qdec_attn_args;
 int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream);
 int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,

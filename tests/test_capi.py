@@ -69,6 +69,9 @@ def _gemm(**kw):
     (dict(flags=capi.GLU), -3, "not supported"),
     (dict(flags=capi.ARGMAX | capi.NORM_IN, ksplit=2), -3, "ksplit 1"),
     (dict(tiles_per_wg=3), -1, "tiles_per_wg"),
+    (dict(x_frag=2), -1, "x_frag"),
+    (dict(flags=capi.RES_OUT, res=16, out_frag=1), -3, "out_frag"),
+    (dict(flags=capi.NORM_IN, norm_w=16, x_frag=1), -3, "x_frag"),
     (dict(x=8), -2, "aligned"),
     (dict(out=None), -1, "null out"),
 ])

@@ -340,6 +340,95 @@ def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chun
     assert torch.equal(results[0].view(torch.int16), results[1].view(torch.int16))
 
 
+def frag_to_rows(buf, rows, cols):
+    """Row-major [rows, cols] view of a buffer written in fragment order
+    (include/qdec.h): element (m, c) at ((c/32*nmt + m/16)*64 + m%16 +
+    16*(c%32/8))*8 + c%8."""
+    nmt = (rows + 15) // 16
+    m = torch.arange(rows)[:, None]
+    c = torch.arange(cols)[None, :]
+    idx = (((c // 32) * nmt + m // 16) * 64 + m % 16 + 16 * ((c % 32) // 8)) * 8 + c % 8
+    return buf.flatten()[idx.flatten().to(buf.device)].view(rows, cols)
+
+
+@pytest.mark.parametrize("B,lens,cap,chunk", [(8, [700, 31, 257, 5, 1000, 640, 64, 300], 1056, 512),
+                                               (20, [100 + 37 * i for i in range(20)], 896, 896)])
+def test_attention_to_o_in_fragment_order_bitexact(lib, B, lens, cap, chunk):
+    """Attention writing its output in fragment order and the O projection
+    reading it that way give the same bits as the row-major handover."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    g = torch.Generator().manual_seed(sum(lens))
+    W = (NQ + 2 * NKV) * D
+    qkv = (torch.randn(B, W, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    qn = bf16(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    kn = bf16(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV)
+    kc0 = torch.randn(B, NKV, cap, D, generator=g).to(torch.bfloat16)
+    vc0 = v_layout(torch.randn(B, NKV, cap, D, generator=g).to(torch.bfloat16))
+    cos, sin = rope_tables(cap, D, 5e6, "bf16")
+    dcos, dsin = cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
+    dl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    Wo = pack(lib, rnd(H, NQ * D, scale=0.02, seed=15).to(DEV))
+    res0 = rnd(B, H, scale=2.0, seed=16).to(DEV)
+    ks, waves, _ = role_plan(H, NQ * D, "o")
+    outs, results = [], []
+    for frag in (0, 1):
+        kc, vc = kc0.to(DEV), vc0.to(DEV)
+        out = torch.zeros((B + 15) // 16 * 16, NQ * D, dtype=torch.bfloat16, device=DEV)
+        a = capi.AttnArgs(qkv=qkv.data_ptr(), q_norm_w=qn.data_ptr(), k_norm_w=kn.data_ptr(), cos_tab=dcos.data_ptr(),
+                          sin_tab=dsin.data_ptr(), lens=dl.data_ptr(), k_cache=kc.data_ptr(), v_cache=vc.data_ptr(),
+                          out=out.data_ptr(), eps=1e-6, sm_scale=D ** -0.5, batch=B, t_rows=1, nq=NQ, nkv=NKV,
+                          head_dim=D, cap=cap, chunk=chunk, waves=4, out_frag=frag)
+        pb, cb = lib.attn_workspace(a)
+        part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
+        cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
+        a.partial, a.counters = part.data_ptr(), cnt.data_ptr()
+        lib.attn(a, stream())
+        res = res0.clone()
+        gw = Gemm(lib, capi.RES_OUT, H, NQ * D, ksplit=ks, waves=waves)
+        o = capi.GemmArgs(x=out.data_ptr(), w=Wo.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=B, n=H, k=NQ * D,
+                          flags=capi.RES_OUT, ksplit=ks, waves=waves, tiles_per_wg=1, x_frag=frag,
+                          partial=gw.partial.data_ptr(), counters=gw.counters.data_ptr())
+        lib.gemm(o, stream())
+        torch.cuda.synchronize()
+        outs.append(frag_to_rows(out, B, NQ * D).cpu() if frag else out[:B].cpu())
+        results.append(res.cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert torch.equal(results[0].view(torch.int16), results[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("rows", [5, 8, 17, 40])
+def test_glu_to_down_in_fragment_order_bitexact(lib, rows):
+    """gate/up writing SwiGLU in fragment order and down reading it that way
+    give the same bits as the row-major handover."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    x = rnd(rows, H, scale=3.0, seed=41).to(DEV)
+    Wgu = pack(lib, rnd(2 * I, H, scale=0.02, seed=42).to(DEV))
+    Wd = pack(lib, rnd(H, I, scale=0.02, seed=43).to(DEV))
+    nw = rnd(H, scale=0.2, seed=44).to(DEV)
+    res0 = rnd(rows, H, scale=2.0, seed=45).to(DEV)
+    pg, pd = role_plan(I, H, "gate_up"), role_plan(H, I, "down")
+    acts, results = [], []
+    for frag in (0, 1):
+        act = torch.zeros((rows + 15) // 16 * 16, I, dtype=torch.bfloat16, device=DEV)
+        g1 = Gemm(lib, capi.NORM_IN | capi.GLU, I, H, ksplit=pg[0], waves=pg[1])
+        a = capi.GemmArgs(x=x.data_ptr(), w=Wgu.data_ptr(), out=act.data_ptr(), norm_w=nw.data_ptr(), eps=1e-6,
+                          rows=rows, n=I, k=H, flags=capi.NORM_IN | capi.GLU, ksplit=pg[0], waves=pg[1],
+                          tiles_per_wg=1, out_frag=frag, partial=g1.partial.data_ptr(), counters=g1.counters.data_ptr())
+        lib.gemm(a, stream())
+        res = res0.clone()
+        d = capi.GemmArgs(x=act.data_ptr(), w=Wd.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=rows, n=H, k=I,
+                          flags=capi.RES_OUT, ksplit=pd[0], waves=pd[1], tiles_per_wg=1, x_frag=frag,
+                          partial=g1.partial.data_ptr(), counters=g1.counters.data_ptr())
+        lib.gemm(d, stream())
+        torch.cuda.synchronize()
+        acts.append(frag_to_rows(act, rows, I).cpu() if frag else act[:rows].cpu())
+        results.append(res.cpu())
+    assert torch.equal(acts[0].view(torch.int16), acts[1].view(torch.int16))
+    assert torch.equal(results[0].view(torch.int16), results[1].view(torch.int16))
+
+
 def attn_oracle(c, B, T):
     qkv = c["qkv"].float().view(B, T, NQ + 2 * NKV, D)
     kc, vc = c["kc"].float().clone(), c["vc"].float().clone()
