@@ -32,8 +32,10 @@ namespace qdec {
 
 namespace {
 
+// Up to 32 query rows per kv head the body fits 256 registers without
+// spills: two workgroups per CU.
 template <int D, int G, int MTQ>
-__global__ void __launch_bounds__(256) attn_kernel(const AttnParams p) {
+__global__ void __launch_bounds__(256, MTQ <= 2 ? 2 : 1) attn_kernel(const AttnParams p) {
   __shared__ __align__(16) unsigned char smem[kAttnLds];
   attn_block<D, G, MTQ>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }

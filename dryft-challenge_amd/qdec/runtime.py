@@ -128,15 +128,17 @@ def attn_chunk(batch, nkv, cap):
     36 layers): once batch x kv heads fills half the CUs one chunk per
     sequence is fastest (no merge); below that, smaller chunks trade the
     cross-workgroup merge against parallelism -- 512 slots at batch 8, 256 at
-    batch 2..7 and at batch 1 with long caches, 128 at batch 1 up to 1024
-    slots (10.4 us vs 12.0 us at 256 for 640 cached slots; 21.5 vs 17.1 us
-    at 4000)."""
+    batch 2..7 and at batch 1 with long caches, 96 at batch 1 up to 1024
+    slots (10.4 us at 128 vs 12.0 us at 256 for 640 cached slots; 21.5 vs
+    17.1 us at 4000; with two attention workgroups per CU a batch-1 step at
+    512..766 cached slots takes 2.187 ms at 96, 2.203 at 128, 2.250 at 64,
+    2.241 at 192; at batch 8, 512 stays ahead of 256, 384 and 768)."""
     cap = round_up(cap, 32)
     if batch * nkv >= 128:
         return cap
     if batch >= 8:
         return min(cap, 512)
-    return min(cap, 128 if batch == 1 and cap <= 1024 else 256)
+    return min(cap, 96 if batch == 1 and cap <= 1024 else 256)
 
 
 class DeviceModel:
