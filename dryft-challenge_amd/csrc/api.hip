@@ -147,11 +147,11 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->xn = nullptr;
   const int ring = gemm_ring(p->ksw, f);
   const int ring_d = gemm_ring_direct(mt, f);
-  // From 8 rows a NORM_IN call does better on the direct path: one
-  // normalisation pre-pass instead of every workgroup reading whole rows
-  // for the statistics and then again for staging (qkv at 8 rows 14.2 us
-  // vs 15.6, gate/up 25.2 vs 27.6 on MI355X).
-  const bool stage_norm = !(f & QDEC_NORM_IN) || a->rows < kGemmDirectNormRows;
+  // Past its register-staged rows a NORM_IN call does better on the direct
+  // path: one normalisation pre-pass instead of every workgroup reading
+  // whole rows for the statistics and then again for staging (gate/up at 8
+  // rows 25.2 us vs 27.6 on MI355X).
+  const bool stage_norm = !(f & QDEC_NORM_IN) || a->rows < (glu ? kGemmDirectGluRows : kGemmDirectNormRows);
   if (a->x_frag) {
     // x already in fragment order: the direct path reads it as it is.
     if (!ring_d || (a->tiles_per_wg != 1 && p->ksw % ring_d))

@@ -51,8 +51,10 @@ namespace {
 constexpr int kWbuf = 20;
 static_assert(kGemmKpMax == kWbuf && 2 * kGemmKpMaxGlu == kWbuf, "pass register budget");
 
-// Activations from registers: up to kFastRows rows, 2 vectors per thread per row.
+// Activations from registers: up to kFastRows rows (kFastRowsNorm under
+// NORM_IN, in a separate instantiation), 2 vectors per thread per row.
 constexpr int kFastRows = 4;
+constexpr int kFastRowsNorm = 8;
 constexpr int kFastVec = 2;
 
 // Sum one fp32 value per thread of the workgroup for up to 8 rows in a fixed
@@ -153,7 +155,7 @@ __device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk)
   return v;
 }
 
-template <int MT, uint32_t FLAGS, int RW, bool XD>
+template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr bool NORM = (FLAGS & QDEC_NORM_IN) != 0;
@@ -249,9 +251,9 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
     // Row m, vectors vr = tid + j*nthr of the workgroup's k range (per_row
     // of them), loaded into registers before the first weights.
     const int per_row = p.ksw * nw * 4;
-    uint4 xr[kFastRows][kFastVec];
+    uint4 xr[FR][kFastVec];
 #pragma unroll
-    for (int m = 0; m < kFastRows; ++m)
+    for (int m = 0; m < FR; ++m)
 #pragma unroll
       for (int j = 0; j < kFastVec; ++j) {
         const int vr = tid + j * nthr;
@@ -270,7 +272,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss[j] = 0.f;
 #pragma unroll
-      for (int m = 0; m < kFastRows; ++m)
+      for (int m = 0; m < FR; ++m)
 #pragma unroll
         for (int j = 0; j < kFastVec; ++j) {
           float f[8];
@@ -281,7 +283,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       block_row_sums(ss, s_red, rows, s_rstd, 0, p.k, p.eps);
     }
 #pragma unroll
-    for (int m = 0; m < kFastRows; ++m)
+    for (int m = 0; m < FR; ++m)
 #pragma unroll
       for (int j = 0; j < kFastVec; ++j) {
         const int vr = tid + j * nthr;
@@ -719,7 +721,11 @@ bool gemm_flags_supported(uint32_t flags) {
 
 bool gemm_fast_path(const GemmParams &p, uint32_t flags) {
   const int per_row = p.ksw * p.waves * 4;
-  return p.lds_all && p.rows <= kFastRows && per_row <= kFastVec * 64 * p.waves &&
+  // 8 register rows pay for NORM_IN without GLU (qkv 12.7 us at 8 rows vs
+  // 14.6 through the pre-pass); gate/up keeps its 3 waves per SIMD instead.
+  const bool norm8 = (flags & QDEC_NORM_IN) && !(flags & QDEC_GLU);
+  return p.lds_all && p.rows <= (norm8 ? kFastRowsNorm : kFastRows) &&
+         per_row <= kFastVec * 64 * p.waves &&
          (!(flags & QDEC_NORM_IN) || p.ksplit == 1);
 }
 
@@ -801,6 +807,20 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   }
   if (p.rw > 0) {
     if (mt != 1) return hipErrorInvalidValue;
+    if (p.xfast && p.rows > kFastRows) {  // 5..8 rows under NORM_IN (no GLU) from registers
+      constexpr int R8 = kFastRowsNorm;
+      if (flags == QDEC_NORM_IN && p.rw == 20)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN, 20, false, R8>), grid, block, lds, s, p);
+      else if (flags == QDEC_NORM_IN && p.rw == 16)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN, 16, false, R8>), grid, block, lds, s, p);
+      else if (flags == (QDEC_NORM_IN | QDEC_ARGMAX) && p.rw == 20)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_ARGMAX, 20, false, R8>), grid, block, lds, s, p);
+      else if (flags == (QDEC_NORM_IN | QDEC_ARGMAX) && p.rw == 16)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_ARGMAX, 16, false, R8>), grid, block, lds, s, p);
+      else
+        return hipErrorInvalidValue;
+      return hipSuccess;
+    }
     if (flags == (QDEC_NORM_IN | QDEC_GLU)) {
       if (p.rw != 10) return hipErrorInvalidValue;
       hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_GLU, 10, false>), grid, block, lds, s, p);

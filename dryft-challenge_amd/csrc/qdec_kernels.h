@@ -15,8 +15,10 @@ constexpr int kGemmLdsX = 64 * 1024;
 // activations are first copied into fragment order; below it the extra
 // launch costs more than the uncoalesced fragment loads.
 constexpr int kGemmRetileRows = 17;
-// NORM_IN calls of at least this many rows take the direct path.
-constexpr int kGemmDirectNormRows = 8;
+// NORM_IN calls of at least this many rows take the direct path (with GLU,
+// whose staged path stops at 4 register rows, from 8).
+constexpr int kGemmDirectNormRows = 9;
+constexpr int kGemmDirectGluRows = 8;
 
 struct GemmParams {
   const void *x;

@@ -119,7 +119,7 @@ def test_embed_gather_exact(lib):
 
 # ------------------------------------------------------------------- GEMM
 
-@pytest.mark.parametrize("rows", [1, 4, 9, 16, 17, 36, 64])
+@pytest.mark.parametrize("rows", [1, 4, 7, 9, 16, 17, 36, 64])
 @pytest.mark.parametrize("role", ["qkv", "o", "gate_up", "down"])
 def test_gemm_roles_vs_oracle(lib, role, rows):
     from qdec import capi
@@ -187,7 +187,7 @@ def test_gemm_row_invariance_bitexact(lib, role):
 
     full = run(list(range(big)))
     for rows_idx in ([5], [0, 1, 2, 3], list(range(36)), [63, 9, 40], list(range(17, 34)), list(range(16)),
-                     list(range(40, 49)), [7] * 12):
+                     list(range(40, 49)), [7] * 12, list(range(40, 48)), [5, 6, 7, 8, 9, 10]):
         part = run(rows_idx)
         assert torch.equal(part.view(torch.int16), full[rows_idx].view(torch.int16)), rows_idx
 
