@@ -254,8 +254,9 @@ def main():
     ap.add_argument("--no-spec", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
     ap.add_argument("--pmc-role", choices=("qkv", "o", "gate_up", "down", "lm"),
-                    help="only launch this role's GEMM over every layer (5 rounds), then a "
-                         "512 MiB device copy as the counter calibration, for rocprofv3 --pmc")
+                    help="only launch this role's GEMM over every layer (6 rounds, rows = the "
+                         "config's batch), then a 512 MiB device copy as the counter calibration, "
+                         "for rocprofv3 --pmc")
     ap.add_argument("--cpu-prompt", type=int, default=64)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -284,7 +285,11 @@ def main():
     sh = eng._shape_for(B, S, N)
     st = sh.state
     if args.pmc_role:
-        st.prefill(prompt.to(eng.device))
+        if B == 1:
+            st.prefill(prompt.to(eng.device))
+        else:  # counters only: batched configs run on random activations, no prefill
+            st.h.normal_(0.0, 1.0)
+            st.act.normal_(0.0, 1.0)
         time_gemm_role(eng, st, args.pmc_role, reps=5)
         src = torch.empty(512 << 20, dtype=torch.uint8, device=eng.device)
         dst = torch.empty_like(src)
