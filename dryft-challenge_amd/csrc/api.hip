@@ -342,4 +342,106 @@ int qdec_spec_accept(const qdec_accept_args *a, qdec_stream_t stream) {
                        "qdec_spec_accept");
 }
 
+// ------------------------------------------------------------- prefill
+int qdec_rownorm(const qdec_rownorm_args *a, qdec_stream_t stream) {
+  if (!a || !a->x || !a->out) return set_error(QDEC_EINVAL, "qdec_rownorm: null pointer");
+  if (a->rows < 1 || a->k < 32 || a->k % 32 || a->tiles < (a->rows + 15) / 16)
+    return set_error(QDEC_EINVAL, "qdec_rownorm: rows %d k %d tiles %d", a->rows, a->k, a->tiles);
+  if (!aligned16(a->x) || !aligned16(a->out) || (a->norm_w && !aligned16(a->norm_w)))
+    return set_error(QDEC_EALIGN, "qdec_rownorm: pointers must be 16-byte aligned");
+  return launch_status(launch_rownorm_rows(a->x, a->norm_w, a->out, a->eps, a->rows, a->k, a->tiles,
+                                           (hipStream_t)stream),
+                       "qdec_rownorm");
+}
+
+int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
+  if (!a || !a->x || !a->w || !a->out) return set_error(QDEC_EINVAL, "qdec_prefill_gemm: null pointer");
+  const uint32_t f = a->flags;
+  if (f != 0u && f != QDEC_RES_OUT && f != QDEC_GLU)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_gemm: flags 0x%x not supported (0, RES_OUT or GLU)", f);
+  if (a->rows < 1 || a->k < kPgStageK || a->k % kPgStageK || a->n < kPgCols || a->n % kPgCols)
+    return set_error(QDEC_EINVAL, "qdec_prefill_gemm: rows %d n %d k %d (n a multiple of %d, k of %d)", a->rows,
+                     a->n, a->k, kPgCols, kPgStageK);
+  if (a->tiles < 1 || a->tiles % (kPgRows / 16) || a->rows > a->tiles * 16)
+    return set_error(QDEC_EINVAL, "qdec_prefill_gemm: tiles %d must be a multiple of %d covering %d rows", a->tiles,
+                     kPgRows / 16, a->rows);
+  if ((f & QDEC_RES_OUT) && (!a->res || a->out_frag))
+    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_gemm: RES_OUT needs res and a row-major out");
+  if (a->out_frag != 0 && a->out_frag != 1) return set_error(QDEC_EINVAL, "qdec_prefill_gemm: out_frag must be 0 or 1");
+  if (!aligned16(a->x) || !aligned16(a->w) || !aligned16(a->out) || (a->res && !aligned16(a->res)))
+    return set_error(QDEC_EALIGN, "qdec_prefill_gemm: pointers must be 16-byte aligned");
+  PgemmParams p;
+  p.x = reinterpret_cast<const uint16_t *>(a->x);
+  p.w = reinterpret_cast<const uint16_t *>(a->w);
+  p.out = reinterpret_cast<uint16_t *>(a->out);
+  p.res = reinterpret_cast<const uint16_t *>(a->res);
+  p.rows = a->rows;
+  p.n = a->n;
+  p.k = a->k;
+  p.tiles = a->tiles;
+  p.ofrag = a->out_frag;
+  const bool glu = (f & QDEC_GLU) != 0;
+  p.n_out = glu ? a->n / 2 : a->n;
+  p.up_tiles = a->n / 32;
+  p.wg_n = glu ? (a->n / 2) / (kPgCols / 2) : a->n / kPgCols;
+  return launch_status(launch_pgemm(p, f, (hipStream_t)stream), "qdec_prefill_gemm");
+}
+
+int qdec_prefill_qk(const qdec_prefill_qk_args *a, qdec_stream_t stream) {
+  if (!a || !a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->k_cache || !a->v_cache)
+    return set_error(QDEC_EINVAL, "qdec_prefill_qk: null pointer");
+  if (a->head_dim != 128 || a->nq < 1 || a->nkv < 1)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_qk: head_dim %d nq %d nkv %d (head_dim 128)", a->head_dim, a->nq,
+                     a->nkv);
+  if (a->batch < 1 || a->t_rows < 1 || a->pos0 < 0 || a->cap < 32 || a->cap % 32 || a->pos0 + a->t_rows > a->cap)
+    return set_error(QDEC_EINVAL, "qdec_prefill_qk: batch %d t_rows %d pos0 %d cap %d", a->batch, a->t_rows, a->pos0,
+                     a->cap);
+  if (!aligned16(a->qkv) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+    return set_error(QDEC_EALIGN, "qdec_prefill_qk: qkv and caches must be 16-byte aligned");
+  PqkParams p;
+  p.qkv = reinterpret_cast<uint16_t *>(a->qkv);
+  p.q_norm_w = reinterpret_cast<const uint16_t *>(a->q_norm_w);
+  p.k_norm_w = reinterpret_cast<const uint16_t *>(a->k_norm_w);
+  p.cos_tab = reinterpret_cast<const uint16_t *>(a->cos_tab);
+  p.sin_tab = reinterpret_cast<const uint16_t *>(a->sin_tab);
+  p.k_cache = reinterpret_cast<uint16_t *>(a->k_cache);
+  p.v_cache = reinterpret_cast<uint16_t *>(a->v_cache);
+  p.eps = a->eps;
+  p.batch = a->batch;
+  p.t_rows = a->t_rows;
+  p.pos0 = a->pos0;
+  p.nq = a->nq;
+  p.nkv = a->nkv;
+  p.cap = a->cap;
+  return launch_status(launch_prefill_qk(p, (hipStream_t)stream), "qdec_prefill_qk");
+}
+
+int qdec_prefill_attn(const qdec_prefill_attn_args *a, qdec_stream_t stream) {
+  if (!a || !a->qkv || !a->k_cache || !a->v_cache || !a->out) return set_error(QDEC_EINVAL, "qdec_prefill_attn: null pointer");
+  if (a->head_dim != 128 || a->nkv < 1 || a->nq != 4 * a->nkv)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_attn: head_dim %d nq %d nkv %d (head_dim 128, 4 query heads per kv head)",
+                     a->head_dim, a->nq, a->nkv);
+  if (a->batch < 1 || a->t_rows < 1 || a->pos0 < 0 || a->cap < 32 || a->cap % 32 || a->pos0 + a->t_rows > a->cap)
+    return set_error(QDEC_EINVAL, "qdec_prefill_attn: batch %d t_rows %d pos0 %d cap %d", a->batch, a->t_rows,
+                     a->pos0, a->cap);
+  const int64_t rows = (int64_t)a->batch * a->t_rows;
+  if (a->tiles < (rows + 15) / 16) return set_error(QDEC_EINVAL, "qdec_prefill_attn: tiles %d < rows %lld / 16", a->tiles, (long long)rows);
+  if (!aligned16(a->qkv) || !aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->out))
+    return set_error(QDEC_EALIGN, "qdec_prefill_attn: pointers must be 16-byte aligned");
+  PattnParams p;
+  p.qkv = reinterpret_cast<const uint16_t *>(a->qkv);
+  p.k_cache = reinterpret_cast<const uint16_t *>(a->k_cache);
+  p.v_cache = reinterpret_cast<const uint16_t *>(a->v_cache);
+  p.out = reinterpret_cast<uint16_t *>(a->out);
+  p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  p.batch = a->batch;
+  p.t_rows = a->t_rows;
+  p.pos0 = a->pos0;
+  p.nq = a->nq;
+  p.nkv = a->nkv;
+  p.cap = a->cap;
+  p.tiles = a->tiles;
+  return launch_status(launch_prefill_attn(p, (hipStream_t)stream), "qdec_prefill_attn");
+}
+
 }  // extern "C"

@@ -161,27 +161,9 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
     }
   }
 
-  // Head RMSNorm (weight w) and RoPE of the two channels 2*lane, 2*lane+1 of
-  // one head row; channel i pairs with i +- D/2, held by lane ^ 32.
+  // Head RMSNorm and RoPE of the two channels 2*lane, 2*lane+1 of one head row.
   auto norm_rope = [&](uint32_t raw, uint32_t w, uint32_t cw, uint32_t sw) -> uint32_t {
-    const float x0 = lo16(raw), x1 = hi16(raw);
-    float ss = x0 * x0 + x1 * x1;
-    ss += shfl_xor(ss, 32);
-    ss += shfl_xor(ss, 16);
-    ss += shfl_xor(ss, 8);
-    ss += shfl_xor(ss, 4);
-    ss += shfl_xor(ss, 2);
-    ss += shfl_xor(ss, 1);
-    const float rstd = 1.0f / sqrtf(ss / (float)D + p.eps);
-    const float y0 = rbf(lo16(w) * rbf(x0 * rstd));
-    const float y1 = rbf(hi16(w) * rbf(x1 * rstd));
-    const float p0 = shfl_xor(y0, 32), p1 = shfl_xor(y1, 32);
-    const bool first_half = lane < 32;
-    const float r0 = first_half ? -p0 : p0;
-    const float r1 = first_half ? -p1 : p1;
-    const float o0 = rbf(y0 * lo16(cw)) + rbf(r0 * lo16(sw));
-    const float o1 = rbf(y1 * hi16(cw)) + rbf(r1 * hi16(sw));
-    return pack2(o0, o1);
+    return head_norm_rope2(raw, w, cw, sw, p.eps);
   };
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {

@@ -784,6 +784,14 @@ hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStre
   return hipSuccess;
 }
 
+hipError_t launch_rownorm_rows(const void *x, const void *norm_w, void *out, float eps, int rows, int k,
+                               int tiles, hipStream_t s) {
+  hipLaunchKernelGGL(rownorm_kernel, dim3(tiles * 16), dim3(256), 0, s, reinterpret_cast<const uint16_t *>(x),
+                     reinterpret_cast<const uint16_t *>(norm_w), reinterpret_cast<uint16_t *>(out), k, eps, rows,
+                     tiles, norm_w ? 1 : 0);
+  return hipSuccess;
+}
+
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   const int mt = (p.rows + 15) / 16;
   const int ntiles = p.n / 16;

@@ -1,0 +1,400 @@
+// Prompt-processing (prefill) kernels for gfx950: the large-M product on the
+// matrix cores, the batched head norm / RoPE / cache fill, and causal GQA
+// flash attention over the cache.
+//
+// Reference behaviour replaced: engine/engine.py:448-490 (_layers_forward,
+// _attend_prefill, _prefill: F.linear, ops.qkv_post_rows, SDPA flash
+// attention), engine/kernels/ops.py:149-205 (_qkv_post_rows_kernel) and
+// :242-267 (_silu_mul_kernel).
+#include "qdec_common.h"
+#include "qdec_kernels.h"
+
+namespace qdec {
+namespace {
+
+// ------------------------------------------------------------------ product
+// A workgroup of 4 wavefronts computes a kPgRows x kPgCols tile of the
+// transposed product D = W . x^T: a weight fragment (16 weight rows x 32 k)
+// is the A operand and an activation fragment (32 k x 16 rows) the B operand
+// of v_mfma_f32_16x16x32_bf16, and both are one contiguous KiB in their
+// layouts.  Waves 2 x 2: wave (wn, wm) owns 4 weight x 8 activation
+// fragments = 32 accumulators.  Each stage of kPgStageK (two k steps) stages
+// 8 weight + 16 activation fragments per k step through LDS, double
+// buffered; the next stage's loads are in flight while this one computes.
+constexpr int kPgWf = kPgCols / 16;          // weight fragments per k step
+constexpr int kPgXf = kPgRows / 16;          // activation fragments per k step
+constexpr int kPgKs = kPgStageK / 32;        // k steps per stage
+constexpr int kPgFrags = kPgWf + kPgXf;      // fragments per k step
+constexpr int kPgStage = kPgKs * kPgFrags;   // fragments per stage
+constexpr int kPgGroupN = 4;                 // column tiles walked together (x reuse in L2)
+static_assert(kPgWf == 8 && kPgXf == 16 && kPgKs == 2, "load split below assumes these");
+
+__device__ __forceinline__ uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+template <uint32_t FLAGS>
+__global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
+  constexpr bool GLU = (FLAGS & QDEC_GLU) != 0;
+  constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
+  __shared__ uint4 lds[2 * kPgStage * 64];  // [buffer][k step][fragment][lane]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int wn = wave & 1, wm = wave >> 1;
+
+  // Tile order: workgroup i runs on XCD i % 8, so each XCD gets a contiguous
+  // range of the sequence; the sequence walks groups of kPgGroupN column
+  // tiles across all row tiles (the group's weights stay in L2, each row
+  // tile of x is read by the group's workgroups together).
+  int id = blockIdx.x;
+  const int G = gridDim.x;
+  if ((G & 7) == 0) id = (id & 7) * (G >> 3) + (id >> 3);
+  const int ntm = p.tiles / kPgXf;
+  const int gsz = kPgGroupN * ntm;
+  const int g = id / gsz, r = id - g * gsz;
+  const int gn = min(kPgGroupN, p.wg_n - g * kPgGroupN);
+  const int tm = r / gn, tn = g * kPgGroupN + (r - (r / gn) * gn);
+
+  const int KS = p.k >> 5;
+  // Weight tile of workgroup fragment f (GLU: 4 gate tiles, then the 4
+  // matching up tiles).
+  auto wtile = [&](int f) -> int {
+    if constexpr (GLU)
+      return f < kPgWf / 2 ? tn * (kPgWf / 2) + f : p.up_tiles + tn * (kPgWf / 2) + f - kPgWf / 2;
+    else
+      return tn * kPgWf + f;
+  };
+  // Loads of one stage: this wave moves fragments wave + 4q of each k step
+  // (q = 0, 1: weights; q = 2..5: activations).
+  const uint16_t *wb0 = p.w + (size_t)wtile(wave) * KS * 512 + lane * 8;
+  const uint16_t *wb1 = p.w + (size_t)wtile(wave + 4) * KS * 512 + lane * 8;
+  const uint16_t *xb = p.x + (size_t)(tm * kPgXf + wave) * 512 + lane * 8;
+  const size_t xks = (size_t)p.tiles * 512;  // elements per k step of x
+  uint4 st[kPgKs * 6];
+  auto gload = [&](int s) {
+#pragma unroll
+    for (int j = 0; j < kPgKs; ++j) {
+      const int ks = s * kPgKs + j;
+      st[j * 6 + 0] = ld16(wb0 + (size_t)ks * 512);
+      st[j * 6 + 1] = ld16(wb1 + (size_t)ks * 512);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) st[j * 6 + 2 + q] = ld16(xb + ks * xks + q * 4 * 512);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kPgKs; ++j)
+#pragma unroll
+      for (int q = 0; q < 6; ++q) lds[((buf * kPgKs + j) * kPgFrags + q * 4 + wave) * 64 + lane] = st[j * 6 + q];
+  };
+  // This wave's weight fragments (GLU: gate 0, 1 pair with up 2, 3).
+  auto wf = [&](int i) -> int {
+    if constexpr (GLU)
+      return i < 2 ? wn * 2 + i : kPgWf / 2 + wn * 2 + i - 2;
+    else
+      return wn * 4 + i;
+  };
+
+  f32x4_t acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[i][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int nst = p.k / kPgStageK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int s = 0; s < nst; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < nst) gload(s + 1);
+#pragma unroll
+    for (int j = 0; j < kPgKs; ++j) {
+      const uint4 *S = lds + (size_t)(buf * kPgKs + j) * kPgFrags * 64 + lane;
+      uint4 a[4], bx[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = S[wf(i) * 64];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) bx[q] = S[(kPgWf + wm * 8 + q) * 64];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[i][q] = mfma16x16x32(a[i], bx[q], acc[i][q]);
+    }
+    if (s + 1 < nst) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds columns n0 .. n0+3 of row m for every fragment pair.
+  auto store = [&](int m, int n0, uint2 o) {
+    uint16_t *dst = p.ofrag ? p.out + frag_off(m, n0, p.tiles) : p.out + (size_t)m * p.n_out + n0;
+    *reinterpret_cast<uint2 *>(dst) = o;
+  };
+  const int m_base = (tm * kPgXf + wm * 8) * 16 + col;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int m = m_base + q * 16;
+    if (m >= p.rows) continue;
+    if constexpr (GLU) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        float o4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float gv = rbf(acc[i][q][e]);
+          const float uv = rbf(acc[i + 2][q][e]);
+          o4[e] = rbf(gv / (1.0f + expf(-gv))) * uv;
+        }
+        store(m, wtile(wf(i)) * 16 + 4 * grp, make_uint2(pack2(o4[0], o4[1]), pack2(o4[2], o4[3])));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n0 = wtile(wf(i)) * 16 + 4 * grp;
+        uint2 o;
+        if constexpr (RES) {
+          const uint2 rv = *reinterpret_cast<const uint2 *>(p.res + (size_t)m * p.n_out + n0);
+          o.x = pack2(lo16(rv.x) + rbf(acc[i][q][0]), hi16(rv.x) + rbf(acc[i][q][1]));
+          o.y = pack2(lo16(rv.y) + rbf(acc[i][q][2]), hi16(rv.y) + rbf(acc[i][q][3]));
+        } else {
+          o.x = pack2(acc[i][q][0], acc[i][q][1]);
+          o.y = pack2(acc[i][q][2], acc[i][q][3]);
+        }
+        store(m, n0, o);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------- head norm + RoPE
+// One workgroup per row: wave w normalises and rotates heads w, w+4, ...
+// (queries back into qkv, keys into the K cache); then the raw values go to
+// the channel-major V cache.
+__global__ void __launch_bounds__(256) pqk_kernel(const PqkParams p) {
+  constexpr int D = 128;
+  const int m = blockIdx.x;
+  const int b = m / p.t_rows, t = m - b * p.t_rows;
+  const int pos = p.pos0 + t;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int width = (p.nq + 2 * p.nkv) * D;
+  uint16_t *row = p.qkv + (size_t)m * width;
+  const uint32_t cw = *reinterpret_cast<const uint32_t *>(p.cos_tab + (size_t)pos * D + 2 * lane);
+  const uint32_t sw = *reinterpret_cast<const uint32_t *>(p.sin_tab + (size_t)pos * D + 2 * lane);
+  const uint32_t qw = *reinterpret_cast<const uint32_t *>(p.q_norm_w + 2 * lane);
+  const uint32_t kw = *reinterpret_cast<const uint32_t *>(p.k_norm_w + 2 * lane);
+  for (int h = wave; h < p.nq + p.nkv; h += 4) {
+    uint32_t *cell = reinterpret_cast<uint32_t *>(row + (size_t)h * D + 2 * lane);
+    const uint32_t o = head_norm_rope2(*cell, h < p.nq ? qw : kw, cw, sw, p.eps);
+    if (h < p.nq)
+      *cell = o;
+    else
+      *reinterpret_cast<uint32_t *>(p.k_cache + (((size_t)b * p.nkv + (h - p.nq)) * p.cap + pos) * D + 2 * lane) = o;
+  }
+  for (int i = threadIdx.x; i < p.nkv * D; i += blockDim.x) {
+    const int kvh = i >> 7, ch = i & 127;
+    p.v_cache[((size_t)b * p.nkv + kvh) * p.cap * D + ((size_t)(pos >> 3) * D + ch) * 8 + (pos & 7)] =
+        row[(size_t)(p.nq + p.nkv + kvh) * D + ch];
+  }
+}
+
+// ---------------------------------------------------------------- attention
+// A workgroup takes kPaRows positions of the 4 query heads of one kv head of
+// one sequence; wave w takes head 4*kvh + w, its positions as 4 M tiles of
+// 16 rows.  Blocks of 32 cache slots are staged in LDS (double buffered) in
+// MFMA operand order and shared by the 4 waves:
+//   K fragment (s, h): lane (c, g) holds slot 8*(c >> 2) + (c & 3) + 4h,
+//     channels 32s + 8g .. +8: the slot order that makes the score registers
+//     of S^T = K . Q^T exactly the B operand of O^T += V^T . P^T (each lane
+//     ends up with 8 consecutive slots of one query row);
+//   V fragment dt: lane (c, g) holds channel 16dt + c, slots 8g .. 8g+7 --
+//     the channel-major cache layout, copied as is.
+// Online softmax in base 2 with fp32 state per row, probabilities rounded to
+// bf16 for the P.V product; slots past a row's position are masked, slots
+// past the block's last row are zeroed in V (the cache may hold anything
+// there, and 0 * NaN would poison the product).
+constexpr int kPaKFrags = 8, kPaVFrags = 8;
+constexpr int kPaBlockVec = (kPaKFrags + kPaVFrags) * 64;  // uint4 per staged block
+
+__global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
+  constexpr int D = 128;
+  __shared__ uint4 lds[2 * kPaBlockVec];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int T = p.t_rows;
+  const int nqb = (T + kPaRows - 1) / kPaRows;
+  const int cells = p.batch * p.nkv;
+  const int qb = nqb - 1 - (int)(blockIdx.x / cells);  // longest rows first
+  const int cell = (int)(blockIdx.x % cells);
+  const int b = cell / p.nkv, kvh = cell - b * p.nkv;
+  const int hq = kvh * 4 + wave;
+  const int width = (p.nq + 2 * p.nkv) * D;
+  const int t0 = qb * kPaRows;
+  const int tlast = min(T, t0 + kPaRows) - 1;
+  const int last = p.pos0 + tlast;  // highest slot any row of the block sees
+  const int nb = last / 32 + 1;
+  const size_t slab = ((size_t)b * p.nkv + kvh) * (size_t)p.cap * D;
+  const uint16_t *kc = p.k_cache + slab;
+  const uint16_t *vc = p.v_cache + slab;
+  const float NEG_INF = -__builtin_huge_valf();
+
+  // Queries as B operands: row col of M tile mt, channels 32s + 8*grp.
+  uint4 qf[4][4];
+  int qpos[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int t = t0 + mt * 16 + col;
+    const bool valid = t <= tlast;
+    qpos[mt] = valid ? p.pos0 + t : -1;
+    const uint16_t *qrow = p.qkv + (size_t)(b * T + min(t, tlast)) * width + (size_t)hq * D + grp * 8;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[mt][s] = valid ? ld16(qrow + s * 32) : zero4();
+  }
+
+  uint4 kr[2], vr[2];
+  auto gload = [&](int j) {
+    const int s0 = j * 32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = tid + 256 * i;
+      kr[i] = ld16(kc + (size_t)(s0 + (u >> 4)) * D + (u & 15) * 8);
+      vr[i] = ld16(vc + (size_t)(s0 >> 3) * D * 8 + (size_t)u * 8);
+    }
+  };
+  auto sstore = [&](int buf, int j) {
+    uint4 *B = lds + buf * kPaBlockVec;
+    const int s0 = j * 32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int u = tid + 256 * i;
+      const int slot = u >> 4, c16 = u & 15;
+      B[((c16 >> 2) * 2 + ((slot >> 2) & 1)) * 64 + 4 * (slot >> 3) + (slot & 3) + 16 * (c16 & 3)] = kr[i];
+      const int gi = u >> 7, ch = u & 127;
+      uint4 v = vr[i];
+      const int sb = s0 + 8 * gi;  // first slot of this 8-slot group
+      if (sb + 7 > last) {
+        uint32_t keep[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          keep[d] = (sb + 2 * d <= last ? 0x0000ffffu : 0u) | (sb + 2 * d + 1 <= last ? 0xffff0000u : 0u);
+        v.x &= keep[0];
+        v.y &= keep[1];
+        v.z &= keep[2];
+        v.w &= keep[3];
+      }
+      B[(kPaKFrags + (ch >> 4)) * 64 + (ch & 15) + 16 * gi] = v;
+    }
+  };
+
+  f32x4_t acc[4][8];
+  float m_run[4], l_run[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    m_run[mt] = NEG_INF;
+    l_run[mt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[mt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  gload(0);
+  sstore(0, 0);
+  __syncthreads();
+  for (int j = 0; j < nb; ++j) {
+    const int buf = j & 1;
+    if (j + 1 < nb) gload(j + 1);
+    const uint4 *B = lds + buf * kPaBlockVec + lane;
+    uint4 ka[4], kb[4], vf[8];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      ka[s] = B[(s * 2) * 64];
+      kb[s] = B[(s * 2 + 1) * 64];
+    }
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) vf[dt] = B[(kPaKFrags + dt) * 64];
+    const int s0 = j * 32;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const int tf = t0 + mt * 16;  // first row of the tile
+      if (tf > tlast || s0 > p.pos0 + min(tf + 15, tlast)) continue;  // tile empty or sees none of the block
+      f32x4_t sa = f32x4_t{0.f, 0.f, 0.f, 0.f}, sb = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        sa = mfma16x16x32(ka[s], qf[mt][s], sa);
+        sb = mfma16x16x32(kb[s], qf[mt][s], sb);
+      }
+      float sc[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sl = s0 + 8 * grp + i;
+        sc[i] = (sl <= qpos[mt]) ? sa[i] * p.scale_log2 : NEG_INF;
+        sc[4 + i] = (sl + 4 <= qpos[mt]) ? sb[i] * p.scale_log2 : NEG_INF;
+      }
+      float bmax = sc[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) bmax = fmaxf(bmax, sc[e]);
+      bmax = fmaxf(bmax, shfl_xor(bmax, 16));
+      bmax = fmaxf(bmax, shfl_xor(bmax, 32));
+      const float m_new = fmaxf(m_run[mt], bmax);
+      const float alpha = (m_new == NEG_INF) ? 1.0f : exp2f(m_run[mt] - m_new);
+      float pj[8];
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pj[e] = (sc[e] == NEG_INF) ? 0.f : exp2f(sc[e] - m_new);
+        psum += pj[e];
+      }
+      l_run[mt] = l_run[mt] * alpha + psum;
+      m_run[mt] = m_new;
+      const uint4 pf = pack8(pj);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        acc[mt][dt] *= alpha;
+        acc[mt][dt] = mfma16x16x32(vf[dt], pf, acc[mt][dt]);
+      }
+    }
+    if (j + 1 < nb) sstore(buf ^ 1, j + 1);
+    __syncthreads();
+  }
+
+  // Rows in fragment order for the O projection: lane holds channels
+  // 16dt + 4*grp .. +3 of its row.
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    if (t0 + mt * 16 > tlast) continue;
+    float l = l_run[mt] + shfl_xor(l_run[mt], 16);
+    l += shfl_xor(l, 32);
+    const int t = t0 + mt * 16 + col;
+    if (t > tlast) continue;
+    const int m = b * T + t;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      uint2 o;
+      o.x = pack2(acc[mt][dt][0] / l, acc[mt][dt][1] / l);
+      o.y = pack2(acc[mt][dt][2] / l, acc[mt][dt][3] / l);
+      *reinterpret_cast<uint2 *>(p.out + frag_off(m, hq * D + dt * 16 + 4 * grp, p.tiles)) = o;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s) {
+  const dim3 grid(p.wg_n * (p.tiles / kPgXf)), block(256);
+  switch (flags) {
+    case 0u: hipLaunchKernelGGL(pgemm_kernel<0u>, grid, block, 0, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL(pgemm_kernel<QDEC_RES_OUT>, grid, block, 0, s, p); break;
+    case QDEC_GLU: hipLaunchKernelGGL(pgemm_kernel<QDEC_GLU>, grid, block, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_prefill_qk(const PqkParams &p, hipStream_t s) {
+  hipLaunchKernelGGL(pqk_kernel, dim3(p.batch * p.t_rows), dim3(256), 0, s, p);
+  return hipSuccess;
+}
+
+hipError_t launch_prefill_attn(const PattnParams &p, hipStream_t s) {
+  const int nqb = (p.t_rows + kPaRows - 1) / kPaRows;
+  hipLaunchKernelGGL(pattn_kernel, dim3(nqb * p.batch * p.nkv), dim3(256), 0, s, p);
+  return hipSuccess;
+}
+
+}  // namespace qdec

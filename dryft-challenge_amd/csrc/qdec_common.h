@@ -147,6 +147,35 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected
 // Cross-lane helpers (wave64).
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
 
+// Per-head RMSNorm (weight w) and RoPE of one 128-channel head row spread
+// over a wavefront: this lane holds channels 2*lane and 2*lane+1 (raw, w,
+// cos cw and sin sw as packed bf16 pairs); channel i pairs with i +- 64,
+// held by lane ^ 32.  rotate_half(y) = [-y[64:], y[:64]].  Returns the two
+// rotated channels as packed bf16:
+//   y = bf16(w * bf16(x * rstd)),  out = bf16(bf16(y * cos) + bf16(rot * sin)).
+__device__ __forceinline__ uint32_t head_norm_rope2(uint32_t raw, uint32_t w, uint32_t cw, uint32_t sw,
+                                                    float eps) {
+  const int lane = threadIdx.x & 63;
+  const float x0 = lo16(raw), x1 = hi16(raw);
+  float ss = x0 * x0 + x1 * x1;
+  ss += shfl_xor(ss, 32);
+  ss += shfl_xor(ss, 16);
+  ss += shfl_xor(ss, 8);
+  ss += shfl_xor(ss, 4);
+  ss += shfl_xor(ss, 2);
+  ss += shfl_xor(ss, 1);
+  const float rstd = 1.0f / sqrtf(ss / 128.0f + eps);
+  const float y0 = rbf(lo16(w) * rbf(x0 * rstd));
+  const float y1 = rbf(hi16(w) * rbf(x1 * rstd));
+  const float p0 = shfl_xor(y0, 32), p1 = shfl_xor(y1, 32);
+  const bool first_half = lane < 32;
+  const float r0 = first_half ? -p0 : p0;
+  const float r1 = first_half ? -p1 : p1;
+  const float o0 = rbf(y0 * lo16(cw)) + rbf(r0 * lo16(sw));
+  const float o1 = rbf(y1 * hi16(cw)) + rbf(r1 * hi16(sw));
+  return pack2(o0, o1);
+}
+
 }  // namespace qdec
 
 // Error plumbing shared by the entry points (api.hip).

@@ -89,6 +89,49 @@ hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 constexpr int kAttnLds = 16 * 136 * 2 + 3 * 128 * 8 * 2 + 4 * 8 * 64 * 16 + 2 * 4 * 16 * 4 + 16;
 
 
+// ---- prefill (prefill.hip)
+// Product tile of a workgroup: kPgRows activation rows x kPgCols weight rows,
+// kPgStageK of k per LDS stage.
+constexpr int kPgRows = 256;
+constexpr int kPgCols = 128;
+constexpr int kPgStageK = 64;
+struct PgemmParams {
+  const uint16_t *x;
+  const uint16_t *w;
+  uint16_t *out;
+  const uint16_t *res;
+  int rows, n, k;
+  int tiles;     // M tiles of x (and of out in fragment order)
+  int ofrag;     // out in fragment order
+  int n_out;     // columns of out (n, or n/2 with GLU)
+  int up_tiles;  // GLU: tile offset of the up half (n/32)
+  int wg_n;      // workgroup tiles along n
+};
+hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s);
+
+struct PqkParams {
+  uint16_t *qkv;
+  const uint16_t *q_norm_w, *k_norm_w, *cos_tab, *sin_tab;
+  uint16_t *k_cache, *v_cache;
+  float eps;
+  int batch, t_rows, pos0, nq, nkv, cap;
+};
+hipError_t launch_prefill_qk(const PqkParams &p, hipStream_t s);
+
+// Positions of one prefill attention workgroup.
+constexpr int kPaRows = 64;
+struct PattnParams {
+  const uint16_t *qkv;
+  const uint16_t *k_cache, *v_cache;
+  uint16_t *out;
+  float scale_log2;
+  int batch, t_rows, pos0, nq, nkv, cap, tiles;
+};
+hipError_t launch_prefill_attn(const PattnParams &p, hipStream_t s);
+
+hipError_t launch_rownorm_rows(const void *x, const void *norm_w, void *out, float eps, int rows, int k,
+                               int tiles, hipStream_t s);
+
 hipError_t launch_embed(const int64_t *ids, const void *emb, void *h, int rows, int hidden,
                         int vocab, hipStream_t s);
 hipError_t launch_pack(const void *src, void *dst, int64_t n, int64_t k, hipStream_t s);

@@ -58,6 +58,27 @@ class AcceptArgs(ctypes.Structure):
                 ("batch", I32), ("cap", I32), ("k", I32), ("stop_len", I32)]
 
 
+class RownormArgs(ctypes.Structure):
+    _fields_ = [("x", P), ("norm_w", P), ("out", P), ("eps", F32), ("rows", I32), ("k", I32), ("tiles", I32)]
+
+
+class PgemmArgs(ctypes.Structure):
+    _fields_ = [("x", P), ("w", P), ("out", P), ("res", P), ("flags", ctypes.c_uint32), ("rows", I32),
+                ("n", I32), ("k", I32), ("tiles", I32), ("out_frag", I32)]
+
+
+class PrefillQkArgs(ctypes.Structure):
+    _fields_ = [("qkv", P), ("q_norm_w", P), ("k_norm_w", P), ("cos_tab", P), ("sin_tab", P),
+                ("k_cache", P), ("v_cache", P), ("eps", F32), ("batch", I32), ("t_rows", I32),
+                ("pos0", I32), ("nq", I32), ("nkv", I32), ("head_dim", I32), ("cap", I32)]
+
+
+class PrefillAttnArgs(ctypes.Structure):
+    _fields_ = [("qkv", P), ("k_cache", P), ("v_cache", P), ("out", P), ("sm_scale", F32),
+                ("batch", I32), ("t_rows", I32), ("pos0", I32), ("nq", I32), ("nkv", I32),
+                ("head_dim", I32), ("cap", I32), ("tiles", I32)]
+
+
 def declared_functions(header=HEADER):
     """Names of every function declared in include/qdec.h."""
     with open(header) as f:
@@ -84,7 +105,9 @@ class Lib:
         so.qdec_tiled_offset.argtypes = [ctypes.c_int64] * 3
         so.qdec_pack_tiles.argtypes = [P, P, ctypes.c_int64, ctypes.c_int64, P]
         for name, st in (("qdec_embed", EmbedArgs), ("qdec_gemm", GemmArgs), ("qdec_attn", AttnArgs),
-                         ("qdec_ngram_draft", DraftArgs), ("qdec_spec_accept", AcceptArgs)):
+                         ("qdec_ngram_draft", DraftArgs), ("qdec_spec_accept", AcceptArgs),
+                         ("qdec_rownorm", RownormArgs), ("qdec_prefill_gemm", PgemmArgs),
+                         ("qdec_prefill_qk", PrefillQkArgs), ("qdec_prefill_attn", PrefillAttnArgs)):
             fn = getattr(so, name)
             fn.argtypes = [ctypes.POINTER(st), P]
             fn.restype = ctypes.c_int
@@ -127,6 +150,18 @@ class Lib:
 
     def spec_accept(self, args, stream):
         self._check("qdec_spec_accept", self.so.qdec_spec_accept(ctypes.byref(args), stream))
+
+    def rownorm(self, args, stream):
+        self._check("qdec_rownorm", self.so.qdec_rownorm(ctypes.byref(args), stream))
+
+    def prefill_gemm(self, args, stream):
+        self._check("qdec_prefill_gemm", self.so.qdec_prefill_gemm(ctypes.byref(args), stream))
+
+    def prefill_qk(self, args, stream):
+        self._check("qdec_prefill_qk", self.so.qdec_prefill_qk(ctypes.byref(args), stream))
+
+    def prefill_attn(self, args, stream):
+        self._check("qdec_prefill_attn", self.so.qdec_prefill_attn(ctypes.byref(args), stream))
 
     def gemm_workspace(self, args):
         pb, cb = ctypes.c_size_t(), ctypes.c_size_t()

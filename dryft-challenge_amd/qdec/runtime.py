@@ -20,6 +20,11 @@ stream, so it can be captured into a hipGraph as is.
 Per-role launch plans are functions of the matrix shape only, never of the
 row count: that keeps every output element's summation order the same for a
 1-row and a 36-row call (the basis of lossless speculation).
+
+``Prefill`` fills the cache from a prompt with the prefill kernels: every
+prompt position of every sequence goes through a layer at once (in position
+chunks of about ``PREFILL_ROWS`` rows), so each weight matrix is read once
+per chunk and the products run on the matrix cores.
 """
 
 import ctypes
@@ -31,6 +36,12 @@ from . import capi
 
 GEMM_MAX_ROWS = 64
 ATTN_MAX_T = 16
+# Rows (sequences x positions) of one prefill chunk: activations of 16K rows
+# take about 1.1 GB, and at that size the products are well past the point
+# where the matrix cores, not the weight stream, set the pace.
+PREFILL_ROWS = 16384
+# Row tile of the prefill product (kPgRows of qdec_kernels.h).
+PREFILL_ROW_TILE = 256
 ATTN_WAVES = 4
 # Plain decode up to this batch merges attention chunks in the O projection.
 MERGE_IN_O_MAX_BATCH = 4
@@ -373,6 +384,20 @@ class DecodeState:
     # ------------------------------------------------------------- prefill
     def prefill(self, prompt, stream=None):
         """Fill cache slots ``0 .. S-1`` from ``prompt`` ``[B, S]`` (device
+        int64) with the prefill kernels (``Prefill``); returns with
+        ``ids[:B]`` = the first generated token and ``lens[:] = S``."""
+        B, S = prompt.shape
+        if B != self.batch:
+            raise ValueError(f"prompt batch {B} != state batch {self.batch}")
+        if S < 1 or S >= self.cap:
+            raise ValueError(f"prompt length {S} must be in [1, {self.cap})")
+        pf = getattr(self, "_prefill", None)
+        if pf is None or pf.chunk < min(S, pf.max_chunk):
+            pf = self._prefill = Prefill(self, S)
+        pf.run(prompt, stream=stream)
+
+    def prefill_steps(self, prompt, stream=None):
+        """Fill cache slots ``0 .. S-1`` from ``prompt`` ``[B, S]`` (device
         int64) in chunks of ``max_t`` rows per sequence through the same
         kernels as decode; returns with ``ids[:B]`` = the first generated
         token and ``lens[:] = S``."""
@@ -391,3 +416,94 @@ class DecodeState:
         t = (S - 1) % T + 1
         self.ids[:B].copy_(self.out_tok[:B * t].view(B, t)[:, t - 1])
         self.lens.fill_(S)
+
+
+class Prefill:
+    """Prompt processing for one ``DecodeState``.
+
+    A chunk of ``chunk`` positions of every sequence (row ``b * T + t`` =
+    sequence ``b`` at position ``c0 + t``) goes through each layer as
+    rownorm -> QKV product -> head norm / RoPE / cache fill -> causal
+    attention over the cache -> O product + residual -> rownorm -> gate/up
+    product with SwiGLU -> down product + residual, the products on the
+    matrix cores (qdec_prefill_gemm).  After the last chunk the final row of
+    each sequence goes through the decode lm_head + argmax.
+
+    Replaces engine/engine.py:448-490 (``_layers_forward`` over the whole
+    prompt, ``_attend_prefill``, ``_prefill``)."""
+
+    def __init__(self, state, prompt_len, rows=PREFILL_ROWS):
+        c = state.model.cfg
+        B = state.batch
+        self.state = state
+        self.max_chunk = max(1, rows // B)
+        self.chunk = min(prompt_len, self.max_chunk)
+        rows = round_up(B * self.chunk, PREFILL_ROW_TILE)
+        dev, bf = state.model.device, torch.bfloat16
+        self.h = torch.zeros((rows, c.hidden), dtype=bf, device=dev)
+        self.xn = torch.zeros((rows * c.hidden,), dtype=bf, device=dev)
+        self.qkv = torch.zeros((rows, c.n_qkv), dtype=bf, device=dev)
+        self.att = torch.zeros((rows * c.nq * c.head_dim,), dtype=bf, device=dev)
+        self.act = torch.zeros((rows * c.inter,), dtype=bf, device=dev)
+        self.ids = torch.zeros((rows,), dtype=torch.int64, device=dev)
+
+    def _gemm(self, x, w, out, n, k, rows, tiles, flags=0, res=None, out_frag=0):
+        a = capi.PgemmArgs()
+        a.x, a.w, a.out = x.data_ptr(), w.data_ptr(), out.data_ptr()
+        a.res = res.data_ptr() if res is not None else None
+        a.flags, a.rows, a.n, a.k, a.tiles, a.out_frag = flags, rows, n, k, tiles, out_frag
+        return a
+
+    def run(self, prompt, stream=None):
+        st = self.state
+        m, c, lib = st.model, st.model.cfg, st.lib
+        B, S = prompt.shape
+        s = (stream or torch.cuda.current_stream(m.device)).cuda_stream
+        H, D = c.hidden, c.head_dim
+        T = self.chunk
+        for c0 in range(0, S, self.chunk):
+            T = min(self.chunk, S - c0)
+            R = B * T
+            tiles = round_up(R, PREFILL_ROW_TILE) // 16
+            self.ids[:R].view(B, T).copy_(prompt[:, c0:c0 + T])
+            e = capi.EmbedArgs()
+            e.ids, e.emb, e.h = self.ids.data_ptr(), m.emb.data_ptr(), self.h.data_ptr()
+            e.rows, e.hidden, e.vocab = R, H, c.vocab
+            lib.embed(e, s)
+            norm = capi.RownormArgs()
+            norm.x, norm.out, norm.eps, norm.rows, norm.k, norm.tiles = (
+                self.h.data_ptr(), self.xn.data_ptr(), c.eps, R, H, tiles)
+            qk = capi.PrefillQkArgs()
+            qk.qkv, qk.cos_tab, qk.sin_tab = self.qkv.data_ptr(), st.cos.data_ptr(), st.sin.data_ptr()
+            qk.eps, qk.batch, qk.t_rows, qk.pos0 = c.eps, B, T, c0
+            qk.nq, qk.nkv, qk.head_dim, qk.cap = c.nq, c.nkv, D, st.cap
+            at = capi.PrefillAttnArgs()
+            at.qkv, at.out, at.sm_scale = self.qkv.data_ptr(), self.att.data_ptr(), D ** -0.5
+            at.batch, at.t_rows, at.pos0, at.nq, at.nkv = B, T, c0, c.nq, c.nkv
+            at.head_dim, at.cap, at.tiles = D, st.cap, tiles
+            g_qkv = self._gemm(self.xn, m.w_qkv[0], self.qkv, c.n_qkv, H, R, tiles)
+            g_o = self._gemm(self.att, m.w_o[0], self.h, H, c.nq * D, R, tiles, capi.RES_OUT, res=self.h)
+            g_gu = self._gemm(self.xn, m.w_gu[0], self.act, 2 * c.inter, H, R, tiles, capi.GLU, out_frag=1)
+            g_dn = self._gemm(self.act, m.w_down[0], self.h, H, c.inter, R, tiles, capi.RES_OUT, res=self.h)
+            for i in range(c.n_layers):
+                norm.norm_w = m.in_w[i].data_ptr()
+                lib.rownorm(norm, s)
+                g_qkv.w = m.w_qkv[i].data_ptr()
+                lib.prefill_gemm(g_qkv, s)
+                qk.q_norm_w, qk.k_norm_w = m.q_norm[i].data_ptr(), m.k_norm[i].data_ptr()
+                qk.k_cache, qk.v_cache = st.k_cache[i].data_ptr(), st.v_cache[i].data_ptr()
+                lib.prefill_qk(qk, s)
+                at.k_cache, at.v_cache = qk.k_cache, qk.v_cache
+                lib.prefill_attn(at, s)
+                g_o.w = m.w_o[i].data_ptr()
+                lib.prefill_gemm(g_o, s)
+                norm.norm_w = m.post_w[i].data_ptr()
+                lib.rownorm(norm, s)
+                g_gu.w = m.w_gu[i].data_ptr()
+                lib.prefill_gemm(g_gu, s)
+                g_dn.w = m.w_down[i].data_ptr()
+                lib.prefill_gemm(g_dn, s)
+        # The last position of every sequence: final norm, lm_head, argmax.
+        st.h[:B].copy_(self.h[:B * T].view(B, T, H)[:, T - 1])
+        lib.gemm(st._gemm_args("lm", 0, B, ids_out=st.ids), s)
+        st.lens.fill_(S)

@@ -259,6 +259,106 @@ typedef struct {
 } qdec_accept_args;
 int qdec_spec_accept(const qdec_accept_args *a, qdec_stream_t stream);
 
+/* ------------------------------------------------------------ prefill */
+
+/* Prompt processing: every prompt position of every sequence in one forward
+ * (or a few position chunks), so each weight matrix is read once per call
+ * and the products run on the matrix cores.  Row m = b*t_rows + t of a call
+ * is sequence b at position pos0 + t (equal-length prompts).  Activations
+ * that feed a product are in the fragment order of qdec_gemm_args with
+ * `tiles` M tiles (16 rows each); rows past the last real one are zero. */
+
+/* RMSNorm of every row into fragment order: out = bf16(w * bf16(x * rsqrt(
+ * mean(x^2) + eps))), or a plain re-layout when norm_w is NULL.  Rows
+ * rows .. 16*tiles-1 of out are written with zeros.
+ * Replaces ops.add_rms_norm (engine/kernels/ops.py:27-76) as the prefill
+ * forward uses it (engine/engine.py:448-461). */
+typedef struct {
+  const void *x;      /* [rows, k] bf16 */
+  const void *norm_w; /* [k] bf16, or NULL */
+  void *out;          /* fragment order, `tiles` M tiles */
+  float eps;
+  int32_t rows;
+  int32_t k;          /* multiple of 32 */
+  int32_t tiles;      /* >= ceil(rows / 16) */
+} qdec_rownorm_args;
+int qdec_rownorm(const qdec_rownorm_args *a, qdec_stream_t stream);
+
+/* out = x @ W^T on the matrix cores for x in fragment order (`tiles` M
+ * tiles, a multiple of 16), W tiled [n, k].  A workgroup computes 256 rows x
+ * 128 weight rows; n must be a multiple of 128, k of 64.  flags:
+ *   0            out = bf16(x @ W^T): [rows, n] row-major, or fragment order
+ *                with out_frag;
+ *   QDEC_RES_OUT out = bf16(res + bf16(x @ W^T)), row-major; res may be out;
+ *   QDEC_GLU     W holds n/2 gate rows then n/2 up rows; out = bf16(bf16(
+ *                silu(bf16 gate)) * bf16 up), n/2 columns, row-major or
+ *                fragment order.
+ * fp32 accumulation in k order, rounded as qdec_gemm rounds.
+ * Replaces F.linear and ops.silu_mul (engine/kernels/ops.py:242-267) and the
+ * residual adds of the prefill forward (engine/engine.py:448-461). */
+typedef struct {
+  const void *x;    /* fragment order, `tiles` M tiles */
+  const void *w;    /* tiled [n, k] bf16 */
+  void *out;
+  const void *res;  /* QDEC_RES_OUT: [rows, n] bf16 */
+  uint32_t flags;   /* 0, QDEC_RES_OUT or QDEC_GLU */
+  int32_t rows;
+  int32_t n;
+  int32_t k;
+  int32_t tiles;
+  int32_t out_frag; /* 1: out in fragment order with `tiles` M tiles */
+} qdec_pgemm_args;
+int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream);
+
+/* Per-head RMSNorm (q_norm / k_norm) and RoPE of every row's query and key
+ * heads, with the arithmetic of qdec_attn; the rotated keys and the raw
+ * values go to cache slot pos0 + t of sequence b, the rotated queries back
+ * over the query columns of qkv.
+ * Replaces ops.qkv_post_rows (engine/kernels/ops.py:149-205). */
+typedef struct {
+  void *qkv;            /* [batch*t_rows, (nq + 2*nkv)*head_dim] bf16; queries rewritten */
+  const void *q_norm_w; /* [head_dim] bf16 */
+  const void *k_norm_w; /* [head_dim] bf16 */
+  const void *cos_tab;  /* [cap, head_dim] bf16 */
+  const void *sin_tab;  /* [cap, head_dim] bf16 */
+  void *k_cache;        /* K slab of this layer */
+  void *v_cache;        /* V slab of this layer */
+  float eps;
+  int32_t batch;
+  int32_t t_rows;
+  int32_t pos0;         /* position of row t = 0 */
+  int32_t nq;
+  int32_t nkv;
+  int32_t head_dim;     /* 128 */
+  int32_t cap;          /* multiple of 32; pos0 + t_rows <= cap */
+} qdec_prefill_qk_args;
+int qdec_prefill_qk(const qdec_prefill_qk_args *a, qdec_stream_t stream);
+
+/* Causal GQA attention of the rows at positions pos0 .. pos0 + t_rows - 1
+ * (queries as qdec_prefill_qk leaves them) over cache slots 0 .. position,
+ * written in fragment order (`tiles` M tiles) for the O projection.  A
+ * workgroup takes 64 positions of the 4 query heads of one kv head; same
+ * arithmetic as qdec_attn (base-2 online softmax in fp32, probabilities
+ * rounded to bf16 before P.V, fp32 accumulation, one rounding).
+ * Replaces Engine._attend_prefill (engine/engine.py:464-478: SDPA flash
+ * attention, causal, GQA). */
+typedef struct {
+  const void *qkv;     /* [batch*t_rows, (nq + 2*nkv)*head_dim] bf16 */
+  const void *k_cache;
+  const void *v_cache;
+  void *out;           /* fragment order, rows batch*t_rows, columns nq*head_dim */
+  float sm_scale;      /* 1/sqrt(head_dim) */
+  int32_t batch;
+  int32_t t_rows;
+  int32_t pos0;
+  int32_t nq;
+  int32_t nkv;
+  int32_t head_dim;    /* 128 */
+  int32_t cap;         /* multiple of 32; pos0 + t_rows <= cap */
+  int32_t tiles;       /* >= ceil(batch*t_rows / 16) */
+} qdec_prefill_attn_args;
+int qdec_prefill_attn(const qdec_prefill_attn_args *a, qdec_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,7 +25,9 @@ def test_structs_match_header_fields():
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     for cname, st in (("qdec_embed_args", capi.EmbedArgs), ("qdec_gemm_args", capi.GemmArgs),
                       ("qdec_attn_args", capi.AttnArgs), ("qdec_draft_args", capi.DraftArgs),
-                      ("qdec_accept_args", capi.AcceptArgs)):
+                      ("qdec_accept_args", capi.AcceptArgs), ("qdec_rownorm_args", capi.RownormArgs),
+                      ("qdec_pgemm_args", capi.PgemmArgs), ("qdec_prefill_qk_args", capi.PrefillQkArgs),
+                      ("qdec_prefill_attn_args", capi.PrefillAttnArgs)):
         body = re.search(r"typedef struct (?:\w+ )?\{([^{}]*)\}\s*" + cname + ";", text).group(1)
         fields = re.findall(r"\*?\s*(\w+)\s*;", body)
         assert fields == [f[0] for f in st._fields_], cname
@@ -147,3 +149,47 @@ def test_role_plans_do_not_depend_on_rows():
     for b, cap in ((1, 800), (4, 1568), (32, 4384)):
         c = attn_chunk(b, 8, cap)
         assert c % 32 == 0 and 64 <= c <= cap
+
+
+def _pgemm(**kw):
+    a = capi.PgemmArgs(x=16, w=16, out=16, res=None, flags=0, rows=300, n=256, k=128, tiles=32, out_frag=0)
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(flags=capi.NORM_IN), -3, "flags"),
+    (dict(n=200), -1, "multiple of 128"),
+    (dict(k=96), -1, "multiple of 128, k of 64"),
+    (dict(tiles=24), -1, "tiles"),
+    (dict(rows=513), -1, "tiles"),
+    (dict(flags=capi.RES_OUT), -3, "RES_OUT"),
+    (dict(flags=capi.RES_OUT, res=16, out_frag=1), -3, "RES_OUT"),
+    (dict(out_frag=2), -1, "out_frag"),
+    (dict(x=8), -2, "aligned"),
+    (dict(w=None), -1, "null"),
+])
+def test_prefill_gemm_validation(qlib, kw, code, needle):
+    rc = qlib.so.qdec_prefill_gemm(ctypes.byref(_pgemm(**kw)), None)
+    assert rc == code
+    assert needle in qlib.last_error()
+
+
+def test_prefill_validation(qlib):
+    r = capi.RownormArgs(x=16, norm_w=None, out=16, eps=1e-6, rows=20, k=2560, tiles=1)
+    assert qlib.so.qdec_rownorm(ctypes.byref(r), None) == -1  # 20 rows need 2 tiles
+    r.tiles, r.k = 2, 100
+    assert qlib.so.qdec_rownorm(ctypes.byref(r), None) == -1
+    q = dict(qkv=16, q_norm_w=16, k_norm_w=16, cos_tab=16, sin_tab=16, k_cache=16, v_cache=16, eps=1e-6,
+             batch=2, t_rows=100, pos0=0, nq=32, nkv=8, head_dim=128, cap=128)
+    assert qlib.so.qdec_prefill_qk(ctypes.byref(capi.PrefillQkArgs(**{**q, "head_dim": 64})), None) == -3
+    assert qlib.so.qdec_prefill_qk(ctypes.byref(capi.PrefillQkArgs(**{**q, "pos0": 40})), None) == -1
+    assert qlib.so.qdec_prefill_qk(ctypes.byref(capi.PrefillQkArgs(**{**q, "cap": 120})), None) == -1
+    at = dict(qkv=16, k_cache=16, v_cache=16, out=16, sm_scale=0.088, batch=2, t_rows=100, pos0=0, nq=32,
+              nkv=8, head_dim=128, cap=128, tiles=13)
+    assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "nq": 16})), None) == -3
+    assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "tiles": 12})), None) == -1
+    assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "t_rows": 129})), None) == -1
+    assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "out": 8})), None) == -2
+

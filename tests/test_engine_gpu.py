@@ -59,8 +59,7 @@ def run_state(engine, prompt, n):
     B, S = prompt.shape
     st = DecodeState(engine.model, B, S + n + 18, max_t=16, keep_logits=True)
     st.prefill(prompt.to(engine.device))
-    t_last = (S - 1) % st.max_t + 1
-    first_logits = st.logits[:B * t_last].view(B, t_last, -1)[:, t_last - 1].float().cpu()
+    first_logits = st.logits[:B].float().cpu()
     toks = [st.ids[:B].cpu()]
     logits = [first_logits]
     for _ in range(n - 1):
@@ -85,6 +84,52 @@ def test_logits_and_tokens_vs_oracle(engine, oracle, B, S, n, seed):
     mism = (ref_pick != toks)
     near = gap < TOL * ref.abs().amax(-1)
     assert bool((~mism | near).all()), f"non-near-tie divergence: {mism.nonzero().tolist()}"
+
+
+def v_rows(v):
+    """Rows [..., cap, D] of a V cache stored channel-major ([..., cap/8, D, 8]
+    in the same memory)."""
+    *lead, cap, d = v.shape
+    return v.reshape(*lead, cap // 8, d, 8).transpose(-1, -2).reshape(*lead, cap, d)
+
+
+@pytest.mark.parametrize("B,S,seed", [(1, 100, 11), (3, 70, 12)])
+def test_prefill_vs_oracle_and_chunking(engine, oracle, B, S, seed):
+    """The matrix-core prefill against the oracle's forward over the whole
+    prompt (first-token logits and the filled K/V slots), against the
+    decode-kernel route, and bit for bit against itself in 16-position
+    chunks."""
+    from qdec.runtime import DecodeState, Prefill
+    prompt = prompts(B, S, seed)
+    dprompt = prompt.to(engine.device)
+    st = DecodeState(engine.model, B, S + 18, max_t=16, keep_logits=True)
+    st.prefill(dprompt)
+    logits, ids = st.logits[:B].float().cpu(), st.ids[:B].cpu()
+    kc, vc = st.k_cache.clone(), st.v_cache.clone()
+    assert st.lens.cpu().tolist() == [S] * B
+    okc, ovc = oracle.new_cache(B, st.cap)
+    ref = oracle.forward(prompt, [0] * B, okc, ovc)[:, -1]
+    err = normalized_max_err(logits, ref)
+    print(f"B={B} S={S}: prefill logits normalised max err {err.max().item():.4g}")
+    assert err.max().item() <= TOL
+    near = top2_gap(ref) < TOL * ref.abs().amax(-1)
+    assert bool(((ref.argmax(-1) == ids) | near).all())
+    for got, want in ((kc[:, :, :, :S].float().cpu(), okc[:, :, :, :S]),
+                      (v_rows(vc.float().cpu())[:, :, :, :S], ovc[:, :, :, :S])):
+        assert (got - want).abs().max().item() <= TOL * want.abs().max().item()
+    # the decode kernels, 16 positions per step, land on the same cache
+    st2 = DecodeState(engine.model, B, S + 18, max_t=16, keep_logits=True)
+    st2.prefill_steps(dprompt)
+    t_last = (S - 1) % st2.max_t + 1
+    steps_logits = st2.logits[:B * t_last].view(B, t_last, -1)[:, t_last - 1].float().cpu()
+    assert normalized_max_err(steps_logits, ref).max().item() <= TOL
+    # chunking does not change a bit
+    st3 = DecodeState(engine.model, B, S + 18, max_t=16, keep_logits=True)
+    st3._prefill = Prefill(st3, S, rows=16 * B)
+    st3.prefill(dprompt)
+    assert st3._prefill.chunk == 16
+    assert torch.equal(st3.k_cache, kc) and torch.equal(st3.v_cache, vc)
+    assert torch.equal(st3.ids[:B].cpu(), ids)
 
 
 def test_generate_matches_eager_steps(engine):
