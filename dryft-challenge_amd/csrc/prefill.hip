@@ -18,24 +18,48 @@ namespace {
 // is the A operand and an activation fragment (32 k x 16 rows) the B operand
 // of v_mfma_f32_16x16x32_bf16, and both are one contiguous KiB in their
 // layouts.  Waves 2 x 2: wave (wn, wm) owns 4 weight x 8 activation
-// fragments = 32 accumulators.  Each stage of kPgStageK (two k steps) stages
-// 8 weight + 16 activation fragments per k step through LDS, double
-// buffered; the next stage's loads are in flight while this one computes.
+// fragments = 32 accumulators.  Each stage of kPgStageK (two k steps) moves
+// 8 weight + 16 activation fragments per k step from global memory straight
+// into LDS (global_load_lds_dwordx4: one instruction per 1 KiB fragment, no
+// registers), through a ring of three stage buffers: stage s+2 is in flight
+// while stage s computes, so a load has two compute phases to arrive.
 constexpr int kPgWf = kPgCols / 16;          // weight fragments per k step
 constexpr int kPgXf = kPgRows / 16;          // activation fragments per k step
 constexpr int kPgKs = kPgStageK / 32;        // k steps per stage
 constexpr int kPgFrags = kPgWf + kPgXf;      // fragments per k step
 constexpr int kPgStage = kPgKs * kPgFrags;   // fragments per stage
 constexpr int kPgGroupN = 4;                 // column tiles walked together (x reuse in L2)
+constexpr int kPgRing = 3;                   // stage buffers in LDS
 static_assert(kPgWf == 8 && kPgXf == 16 && kPgKs == 2, "load split below assumes these");
 
 __device__ __forceinline__ uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// 16 bytes per lane from global memory into LDS at byte address lds_addr +
+// 16 * lane (global_load_lds_dwordx4; M0 holds the wave's LDS address).
+// Issued from inline assembly so the compiler does not make every later LDS
+// read wait for all of these loads; the caller waits (vmcnt) and
+// synchronises the workgroup itself.
+// M0 is saved and restored around the load.
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+      : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
+
+// s_waitcnt encodings (gfx9 family): vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8; the other counters at their maximum (no wait).
+constexpr int kVmcnt0 = (7 << 4) | (15 << 8);
+constexpr int kVmcnt12 = 12 | (7 << 4) | (15 << 8);
 
 template <uint32_t FLAGS>
 __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
   constexpr bool GLU = (FLAGS & QDEC_GLU) != 0;
   constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
-  __shared__ uint4 lds[2 * kPgStage * 64];  // [buffer][k step][fragment][lane]
+  __shared__ uint4 lds[kPgRing * kPgStage * 64];  // [ring slot][k step][fragment][lane]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int wn = wave & 1, wm = wave >> 1;
@@ -68,22 +92,19 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
   const uint16_t *wb1 = p.w + (size_t)wtile(wave + 4) * KS * 512 + lane * 8;
   const uint16_t *xb = p.x + (size_t)(tm * kPgXf + wave) * 512 + lane * 8;
   const size_t xks = (size_t)p.tiles * 512;  // elements per k step of x
-  uint4 st[kPgKs * 6];
-  auto gload = [&](int s) {
+  // Stage s into ring slot `slot`: this wave moves fragments wave + 4q of
+  // each k step (q = 0, 1: weights; q = 2..5: activations).
+  const uint32_t lds0 = lds_addr(lds);
+  auto dma = [&](int s, int slot) {
 #pragma unroll
     for (int j = 0; j < kPgKs; ++j) {
       const int ks = s * kPgKs + j;
-      st[j * 6 + 0] = ld16(wb0 + (size_t)ks * 512);
-      st[j * 6 + 1] = ld16(wb1 + (size_t)ks * 512);
+      const uint32_t dst = lds0 + (uint32_t)(((slot * kPgKs + j) * kPgFrags + wave) * 1024);
+      dma16(wb0 + (size_t)ks * 512, dst);
+      dma16(wb1 + (size_t)ks * 512, dst + 4 * 1024);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) st[j * 6 + 2 + q] = ld16(xb + ks * xks + q * 4 * 512);
+      for (int q = 0; q < 4; ++q) dma16(xb + ks * xks + q * 4 * 512, dst + (2 + q) * 4 * 1024);
     }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < kPgKs; ++j)
-#pragma unroll
-      for (int q = 0; q < 6; ++q) lds[((buf * kPgKs + j) * kPgFrags + q * 4 + wave) * 64 + lane] = st[j * 6 + q];
   };
   // This wave's weight fragments (GLU: gate 0, 1 pair with up 2, 3).
   auto wf = [&](int i) -> int {
@@ -100,15 +121,23 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
     for (int q = 0; q < 8; ++q) acc[i][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nst = p.k / kPgStageK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
+  dma(0, 0);
+  if (nst > 1) dma(1, 1);
+  int slot = 0;
   for (int s = 0; s < nst; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < nst) gload(s + 1);
+    // this wave's loads of stage s are done once at most the next stage's
+    // are outstanding; the barrier makes every wave's visible and frees
+    // the slot of stage s-1 for stage s+2
+    if (s + 1 < nst)
+      __builtin_amdgcn_s_waitcnt(kVmcnt12);
+    else
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (s + 2 < nst) dma(s + 2, slot == 0 ? 2 : slot - 1);
 #pragma unroll
     for (int j = 0; j < kPgKs; ++j) {
-      const uint4 *S = lds + (size_t)(buf * kPgKs + j) * kPgFrags * 64 + lane;
+      const uint4 *S = lds + (size_t)(slot * kPgKs + j) * kPgFrags * 64 + lane;
       uint4 a[4], bx[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) a[i] = S[wf(i) * 64];
@@ -119,8 +148,7 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) acc[i][q] = mfma16x16x32(a[i], bx[q], acc[i][q]);
     }
-    if (s + 1 < nst) sstore(buf ^ 1);
-    __syncthreads();
+    slot = slot == kPgRing - 1 ? 0 : slot + 1;
   }
 
   // Epilogue: lane holds columns n0 .. n0+3 of row m for every fragment pair.
