@@ -50,6 +50,18 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds_addr) {
 }
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)reinterpret_cast<uintptr_t>(p); }
 
+// Maximum of v over the lane pairs (l, l ^ 16) and then (l, l ^ 32), with
+// gfx950's row swaps instead of LDS permutes: after v_permlane16_swap the two
+// outputs hold the odd / even 16-lane rows exchanged, after
+// v_permlane32_swap the two halves, so the maximum of both outputs is the
+// pairwise maximum in every lane.
+__device__ __forceinline__ float max_xor16_32(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // s_waitcnt encodings (gfx9 family): vmcnt in bits 3:0 and 15:14, expcnt
 // 6:4, lgkmcnt 11:8; the other counters at their maximum (no wait).
 constexpr int kVmcnt0 = (7 << 4) | (15 << 8);
@@ -226,24 +238,32 @@ __global__ void __launch_bounds__(256) pqk_kernel(const PqkParams p) {
 // ---------------------------------------------------------------- attention
 // A workgroup takes kPaRows positions of the 4 query heads of one kv head of
 // one sequence; wave w takes head 4*kvh + w, its positions as 4 M tiles of
-// 16 rows.  Blocks of 32 cache slots are staged in LDS (double buffered) in
-// MFMA operand order and shared by the 4 waves:
+// 16 rows.  Blocks of 32 cache slots go from global memory straight into
+// LDS (global_load_lds_dwordx4 with per-lane gather addresses, so every
+// fragment lands in MFMA operand order), three blocks in a ring, two ahead
+// of the compute, shared by the 4 waves:
 //   K fragment (s, h): lane (c, g) holds slot 8*(c >> 2) + (c & 3) + 4h,
 //     channels 32s + 8g .. +8: the slot order that makes the score registers
 //     of S^T = K . Q^T exactly the B operand of O^T += V^T . P^T (each lane
 //     ends up with 8 consecutive slots of one query row);
 //   V fragment dt: lane (c, g) holds channel 16dt + c, slots 8g .. 8g+7 --
-//     the channel-major cache layout, copied as is.
-// Online softmax in base 2 with fp32 state per row, probabilities rounded to
-// bf16 for the P.V product; slots past a row's position are masked, slots
-// past the block's last row are zeroed in V (the cache may hold anything
-// there, and 0 * NaN would poison the product).
+//     16 contiguous bytes of the channel-major cache.
+// Online softmax in base 2 with fp32 state per row (running max kept in
+// score units, exp2(s * scale - m * scale) as one FMA), probabilities rounded
+// to bf16 for the P.V product, two tiles at a time in straight-line code
+// (independent MFMA chains and softmaxes interleave).  Only blocks that
+// cross some row's position are masked; the accumulators are rescaled only
+// when some row's max moved.
+// Slots past the block's last row are zeroed in V after the LDS read (the
+// cache may hold anything there, and 0 * NaN would poison the product).
 constexpr int kPaKFrags = 8, kPaVFrags = 8;
 constexpr int kPaBlockVec = (kPaKFrags + kPaVFrags) * 64;  // uint4 per staged block
+constexpr int kPaRing = 3;
+constexpr int kVmcnt4 = 4 | (7 << 4) | (15 << 8);
 
 __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
   constexpr int D = 128;
-  __shared__ uint4 lds[2 * kPaBlockVec];
+  __shared__ uint4 lds[kPaRing * kPaBlockVec];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int T = p.t_rows;
@@ -262,6 +282,8 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
   const uint16_t *kc = p.k_cache + slab;
   const uint16_t *vc = p.v_cache + slab;
   const float NEG_INF = -__builtin_huge_valf();
+  const float scale = p.scale_log2;
+  const bool rows_full = t0 + kPaRows - 1 <= tlast;  // all 64 rows are real
 
   // Queries as B operands: row col of M tile mt, channels 32s + 8*grp.
   uint4 qf[4][4];
@@ -276,38 +298,23 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
     for (int s = 0; s < 4; ++s) qf[mt][s] = valid ? ld16(qrow + s * 32) : zero4();
   }
 
-  uint4 kr[2], vr[2];
-  auto gload = [&](int j) {
+  // Block j into ring slot `slot`: this wave gathers K fragments wave and
+  // wave + 4 (index 2s + h) and V fragments wave and wave + 4.
+  const uint32_t lds0 = lds_addr(lds);
+  const uint16_t *kg = kc + (size_t)(8 * (col >> 2) + (col & 3)) * D + 8 * grp;
+  const uint16_t *vg = vc + (size_t)grp * D * 8 + col * 8;
+  auto dma_block = [&](int j, int slot) {
     const int s0 = j * 32;
+    const uint32_t base = lds0 + (uint32_t)(slot * kPaBlockVec * 16);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int u = tid + 256 * i;
-      kr[i] = ld16(kc + (size_t)(s0 + (u >> 4)) * D + (u & 15) * 8);
-      vr[i] = ld16(vc + (size_t)(s0 >> 3) * D * 8 + (size_t)u * 8);
+      const int f = wave + 4 * i;
+      dma16(kg + (size_t)(s0 + 4 * (f & 1)) * D + 32 * (f >> 1), base + f * 1024);
     }
-  };
-  auto sstore = [&](int buf, int j) {
-    uint4 *B = lds + buf * kPaBlockVec;
-    const int s0 = j * 32;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int u = tid + 256 * i;
-      const int slot = u >> 4, c16 = u & 15;
-      B[((c16 >> 2) * 2 + ((slot >> 2) & 1)) * 64 + 4 * (slot >> 3) + (slot & 3) + 16 * (c16 & 3)] = kr[i];
-      const int gi = u >> 7, ch = u & 127;
-      uint4 v = vr[i];
-      const int sb = s0 + 8 * gi;  // first slot of this 8-slot group
-      if (sb + 7 > last) {
-        uint32_t keep[4];
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-          keep[d] = (sb + 2 * d <= last ? 0x0000ffffu : 0u) | (sb + 2 * d + 1 <= last ? 0xffff0000u : 0u);
-        v.x &= keep[0];
-        v.y &= keep[1];
-        v.z &= keep[2];
-        v.w &= keep[3];
-      }
-      B[(kPaKFrags + (ch >> 4)) * 64 + (ch & 15) + 16 * gi] = v;
+      const int dt = wave + 4 * i;
+      dma16(vg + (size_t)(s0 >> 3) * D * 8 + dt * 128, base + (kPaKFrags + dt) * 1024);
     }
   };
 
@@ -321,13 +328,24 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
     for (int dt = 0; dt < 8; ++dt) acc[mt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  gload(0);
-  sstore(0, 0);
-  __syncthreads();
+  // The query loads complete here, so no wait inside the loop (where it
+  // would also wait for the blocks in flight) is needed for them.
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+  dma_block(0, 0);
+  if (nb > 1) dma_block(1, 1);
+  int slot = 0;
   for (int j = 0; j < nb; ++j) {
-    const int buf = j & 1;
-    if (j + 1 < nb) gload(j + 1);
-    const uint4 *B = lds + buf * kPaBlockVec + lane;
+    // this wave's loads of block j are done once at most the next block's
+    // are outstanding; the barrier makes every wave's visible and frees the
+    // slot of block j-1 for block j+2
+    if (j + 1 < nb)
+      __builtin_amdgcn_s_waitcnt(kVmcnt4);
+    else
+      __builtin_amdgcn_s_waitcnt(kVmcnt0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (j + 2 < nb) dma_block(j + 2, slot == 0 ? kPaRing - 1 : slot - 1);
+    const uint4 *B = lds + slot * kPaBlockVec + lane;
     uint4 ka[4], kb[4], vf[8];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -337,48 +355,84 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) vf[dt] = B[(kPaKFrags + dt) * 64];
     const int s0 = j * 32;
+    const int sb = s0 + 8 * grp;  // first of this lane's 8 slots
+    if (sb + 7 > last) {          // slots past the last row: zero V
+      uint32_t keep[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int tf = t0 + mt * 16;  // first row of the tile
-      if (tf > tlast || s0 > p.pos0 + min(tf + 15, tlast)) continue;  // tile empty or sees none of the block
-      f32x4_t sa = f32x4_t{0.f, 0.f, 0.f, 0.f}, sb = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int d = 0; d < 4; ++d)
+        keep[d] = (sb + 2 * d <= last ? 0x0000ffffu : 0u) | (sb + 2 * d + 1 <= last ? 0xffff0000u : 0u);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        sa = mfma16x16x32(ka[s], qf[mt][s], sa);
-        sb = mfma16x16x32(kb[s], qf[mt][s], sb);
+      for (int dt = 0; dt < 8; ++dt) {
+        vf[dt].x &= keep[0];
+        vf[dt].y &= keep[1];
+        vf[dt].z &= keep[2];
+        vf[dt].w &= keep[3];
       }
-      float sc[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int sl = s0 + 8 * grp + i;
-        sc[i] = (sl <= qpos[mt]) ? sa[i] * p.scale_log2 : NEG_INF;
-        sc[4 + i] = (sl + 4 <= qpos[mt]) ? sb[i] * p.scale_log2 : NEG_INF;
-      }
+    }
+    // Online softmax of one tile's 8 scores per lane (masked ones -inf):
+    // updates the row state, returns the rescale factor and the bf16
+    // probabilities as the B operand of the P.V product.
+    auto softmax = [&](int mt, const float (&sc)[8], float &alpha, uint4 &pf) {
       float bmax = sc[0];
 #pragma unroll
       for (int e = 1; e < 8; ++e) bmax = fmaxf(bmax, sc[e]);
-      bmax = fmaxf(bmax, shfl_xor(bmax, 16));
-      bmax = fmaxf(bmax, shfl_xor(bmax, 32));
+      bmax = max_xor16_32(bmax);
       const float m_new = fmaxf(m_run[mt], bmax);
-      const float alpha = (m_new == NEG_INF) ? 1.0f : exp2f(m_run[mt] - m_new);
+      alpha = (m_new == NEG_INF) ? 1.0f : __builtin_amdgcn_exp2f((m_run[mt] - m_new) * scale);
+      const float mc = m_new * scale;
       float pj[8];
       float psum = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        pj[e] = (sc[e] == NEG_INF) ? 0.f : exp2f(sc[e] - m_new);
+        pj[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[e], scale, -mc));
         psum += pj[e];
       }
       l_run[mt] = l_run[mt] * alpha + psum;
       m_run[mt] = m_new;
-      const uint4 pf = pack8(pj);
+      pf = pack8(pj);
+    };
+    // Masks only where the block crosses some row's position (the diagonal,
+    // rows past the end); a tile that sees none of the block gets all -inf
+    // and leaves its rows unchanged (alpha 1, p 0).
+    const bool masked = !(rows_full && s0 + 31 <= p.pos0 + t0);
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        acc[mt][dt] *= alpha;
-        acc[mt][dt] = mfma16x16x32(vf[dt], pf, acc[mt][dt]);
+    for (int m2 = 0; m2 < 4; m2 += 2) {
+      f32x4_t sa[2], sbv[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) sa[u] = sbv[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          sa[u] = mfma16x16x32(ka[s], qf[m2 + u][s], sa[u]);
+          sbv[u] = mfma16x16x32(kb[s], qf[m2 + u][s], sbv[u]);
+        }
+      float alpha[2];
+      uint4 pf[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float sc[8] = {sa[u][0], sa[u][1], sa[u][2], sa[u][3], sbv[u][0], sbv[u][1], sbv[u][2], sbv[u][3]};
+        if (masked) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (sb + i > qpos[m2 + u]) sc[i] = NEG_INF;
+            if (sb + 4 + i > qpos[m2 + u]) sc[4 + i] = NEG_INF;
+          }
+        }
+        softmax(m2 + u, sc, alpha[u], pf[u]);
       }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        if (__any(alpha[u] != 1.0f)) {
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) acc[m2 + u][dt] *= alpha[u];
+        }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) acc[m2 + u][dt] = mfma16x16x32(vf[dt], pf[u], acc[m2 + u][dt]);
     }
-    if (j + 1 < nb) sstore(buf ^ 1, j + 1);
-    __syncthreads();
+    slot = slot == kPaRing - 1 ? 0 : slot + 1;
   }
 
   // Rows in fragment order for the O projection: lane holds channels
