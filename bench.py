@@ -20,9 +20,12 @@ Printed JSON fields beyond the driver contract:
   cpu_baseline  the Transformers CPU greedy loop on the same checkpoint
                 (the reference's own oracle path), on a bounded sample;
   step_hbm      algorithmic bytes per step (weights + KV read/write) / step time;
-  batched       decode tok/s of configs[2] (batch 8, 1024 cached) and configs[3]
-                (batch 32, 4096 cached) on synthetic cache contents (skip
-                with --no-batched);
+  prefill       prompt processing of the headline prompt (time to first
+                token: the prompt through the 36 layers on the matrix cores,
+                lm_head + argmax of the last position), tok/s and TFLOP/s;
+  batched       decode tok/s of configs[2] (batch 8, 1024 prompt tokens) and
+                configs[3] (batch 32, 4096), each after a real (timed)
+                prefill of its random prompts (skip with --no-batched);
   speculation   BASELINE.json configs[4] through the same engine: batch 4,
                 1024-token prompts tiling a seeded 64-token motif with 10%
                 random substitutions, 512 new tokens, n-gram drafter (n=3,
@@ -90,6 +93,35 @@ def time_gemm_role(engine, state, role, reps=5):
     return e0.elapsed_time(e1) / 1e3 / (reps * len(args))
 
 
+def prefill_flops(mc, batch, prompt_len):
+    """Algorithmic flops of a prefill: every layer matrix once per prompt
+    token (2 flops per weight), causal attention (QK and PV over slots
+    0..t for position t), the lm_head for the last position of each
+    sequence."""
+    per_tok = mc.n_layers * (mc.n_qkv * mc.hidden + mc.hidden * mc.nq * mc.head_dim
+                             + 2 * mc.inter * mc.hidden + mc.hidden * mc.inter)
+    attn = mc.n_layers * mc.nq * 4 * mc.head_dim * prompt_len * (prompt_len + 1) // 2
+    return batch * (2 * per_tok * prompt_len + attn + 2 * mc.vocab * mc.hidden)
+
+
+def time_prefill(state, prompt, reps=2):
+    """Prefill of ``prompt`` (device [B, S]) into ``state``: the best of
+    ``reps`` runs (the first also allocates the prefill buffers), wall clock
+    around device synchronisations."""
+    import torch
+    best = float("inf")
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        state.prefill(prompt)
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+    B, S = prompt.shape
+    fl = prefill_flops(state.model.cfg, B, S)
+    return {"tokens": B * S, "ms": round(best * 1e3, 3), "tok_s": round(B * S / best, 1),
+            "tflops": round(fl / best / 1e12, 1)}
+
+
 def motif_prompts(batch, length, vocab, seed, motif=64, subst=0.10):
     """Each sequence tiles its own seeded random ``motif``-token pattern to
     ``length`` tokens, then replaces a ``subst`` fraction of positions with
@@ -144,21 +176,18 @@ def spec_bench(eng, vocab, batch=4, prompt_len=1024, new_tokens=512, seed=5):
 
 
 def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):
-    """Decode throughput of a batched configuration with synthetic cache
-    contents: the shape's KV cache is filled with random bf16 values (the
-    step's cost does not depend on them) instead of a real prefill, every
-    sequence sits at ``prompt_len`` cached tokens, and the timed replays walk
-    the workload's positions like the headline measurement."""
+    """Decode throughput of a batched configuration: its prompts (uniform
+    random tokens from ``seed``) are prefilled for real (timed), every
+    sequence then sits at ``prompt_len`` cached tokens, and the timed replays
+    walk the workload's positions like the headline measurement."""
     import torch
     mc = eng.model.cfg
     sh = eng._shape_for(batch, prompt_len, new_tokens)
     st = sh.state
-    g = torch.Generator(device=eng.device).manual_seed(seed)
-    for cache in (st.k_cache, st.v_cache):
-        for layer in range(cache.shape[0]):
-            cache[layer].normal_(0.0, 1.0, generator=g)
-    st.ids[:batch].random_(0, mc.vocab, generator=g)
-    st.lens.fill_(prompt_len)
+    g = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(0, mc.vocab, (batch, prompt_len), generator=g).to(eng.device)
+    pf = time_prefill(st, prompt)
+    log(f"prefill {batch}x{prompt_len}: {pf}")
     last_pos = prompt_len + new_tokens - 2
     span = last_pos - prompt_len + 1
     done = [0]
@@ -184,7 +213,8 @@ def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):
     kv_bytes = 2 * mc.n_layers * batch * mc.nkv * st.cap * mc.head_dim * 2
     res = {"workload": f"qwen3-4b bf16 bs{batch} prompt{prompt_len} new{new_tokens}",
            "tok_s": round(batch * steps / elapsed, 2), "ms_per_step": round(1e3 * elapsed / steps, 4),
-           "steps": steps, "cache": f"synthetic random K/V, {kv_bytes / 1e9:.1f} GB allocated"}
+           "steps": steps, "cache": f"prefilled from the prompts, {kv_bytes / 1e9:.1f} GB allocated",
+           "prefill": pf}
     eng.shape = None
     del sh, st
     torch.cuda.empty_cache()
@@ -298,10 +328,8 @@ def main():
         torch.cuda.synchronize()
         log(f"pmc: {args.pmc_role} x {mc.n_layers} layers x 6 rounds, then 6 copies of {src.numel()} bytes")
         return
-    t0 = time.perf_counter()
-    st.prefill(prompt.to(eng.device))
-    torch.cuda.synchronize()
-    log(f"prefill {B}x{S}: {time.perf_counter() - t0:.3f}s")
+    prefill = time_prefill(st, prompt.to(eng.device), reps=3)
+    log(f"prefill {B}x{S}: {prefill}")
     graph = sh.graph
     last_pos = S + N - 2  # the last decode step of the workload feeds position S+N-2
     span = last_pos - S + 1
@@ -402,6 +430,7 @@ def main():
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
         "role_us_per_launch": roles,
+        "prefill": prefill,
         "batched": batched or None,
         "speculation": spec,
         "cpu_baseline": cpu,
