@@ -288,6 +288,8 @@ def main():
                          "config's batch), then a 512 MiB device copy as the counter calibration, "
                          "for rocprofv3 --pmc")
     ap.add_argument("--cpu-prompt", type=int, default=64)
+    ap.add_argument("--prefill-only", type=int, default=0, metavar="REPS",
+                    help="only prefill the config's prompts REPS times and print their timing (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (every box has one MI355X); "
@@ -314,6 +316,10 @@ def main():
     prompt = torch.randint(0, mc.vocab, (B, S), generator=g)
     sh = eng._shape_for(B, S, N)
     st = sh.state
+    if args.prefill_only:
+        pf = time_prefill(st, prompt.to(eng.device), reps=args.prefill_only)
+        print(json.dumps({"prefill": pf, "config": desc}), flush=True)
+        return
     if args.pmc_role:
         if B == 1:
             st.prefill(prompt.to(eng.device))
