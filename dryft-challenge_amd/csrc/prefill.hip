@@ -13,24 +13,31 @@ namespace qdec {
 namespace {
 
 // ------------------------------------------------------------------ product
-// A workgroup of 4 wavefronts computes a kPgRows x kPgCols tile of the
+// A workgroup of 4 wavefronts computes a kPgRows x (32 WN) tile of the
 // transposed product D = W . x^T: a weight fragment (16 weight rows x 32 k)
 // is the A operand and an activation fragment (32 k x 16 rows) the B operand
 // of v_mfma_f32_16x16x32_bf16, and both are one contiguous KiB in their
-// layouts.  Waves 2 x 2: wave (wn, wm) owns 4 weight x 8 activation
-// fragments = 32 accumulators.  Each stage of kPgStageK (two k steps) moves
-// 8 weight + 16 activation fragments per k step from global memory straight
-// into LDS (global_load_lds_dwordx4: one instruction per 1 KiB fragment, no
-// registers), through a ring of three stage buffers: stage s+2 is in flight
-// while stage s computes, so a load has two compute phases to arrive.
-constexpr int kPgWf = kPgCols / 16;          // weight fragments per k step
-constexpr int kPgXf = kPgRows / 16;          // activation fragments per k step
-constexpr int kPgKs = kPgStageK / 32;        // k steps per stage
-constexpr int kPgFrags = kPgWf + kPgXf;      // fragments per k step
-constexpr int kPgStage = kPgKs * kPgFrags;   // fragments per stage
-constexpr int kPgGroupN = 4;                 // column tiles walked together (x reuse in L2)
-constexpr int kPgRing = 3;                   // stage buffers in LDS
-static_assert(kPgWf == 8 && kPgXf == 16 && kPgKs == 2, "load split below assumes these");
+// layouts.  Waves 2 x 2: wave (wn, wm) owns WN weight x 8 activation
+// fragments (WN = 4: 32 accumulators, WN = 8: 64).  Every fragment moves
+// from global memory straight into LDS (global_load_lds_dwordx4: one
+// instruction per 1 KiB fragment, no registers) through a ring of stage
+// buffers, RING - 1 stages in flight while one computes:
+//   WN = 4: stages of two k steps (48 KiB), RING 3;
+//   WN = 8: stages of one k step (32 KiB), RING 4.
+// The wider tile reads a third fewer LDS bytes per MFMA; the narrower one
+// makes twice as many workgroups (better for few row tiles).
+template <int WN>
+struct PgShape {
+  static constexpr int Wf = 2 * WN;                 // weight fragments per k step
+  static constexpr int Xf = kPgRows / 16;           // activation fragments per k step
+  static constexpr int KS = WN == 4 ? 2 : 1;        // k steps per stage
+  static constexpr int RING = WN == 4 ? 3 : 4;      // stage buffers
+  static constexpr int Frags = Wf + Xf;             // fragments per k step
+  static constexpr int Stage = KS * Frags;          // fragments per stage
+  static constexpr int Loads = Stage / 4;           // loads per wave per stage
+  static constexpr int WQ = Wf / 4;                 // weight loads per wave per k step
+};
+constexpr int kPgGroupN = 4;  // column tiles walked together (x reuse in L2)
 
 __device__ __forceinline__ uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
@@ -64,14 +71,15 @@ __device__ __forceinline__ float max_xor16_32(float v) {
 
 // s_waitcnt encodings (gfx9 family): vmcnt in bits 3:0 and 15:14, expcnt
 // 6:4, lgkmcnt 11:8; the other counters at their maximum (no wait).
-constexpr int kVmcnt0 = (7 << 4) | (15 << 8);
-constexpr int kVmcnt12 = 12 | (7 << 4) | (15 << 8);
+constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kVmcnt0 = vmcnt_enc(0);
 
-template <uint32_t FLAGS>
+template <uint32_t FLAGS, int WN>
 __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
+  using S = PgShape<WN>;
   constexpr bool GLU = (FLAGS & QDEC_GLU) != 0;
   constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
-  __shared__ uint4 lds[kPgRing * kPgStage * 64];  // [ring slot][k step][fragment][lane]
+  __shared__ uint4 lds[S::RING * S::Stage * 64];  // [ring slot][k step][fragment][lane]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int wn = wave & 1, wm = wave >> 1;
@@ -83,84 +91,87 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
   int id = blockIdx.x;
   const int G = gridDim.x;
   if ((G & 7) == 0) id = (id & 7) * (G >> 3) + (id >> 3);
-  const int ntm = p.tiles / kPgXf;
+  const int ntm = p.tiles / S::Xf;
   const int gsz = kPgGroupN * ntm;
   const int g = id / gsz, r = id - g * gsz;
   const int gn = min(kPgGroupN, p.wg_n - g * kPgGroupN);
   const int tm = r / gn, tn = g * kPgGroupN + (r - (r / gn) * gn);
 
   const int KS = p.k >> 5;
-  // Weight tile of workgroup fragment f (GLU: 4 gate tiles, then the 4
+  // Weight tile of workgroup fragment f (GLU: WN gate tiles, then the WN
   // matching up tiles).
   auto wtile = [&](int f) -> int {
     if constexpr (GLU)
-      return f < kPgWf / 2 ? tn * (kPgWf / 2) + f : p.up_tiles + tn * (kPgWf / 2) + f - kPgWf / 2;
+      return f < WN ? tn * WN + f : p.up_tiles + tn * WN + f - WN;
     else
-      return tn * kPgWf + f;
+      return tn * S::Wf + f;
   };
-  // Loads of one stage: this wave moves fragments wave + 4q of each k step
-  // (q = 0, 1: weights; q = 2..5: activations).
-  const uint16_t *wb0 = p.w + (size_t)wtile(wave) * KS * 512 + lane * 8;
-  const uint16_t *wb1 = p.w + (size_t)wtile(wave + 4) * KS * 512 + lane * 8;
-  const uint16_t *xb = p.x + (size_t)(tm * kPgXf + wave) * 512 + lane * 8;
+  // Loads of one k step: this wave moves fragments wave + 4q (q < WQ:
+  // weights, then activations).
+  const uint16_t *wb[S::WQ];
+#pragma unroll
+  for (int q = 0; q < S::WQ; ++q) wb[q] = p.w + (size_t)wtile(wave + 4 * q) * KS * 512 + lane * 8;
+  const uint16_t *xb = p.x + (size_t)(tm * S::Xf + wave) * 512 + lane * 8;
   const size_t xks = (size_t)p.tiles * 512;  // elements per k step of x
-  // Stage s into ring slot `slot`: this wave moves fragments wave + 4q of
-  // each k step (q = 0, 1: weights; q = 2..5: activations).
   const uint32_t lds0 = lds_addr(lds);
   auto dma = [&](int s, int slot) {
 #pragma unroll
-    for (int j = 0; j < kPgKs; ++j) {
-      const int ks = s * kPgKs + j;
-      const uint32_t dst = lds0 + (uint32_t)(((slot * kPgKs + j) * kPgFrags + wave) * 1024);
-      dma16(wb0 + (size_t)ks * 512, dst);
-      dma16(wb1 + (size_t)ks * 512, dst + 4 * 1024);
+    for (int j = 0; j < S::KS; ++j) {
+      const int ks = s * S::KS + j;
+      const uint32_t dst = lds0 + (uint32_t)(((slot * S::KS + j) * S::Frags + wave) * 1024);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) dma16(xb + ks * xks + q * 4 * 512, dst + (2 + q) * 4 * 1024);
+      for (int q = 0; q < S::WQ; ++q) dma16(wb[q] + (size_t)ks * 512, dst + q * 4 * 1024);
+#pragma unroll
+      for (int q = 0; q < S::Xf / 4; ++q) dma16(xb + ks * xks + q * 4 * 512, dst + (S::WQ + q) * 4 * 1024);
     }
   };
-  // This wave's weight fragments (GLU: gate 0, 1 pair with up 2, 3).
+  // This wave's weight fragments (GLU: gate i pairs with up i + WN/2).
   auto wf = [&](int i) -> int {
     if constexpr (GLU)
-      return i < 2 ? wn * 2 + i : kPgWf / 2 + wn * 2 + i - 2;
+      return i < WN / 2 ? wn * (WN / 2) + i : WN + wn * (WN / 2) + i - WN / 2;
     else
-      return wn * 4 + i;
+      return wn * WN + i;
   };
 
-  f32x4_t acc[4][8];
+  f32x4_t acc[WN][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WN; ++i)
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[i][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nst = p.k / kPgStageK;
-  dma(0, 0);
-  if (nst > 1) dma(1, 1);
+  const int nst = p.k / (32 * S::KS);
+#pragma unroll
+  for (int s = 0; s < S::RING - 1; ++s)
+    if (s < nst) dma(s, s);
   int slot = 0;
   for (int s = 0; s < nst; ++s) {
-    // this wave's loads of stage s are done once at most the next stage's
-    // are outstanding; the barrier makes every wave's visible and frees
-    // the slot of stage s-1 for stage s+2
-    if (s + 1 < nst)
-      __builtin_amdgcn_s_waitcnt(kVmcnt12);
+    // this wave's loads of stage s are done once at most the younger
+    // stages' are outstanding; the barrier makes every wave's visible and
+    // frees the slot of stage s-1 for stage s + RING - 1
+    const int younger = min(S::RING - 2, nst - 1 - s);
+    if (younger >= 2)
+      __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * S::Loads));
+    else if (younger == 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_enc(S::Loads));
     else
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (s + 2 < nst) dma(s + 2, slot == 0 ? 2 : slot - 1);
+    if (s + S::RING - 1 < nst) dma(s + S::RING - 1, slot == 0 ? S::RING - 1 : slot - 1);
 #pragma unroll
-    for (int j = 0; j < kPgKs; ++j) {
-      const uint4 *S = lds + (size_t)(slot * kPgKs + j) * kPgFrags * 64 + lane;
-      uint4 a[4], bx[8];
+    for (int j = 0; j < S::KS; ++j) {
+      const uint4 *L = lds + (size_t)(slot * S::KS + j) * S::Frags * 64 + lane;
+      uint4 a[WN], bx[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = S[wf(i) * 64];
+      for (int i = 0; i < WN; ++i) a[i] = L[wf(i) * 64];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) bx[q] = S[(kPgWf + wm * 8 + q) * 64];
+      for (int q = 0; q < 8; ++q) bx[q] = L[(S::Wf + wm * 8 + q) * 64];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < WN; ++i)
 #pragma unroll
         for (int q = 0; q < 8; ++q) acc[i][q] = mfma16x16x32(a[i], bx[q], acc[i][q]);
     }
-    slot = slot == kPgRing - 1 ? 0 : slot + 1;
+    slot = slot == S::RING - 1 ? 0 : slot + 1;
   }
 
   // Epilogue: lane holds columns n0 .. n0+3 of row m for every fragment pair.
@@ -168,26 +179,26 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
     uint16_t *dst = p.ofrag ? p.out + frag_off(m, n0, p.tiles) : p.out + (size_t)m * p.n_out + n0;
     *reinterpret_cast<uint2 *>(dst) = o;
   };
-  const int m_base = (tm * kPgXf + wm * 8) * 16 + col;
+  const int m_base = (tm * S::Xf + wm * 8) * 16 + col;
 #pragma unroll
   for (int q = 0; q < 8; ++q) {
     const int m = m_base + q * 16;
     if (m >= p.rows) continue;
     if constexpr (GLU) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < WN / 2; ++i) {
         float o4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float gv = rbf(acc[i][q][e]);
-          const float uv = rbf(acc[i + 2][q][e]);
+          const float uv = rbf(acc[i + WN / 2][q][e]);
           o4[e] = rbf(gv / (1.0f + expf(-gv))) * uv;
         }
         store(m, wtile(wf(i)) * 16 + 4 * grp, make_uint2(pack2(o4[0], o4[1]), pack2(o4[2], o4[3])));
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < WN; ++i) {
         const int n0 = wtile(wf(i)) * 16 + 4 * grp;
         uint2 o;
         if constexpr (RES) {
@@ -457,15 +468,20 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
 
 }  // namespace
 
-hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s) {
-  const dim3 grid(p.wg_n * (p.tiles / kPgXf)), block(256);
+template <int WN>
+hipError_t launch_pgemm_wn(const PgemmParams &p, uint32_t flags, hipStream_t s) {
+  const dim3 grid(p.wg_n * (p.tiles / PgShape<WN>::Xf)), block(256);
   switch (flags) {
-    case 0u: hipLaunchKernelGGL(pgemm_kernel<0u>, grid, block, 0, s, p); break;
-    case QDEC_RES_OUT: hipLaunchKernelGGL(pgemm_kernel<QDEC_RES_OUT>, grid, block, 0, s, p); break;
-    case QDEC_GLU: hipLaunchKernelGGL(pgemm_kernel<QDEC_GLU>, grid, block, 0, s, p); break;
+    case 0u: hipLaunchKernelGGL((pgemm_kernel<0u, WN>), grid, block, 0, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL((pgemm_kernel<QDEC_RES_OUT, WN>), grid, block, 0, s, p); break;
+    case QDEC_GLU: hipLaunchKernelGGL((pgemm_kernel<QDEC_GLU, WN>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;
+}
+
+hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s) {
+  return p.tile_cols == 256 ? launch_pgemm_wn<8>(p, flags, s) : launch_pgemm_wn<4>(p, flags, s);
 }
 
 hipError_t launch_prefill_qk(const PqkParams &p, hipStream_t s) {

@@ -286,7 +286,9 @@ int qdec_rownorm(const qdec_rownorm_args *a, qdec_stream_t stream);
 
 /* out = x @ W^T on the matrix cores for x in fragment order (`tiles` M
  * tiles, a multiple of 16), W tiled [n, k].  A workgroup computes 256 rows x
- * 128 weight rows; n must be a multiple of 128, k of 64.  flags:
+ * tile_cols weight rows (128 or 256; 0 picks 256 when n allows it and the
+ * launch still has at least 768 workgroups); n must be a multiple of the
+ * tile, k of 64.  flags:
  *   0            out = bf16(x @ W^T): [rows, n] row-major, or fragment order
  *                with out_frag;
  *   QDEC_RES_OUT out = bf16(res + bf16(x @ W^T)), row-major; res may be out;
@@ -307,6 +309,7 @@ typedef struct {
   int32_t k;
   int32_t tiles;
   int32_t out_frag; /* 1: out in fragment order with `tiles` M tiles */
+  int32_t tile_cols; /* 0, 128 or 256 */
 } qdec_pgemm_args;
 int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream);
 

@@ -161,6 +161,8 @@ def _pgemm(**kw):
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(flags=capi.NORM_IN), -3, "flags"),
     (dict(n=200), -1, "multiple of 128"),
+    (dict(n=384, tile_cols=256), -1, "multiple of 256"),
+    (dict(tile_cols=64), -1, "tile_cols"),
     (dict(k=96), -1, "multiple of 128, k of 64"),
     (dict(tiles=24), -1, "tiles"),
     (dict(rows=513), -1, "tiles"),
