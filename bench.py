@@ -31,7 +31,10 @@ Printed JSON fields beyond the driver contract:
                 random substitutions, 512 new tokens, n-gram drafter (n=3,
                 backoff 2, up to 8 drafts); plain and speculative generate()
                 timed from the first emitted token to the last, tokens
-                compared for identity (skip with --no-spec).
+                compared for identity (skip with --no-spec).  Its "ceiling"
+                runs the same verify / accept loop with drafts taken from the
+                plain run's own output (every draft right): an upper bound of
+                the speculative path, not a drafter result.
 """
 
 import argparse
@@ -158,10 +161,12 @@ def spec_bench(eng, vocab, batch=4, prompt_len=1024, new_tokens=512, seed=5):
             f"{dt * 1e3:.1f} ms for {new_tokens - 1} decode steps")
     stats = dict(eng.stats.get("spec", {}))
     n_draft = eng.shape.spec_k if eng.shape is not None else None
-    eng.speculate = False
-    torch.cuda.empty_cache()
     n_tok = batch * (new_tokens - 1)
     plain_tps, spec_tps = n_tok / res[False][1], n_tok / res[True][1]
+    ceiling = spec_ceiling(eng, prompts, res[False][0], new_tokens, plain_tps)
+    log(f"speculation ceiling (drafts = the plain run's tokens): {ceiling}")
+    eng.speculate = False
+    torch.cuda.empty_cache()
     return {"workload": f"qwen3-4b bf16 bs{batch} motif prompt{prompt_len} new{new_tokens}, drafter n=3/2 k<=8",
             "plain_tok_s": round(plain_tps, 2), "spec_tok_s": round(spec_tps, 2),
             "speedup": round(spec_tps / plain_tps, 3),
@@ -172,7 +177,57 @@ def spec_bench(eng, vocab, batch=4, prompt_len=1024, new_tokens=512, seed=5):
             "plain_iterations": stats.get("plain_iterations"),
             "verify_cost_ratio": stats.get("cost_ratio"),
             "drafts_per_verify": n_draft,
-            "token_identical": res[False][0] == res[True][0]}
+            "token_identical": res[False][0] == res[True][0],
+            "ceiling": ceiling}
+
+
+def spec_ceiling(eng, prompts, plain_steps, new_tokens, plain_tps):
+    """The speculative loop with every draft right: the drafts of an
+    iteration are the plain run's next tokens after the sequence's current
+    length, written on the device (gather by ``lens``) in place of the n-gram
+    drafter; verify, accept, rollback and the host loop are unchanged.
+    Tokens must still equal the plain run's."""
+    import torch
+    from engine import SPEC_BACKOFF, SPEC_PRIMARY
+    from qdec.spec import SpecDecoder
+    eng.speculate = True
+    B, S = len(prompts), len(prompts[0])
+    sh = eng._shape_for(B, S, new_tokens)
+    k = sh.spec_k
+    dev = eng.device
+    # future[b, i] = plain token i of sequence b, padded so every gather is in range
+    plain = torch.tensor(plain_steps, dtype=torch.int64).T.contiguous()  # [B, N]
+    future = torch.cat([plain, plain[:, -1:].expand(B, k + 1)], 1).to(dev)
+    offs = torch.arange(1, k + 1, device=dev)[None, :]
+
+    class Forced(SpecDecoder):
+        def _draft(self, kk):
+            st = self.state
+            L = st.lens[:B].long()
+            cur = self.hist.gather(1, L[:, None])
+            if kk == 0:
+                st.ids[:B].copy_(cur[:, 0])
+                return
+            d = future.gather(1, (L - S)[:, None] + offs[:, :kk])
+            self.draft[:B * kk].view(B, kk).copy_(d)
+            st.ids[:B * (kk + 1)].view(B, kk + 1).copy_(torch.cat([cur, d], 1))
+
+    dec = Forced(eng, sh.state, SPEC_PRIMARY, SPEC_BACKOFF, k)
+    prompt_t = torch.tensor(prompts, dtype=torch.int64)
+    for _ in range(2):  # the first call captures the graphs
+        toks, t_first = [], None
+        for i, step in enumerate(dec.generate(prompt_t, new_tokens, gate=False)):
+            if i == 0:
+                t_first = time.perf_counter()
+            toks.append(step)
+        dt = time.perf_counter() - t_first
+    stats = dec.last_stats
+    tps = B * (new_tokens - 1) / dt
+    eng.shape = None
+    return {"spec_tok_s": round(tps, 2), "speedup": round(tps / plain_tps, 3),
+            "tokens_per_verify": round(stats.get("tokens_per_verify", float("nan")), 3),
+            "verify_cost_ratio": stats.get("cost_ratio"), "drafts_per_verify": k,
+            "token_identical": toks == plain_steps}
 
 
 def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):

@@ -66,15 +66,22 @@ class SpecDecoder:
         self.cost_ratio = None  # time of a verify iteration / a k = 0 iteration
         self.last_stats = {}
 
+    def _draft(self, k):
+        """Write the verify rows ``ids[b*(k+1) ..]`` = [current token, k
+        drafts] and ``draft`` (the n-gram drafter kernel)."""
+        st = self.state
+        s = torch.cuda.current_stream(st.model.device).cuda_stream
+        d = capi.DraftArgs()
+        d.hist, d.lens, d.ids, d.draft = (self.hist.data_ptr(), st.lens.data_ptr(), st.ids.data_ptr(),
+                                          self.draft.data_ptr())
+        d.batch, d.cap, d.primary, d.backoff, d.k = st.batch, st.cap, self.primary, self.backoff, k
+        self.lib.ngram_draft(d, s)
+
     def _iteration(self, k, stop_len):
         st, lib = self.state, self.lib
         s = torch.cuda.current_stream(st.model.device).cuda_stream
         B = st.batch
-        d = capi.DraftArgs()
-        d.hist, d.lens, d.ids, d.draft = (self.hist.data_ptr(), st.lens.data_ptr(), st.ids.data_ptr(),
-                                          self.draft.data_ptr())
-        d.batch, d.cap, d.primary, d.backoff, d.k = B, st.cap, self.primary, self.backoff, k
-        lib.ngram_draft(d, s)
+        self._draft(k)
         st.step(t_rows=k + 1, lm_head=True, ids_out=st.out_tok, advance=False)
         a = capi.AcceptArgs()
         a.out_tok, a.draft, a.hist, a.lens, a.naccept = (st.out_tok.data_ptr(), self.draft.data_ptr(),
