@@ -359,12 +359,31 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
   const uint32_t f = a->flags;
   if (f != 0u && f != QDEC_RES_OUT && f != QDEC_GLU)
     return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_gemm: flags 0x%x not supported (0, RES_OUT or GLU)", f);
-  if (a->tile_cols != 0 && a->tile_cols != 128 && a->tile_cols != 256)
-    return set_error(QDEC_EINVAL, "qdec_prefill_gemm: tile_cols %d must be 0, 128 or 256", a->tile_cols);
-  const int min_cols = a->tile_cols ? a->tile_cols : 128;
-  if (a->rows < 1 || a->k < kPgStageK || a->k % kPgStageK || a->n < min_cols || a->n % min_cols)
+  // Workgroup tile (activation rows x weight rows): 256 x 256 reads a third
+  // fewer LDS bytes per MFMA than 256 x 128 but makes half the workgroups;
+  // 64 x 64 makes 8x the workgroups of 256 x 128 for few rows.  Picked by
+  // the launch size: 256 x 256 from 768 workgroups (three per CU; at 16K
+  // rows QKV +10%, gate/up +7%), 256 x 128 from 512, else 64 x 64 (a
+  // 512-token prompt: O and down would have 40 workgroups of 256 x 128).
+  int trows = a->tile_rows, tcols = a->tile_cols;
+  const bool pair_ok = (trows == 0 && tcols == 0) || (trows == 256 && (tcols == 128 || tcols == 256)) ||
+                       (trows == 64 && tcols == 64);
+  if (!pair_ok)
+    return set_error(QDEC_EINVAL, "qdec_prefill_gemm: tile %d x %d (0 x 0, 256 x 128, 256 x 256 or 64 x 64)",
+                     trows, tcols);
+  if (trows == 0) {
+    const int64_t row_tiles = a->tiles / 16;
+    if (a->n % 256 == 0 && (a->n / 256) * row_tiles >= 768) {
+      trows = 256, tcols = 256;
+    } else if (a->n % 128 == 0 && (a->n / 128) * row_tiles >= 512) {
+      trows = 256, tcols = 128;
+    } else {
+      trows = 64, tcols = 64;
+    }
+  }
+  if (a->rows < 1 || a->k < kPgStageK || a->k % kPgStageK || a->n < tcols || a->n % tcols)
     return set_error(QDEC_EINVAL, "qdec_prefill_gemm: rows %d n %d k %d (n a multiple of %d, k of %d)", a->rows,
-                     a->n, a->k, min_cols, kPgStageK);
+                     a->n, a->k, tcols, kPgStageK);
   if (a->tiles < 1 || a->tiles % (kPgRows / 16) || a->rows > a->tiles * 16)
     return set_error(QDEC_EINVAL, "qdec_prefill_gemm: tiles %d must be a multiple of %d covering %d rows", a->tiles,
                      kPgRows / 16, a->rows);
@@ -386,13 +405,9 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
   const bool glu = (f & QDEC_GLU) != 0;
   p.n_out = glu ? a->n / 2 : a->n;
   p.up_tiles = a->n / 32;
-  // 256-column tiles read a third fewer LDS bytes per MFMA but halve the
-  // workgroup count: they pay once the launch keeps 768 workgroups (three
-  // per CU; at 16K rows QKV +10%, gate/up +7%; O and down, 640 workgroups,
-  // stay on 128).
-  p.tile_cols = a->tile_cols;
-  if (p.tile_cols == 0) p.tile_cols = (a->n % 256 == 0 && (a->n / 256) * (a->tiles / 16) >= 768) ? 256 : 128;
-  p.wg_n = glu ? (a->n / 2) / (p.tile_cols / 2) : a->n / p.tile_cols;
+  p.tile_rows = trows;
+  p.tile_cols = tcols;
+  p.wg_n = glu ? (a->n / 2) / (tcols / 2) : a->n / tcols;
   return launch_status(launch_pgemm(p, f, (hipStream_t)stream), "qdec_prefill_gemm");
 }
 

@@ -13,29 +13,31 @@ namespace qdec {
 namespace {
 
 // ------------------------------------------------------------------ product
-// A workgroup of 4 wavefronts computes a kPgRows x (32 WN) tile of the
+// A workgroup of 4 wavefronts computes a (32 XW) x (32 WN) tile of the
 // transposed product D = W . x^T: a weight fragment (16 weight rows x 32 k)
 // is the A operand and an activation fragment (32 k x 16 rows) the B operand
 // of v_mfma_f32_16x16x32_bf16, and both are one contiguous KiB in their
-// layouts.  Waves 2 x 2: wave (wn, wm) owns WN weight x 8 activation
-// fragments (WN = 4: 32 accumulators, WN = 8: 64).  Every fragment moves
-// from global memory straight into LDS (global_load_lds_dwordx4: one
-// instruction per 1 KiB fragment, no registers) through a ring of stage
-// buffers, RING - 1 stages in flight while one computes:
-//   WN = 4: stages of two k steps (48 KiB), RING 3;
-//   WN = 8: stages of one k step (32 KiB), RING 4.
-// The wider tile reads a third fewer LDS bytes per MFMA; the narrower one
-// makes twice as many workgroups (better for few row tiles).
-template <int WN>
+// layouts.  Waves 2 x 2: wave (wn, wm) owns WN weight x XW activation
+// fragments.  Every fragment moves from global memory straight into LDS
+// (global_load_lds_dwordx4: one instruction per 1 KiB fragment, no
+// registers) through a ring of stage buffers, RING - 1 stages in flight
+// while one computes:
+//   256 x 128 (WN 4, XW 8): stages of two k steps (48 KiB), RING 3;
+//   256 x 256 (WN 8, XW 8): stages of one k step (32 KiB), RING 4 -- a
+//     third fewer LDS bytes per MFMA, half the workgroups;
+//   64 x 64 (WN 2, XW 2): stages of two k steps (16 KiB), RING 3 -- for
+//     few rows: 8x the workgroups of 256 x 128, several per CU.
+template <int WN, int XW>
 struct PgShape {
   static constexpr int Wf = 2 * WN;                 // weight fragments per k step
-  static constexpr int Xf = kPgRows / 16;           // activation fragments per k step
-  static constexpr int KS = WN == 4 ? 2 : 1;        // k steps per stage
-  static constexpr int RING = WN == 4 ? 3 : 4;      // stage buffers
+  static constexpr int Xf = 2 * XW;                 // activation fragments per k step
+  static constexpr int KS = WN == 8 ? 1 : 2;        // k steps per stage
+  static constexpr int RING = WN == 8 ? 4 : 3;      // stage buffers
   static constexpr int Frags = Wf + Xf;             // fragments per k step
   static constexpr int Stage = KS * Frags;          // fragments per stage
   static constexpr int Loads = Stage / 4;           // loads per wave per stage
   static constexpr int WQ = Wf / 4;                 // weight loads per wave per k step
+  static_assert(Wf % 4 == 0 && Xf % 4 == 0, "each wave loads whole fragments");
 };
 constexpr int kPgGroupN = 4;  // column tiles walked together (x reuse in L2)
 
@@ -74,9 +76,9 @@ __device__ __forceinline__ float max_xor16_32(float v) {
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int kVmcnt0 = vmcnt_enc(0);
 
-template <uint32_t FLAGS, int WN>
+template <uint32_t FLAGS, int WN, int XW>
 __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
-  using S = PgShape<WN>;
+  using S = PgShape<WN, XW>;
   constexpr bool GLU = (FLAGS & QDEC_GLU) != 0;
   constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
   __shared__ uint4 lds[S::RING * S::Stage * 64];  // [ring slot][k step][fragment][lane]
@@ -133,11 +135,11 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
       return wn * WN + i;
   };
 
-  f32x4_t acc[WN][8];
+  f32x4_t acc[WN][XW];
 #pragma unroll
   for (int i = 0; i < WN; ++i)
 #pragma unroll
-    for (int q = 0; q < 8; ++q) acc[i][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < XW; ++q) acc[i][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   const int nst = p.k / (32 * S::KS);
 #pragma unroll
@@ -161,15 +163,15 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
 #pragma unroll
     for (int j = 0; j < S::KS; ++j) {
       const uint4 *L = lds + (size_t)(slot * S::KS + j) * S::Frags * 64 + lane;
-      uint4 a[WN], bx[8];
+      uint4 a[WN], bx[XW];
 #pragma unroll
       for (int i = 0; i < WN; ++i) a[i] = L[wf(i) * 64];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) bx[q] = L[(S::Wf + wm * 8 + q) * 64];
+      for (int q = 0; q < XW; ++q) bx[q] = L[(S::Wf + wm * XW + q) * 64];
 #pragma unroll
       for (int i = 0; i < WN; ++i)
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[i][q] = mfma16x16x32(a[i], bx[q], acc[i][q]);
+        for (int q = 0; q < XW; ++q) acc[i][q] = mfma16x16x32(a[i], bx[q], acc[i][q]);
     }
     slot = slot == S::RING - 1 ? 0 : slot + 1;
   }
@@ -179,9 +181,9 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
     uint16_t *dst = p.ofrag ? p.out + frag_off(m, n0, p.tiles) : p.out + (size_t)m * p.n_out + n0;
     *reinterpret_cast<uint2 *>(dst) = o;
   };
-  const int m_base = (tm * S::Xf + wm * 8) * 16 + col;
+  const int m_base = (tm * S::Xf + wm * XW) * 16 + col;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
+  for (int q = 0; q < XW; ++q) {
     const int m = m_base + q * 16;
     if (m >= p.rows) continue;
     if constexpr (GLU) {
@@ -468,20 +470,21 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
 
 }  // namespace
 
-template <int WN>
-hipError_t launch_pgemm_wn(const PgemmParams &p, uint32_t flags, hipStream_t s) {
-  const dim3 grid(p.wg_n * (p.tiles / PgShape<WN>::Xf)), block(256);
+template <int WN, int XW>
+hipError_t launch_pgemm_tile(const PgemmParams &p, uint32_t flags, hipStream_t s) {
+  const dim3 grid(p.wg_n * (p.tiles / PgShape<WN, XW>::Xf)), block(256);
   switch (flags) {
-    case 0u: hipLaunchKernelGGL((pgemm_kernel<0u, WN>), grid, block, 0, s, p); break;
-    case QDEC_RES_OUT: hipLaunchKernelGGL((pgemm_kernel<QDEC_RES_OUT, WN>), grid, block, 0, s, p); break;
-    case QDEC_GLU: hipLaunchKernelGGL((pgemm_kernel<QDEC_GLU, WN>), grid, block, 0, s, p); break;
+    case 0u: hipLaunchKernelGGL((pgemm_kernel<0u, WN, XW>), grid, block, 0, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL((pgemm_kernel<QDEC_RES_OUT, WN, XW>), grid, block, 0, s, p); break;
+    case QDEC_GLU: hipLaunchKernelGGL((pgemm_kernel<QDEC_GLU, WN, XW>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;
 }
 
 hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s) {
-  return p.tile_cols == 256 ? launch_pgemm_wn<8>(p, flags, s) : launch_pgemm_wn<4>(p, flags, s);
+  if (p.tile_rows == 64) return launch_pgemm_tile<2, 2>(p, flags, s);
+  return p.tile_cols == 256 ? launch_pgemm_tile<8, 8>(p, flags, s) : launch_pgemm_tile<4, 8>(p, flags, s);
 }
 
 hipError_t launch_prefill_qk(const PqkParams &p, hipStream_t s) {

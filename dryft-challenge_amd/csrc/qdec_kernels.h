@@ -90,8 +90,9 @@ constexpr int kAttnLds = 16 * 136 * 2 + 3 * 128 * 8 * 2 + 4 * 8 * 64 * 16 + 2 * 
 
 
 // ---- prefill (prefill.hip)
-// Product tile of a workgroup: kPgRows activation rows x 128 or 256 weight
-// rows; k a multiple of kPgStageK.
+// Product tiles of a workgroup (activation rows x weight rows): 256 x 128,
+// 256 x 256 or 64 x 64; k a multiple of kPgStageK; the activation buffers
+// hold whole kPgRows row tiles.
 constexpr int kPgRows = 256;
 constexpr int kPgStageK = 64;
 struct PgemmParams {
@@ -104,7 +105,8 @@ struct PgemmParams {
   int ofrag;     // out in fragment order
   int n_out;     // columns of out (n, or n/2 with GLU)
   int up_tiles;  // GLU: tile offset of the up half (n/32)
-  int tile_cols; // weight rows per workgroup tile: 128 or 256
+  int tile_rows; // activation rows per workgroup tile: 256 or 64
+  int tile_cols; // weight rows per workgroup tile: 128 or 256 (64 with 64 rows)
   int wg_n;      // workgroup tiles along n
 };
 hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s);

@@ -64,7 +64,8 @@ class RownormArgs(ctypes.Structure):
 
 class PgemmArgs(ctypes.Structure):
     _fields_ = [("x", P), ("w", P), ("out", P), ("res", P), ("flags", ctypes.c_uint32), ("rows", I32),
-                ("n", I32), ("k", I32), ("tiles", I32), ("out_frag", I32), ("tile_cols", I32)]
+                ("n", I32), ("k", I32), ("tiles", I32), ("out_frag", I32), ("tile_rows", I32),
+                ("tile_cols", I32)]
 
 
 class PrefillQkArgs(ctypes.Structure):

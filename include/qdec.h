@@ -285,10 +285,10 @@ typedef struct {
 int qdec_rownorm(const qdec_rownorm_args *a, qdec_stream_t stream);
 
 /* out = x @ W^T on the matrix cores for x in fragment order (`tiles` M
- * tiles, a multiple of 16), W tiled [n, k].  A workgroup computes 256 rows x
- * tile_cols weight rows (128 or 256; 0 picks 256 when n allows it and the
- * launch still has at least 768 workgroups); n must be a multiple of the
- * tile, k of 64.  flags:
+ * tiles, a multiple of 16), W tiled [n, k].  A workgroup computes tile_rows
+ * x tile_cols of it: 256 x 128, 256 x 256 or 64 x 64 (0 x 0 picks by launch
+ * size: 256 x 256 while it keeps 768 workgroups, 256 x 128 while 512, else
+ * 64 x 64); n must be a multiple of tile_cols, k of 64.  flags:
  *   0            out = bf16(x @ W^T): [rows, n] row-major, or fragment order
  *                with out_frag;
  *   QDEC_RES_OUT out = bf16(res + bf16(x @ W^T)), row-major; res may be out;
@@ -309,7 +309,8 @@ typedef struct {
   int32_t k;
   int32_t tiles;
   int32_t out_frag; /* 1: out in fragment order with `tiles` M tiles */
-  int32_t tile_cols; /* 0, 128 or 256 */
+  int32_t tile_rows; /* 0, 256 or 64 */
+  int32_t tile_cols; /* 0, 128 or 256 (with 256 rows), 64 (with 64 rows) */
 } qdec_pgemm_args;
 int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream);
 

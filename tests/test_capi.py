@@ -160,10 +160,12 @@ def _pgemm(**kw):
 
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(flags=capi.NORM_IN), -3, "flags"),
-    (dict(n=200), -1, "multiple of 128"),
-    (dict(n=384, tile_cols=256), -1, "multiple of 256"),
-    (dict(tile_cols=64), -1, "tile_cols"),
-    (dict(k=96), -1, "multiple of 128, k of 64"),
+    (dict(n=200), -1, "multiple of 64"),
+    (dict(n=384, tile_rows=256, tile_cols=256), -1, "multiple of 256"),
+    (dict(n=320, tile_rows=256, tile_cols=128), -1, "multiple of 128"),
+    (dict(tile_rows=256, tile_cols=64), -1, "tile 256 x 64"),
+    (dict(tile_cols=128), -1, "tile 0 x 128"),
+    (dict(k=96), -1, "k of 64"),
     (dict(tiles=24), -1, "tiles"),
     (dict(rows=513), -1, "tiles"),
     (dict(flags=capi.RES_OUT), -3, "RES_OUT"),

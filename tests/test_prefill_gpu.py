@@ -84,7 +84,7 @@ def to_frag(lib, x, tiles, norm_w=None, eps=1e-6):
     return out
 
 
-def pgemm(lib, xf, wp, rows, n, k, tiles, flags=0, res=None, out_frag=0, tile_cols=0):
+def pgemm(lib, xf, wp, rows, n, k, tiles, flags=0, res=None, out_frag=0, tile=(0, 0)):
     from qdec import capi
     n_out = n // 2 if flags == capi.GLU else n
     out = torch.full((tiles * 16 if out_frag else rows, n_out), float("nan"), dtype=torch.bfloat16, device=DEV)
@@ -93,7 +93,8 @@ def pgemm(lib, xf, wp, rows, n, k, tiles, flags=0, res=None, out_frag=0, tile_co
     a = capi.PgemmArgs()
     a.x, a.w, a.out = xf.data_ptr(), wp.data_ptr(), out.data_ptr()
     a.res = out.data_ptr() if flags == capi.RES_OUT else None
-    a.flags, a.rows, a.n, a.k, a.tiles, a.out_frag, a.tile_cols = flags, rows, n, k, tiles, out_frag, tile_cols
+    a.flags, a.rows, a.n, a.k, a.tiles, a.out_frag = flags, rows, n, k, tiles, out_frag
+    a.tile_rows, a.tile_cols = tile
     lib.prefill_gemm(a, stream())
     torch.cuda.synchronize()
     return out.cpu()
@@ -115,18 +116,21 @@ def test_rownorm_layout_and_norm(lib):
     assert exact >= 0.99
 
 
-@pytest.mark.parametrize("tile_cols", [128, 256])
+TILES = [(256, 128), (256, 256), (64, 64)]
+
+
+@pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("rows,n,k", [(1, 256, 64), (37, 256, 128), (256, 384, 192), (300, 512, 512),
-                                      (700, 128, 256)])
-def test_prefill_gemm_exact_small_ints(lib, rows, n, k, tile_cols):
+                                      (700, 128, 256), (90, 192, 320)])
+def test_prefill_gemm_exact_small_ints(lib, rows, n, k, tile):
     from qdec import capi
-    if n % tile_cols:
+    if n % tile[1]:
         pytest.skip("n is not a multiple of the tile")
     x, w = small_ints(rows, k, seed=rows), small_ints(n, k, seed=n + k)
     tiles = round_up(rows, ROW_TILE) // 16
     xf, wp = to_frag(lib, x, tiles), pack(lib, w)
     ref = x.float() @ w.float().T  # exact integers
-    kw = dict(tile_cols=tile_cols)
+    kw = dict(tile=tile)
     assert torch.equal(pgemm(lib, xf, wp, rows, n, k, tiles, **kw).float(), ref)
     res = small_ints(rows, n, lo=-8, hi=8, seed=3)
     assert torch.equal(pgemm(lib, xf, wp, rows, n, k, tiles, capi.RES_OUT, res=res, **kw).float(), res.float() + ref)
@@ -134,9 +138,9 @@ def test_prefill_gemm_exact_small_ints(lib, rows, n, k, tile_cols):
     assert torch.equal(frag_to_rows(fr, rows, n, tiles).float(), ref)
 
 
-@pytest.mark.parametrize("tile_cols", [128, 256])
+@pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("rows,n,k", [(5, 256, 128), (300, 512, 2560), (512, 1024, 640)])
-def test_prefill_gemm_glu(lib, rows, n, k, tile_cols):
+def test_prefill_gemm_glu(lib, rows, n, k, tile):
     from qdec import capi
     x, w = rnd(rows, k, seed=4), rnd(n, k, scale=0.05, seed=5)
     tiles = round_up(rows, ROW_TILE) // 16
@@ -145,7 +149,7 @@ def test_prefill_gemm_glu(lib, rows, n, k, tile_cols):
     g, u = bf16(acc[:, : n // 2]), bf16(acc[:, n // 2:])
     ref = silu_mul(g, u)
     for out_frag in (0, 1):
-        out = pgemm(lib, xf, wp, rows, n, k, tiles, capi.GLU, out_frag=out_frag, tile_cols=tile_cols)
+        out = pgemm(lib, xf, wp, rows, n, k, tiles, capi.GLU, out_frag=out_frag, tile=tile)
         got = frag_to_rows(out, rows, n // 2, tiles) if out_frag else out
         got = got.float()
         assert torch.isfinite(got).all()
