@@ -141,39 +141,114 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
 #pragma unroll
     for (int q = 0; q < XW; ++q) acc[i][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int nst = p.k / (32 * S::KS);
-#pragma unroll
-  for (int s = 0; s < S::RING - 1; ++s)
-    if (s < nst) dma(s, s);
-  int slot = 0;
-  for (int s = 0; s < nst; ++s) {
-    // this wave's loads of stage s are done once at most the younger
-    // stages' are outstanding; the barrier makes every wave's visible and
-    // frees the slot of stage s-1 for stage s + RING - 1
-    const int younger = min(S::RING - 2, nst - 1 - s);
-    if (younger >= 2)
-      __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * S::Loads));
-    else if (younger == 1)
-      __builtin_amdgcn_s_waitcnt(vmcnt_enc(S::Loads));
-    else
-      __builtin_amdgcn_s_waitcnt(kVmcnt0);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (s + S::RING - 1 < nst) dma(s + S::RING - 1, slot == 0 ? S::RING - 1 : slot - 1);
-#pragma unroll
-    for (int j = 0; j < S::KS; ++j) {
-      const uint4 *L = lds + (size_t)(slot * S::KS + j) * S::Frags * 64 + lane;
-      uint4 a[WN], bx[XW];
-#pragma unroll
+  if constexpr (WN == 8) {
+    // 256 x 256 tiles (one k step per stage): the next step's fragments are
+    // read while this step multiplies (+5-10% there; the other tiles, two
+    // steps per stage, measured slower with it and read each step's
+    // fragments right before its MFMAs).
+    // k steps run through two register sets of fragments: the fragments of
+    // step t+1 are read from LDS while step t's MFMAs run.  Entering a new
+    // stage (before reading its first step) waits for this wave's loads of
+    // it, then a barrier makes every wave's visible and frees the slot of the
+    // stage before it -- all of whose steps are already in registers -- for
+    // the stage RING - 1 ahead.
+    const int nst = p.k / (32 * S::KS);
+    const int nsteps = nst * S::KS;
+    auto slot_of = [&](int st) { return st % S::RING; };
+    auto enter_stage = [&](int st) {
+      const int younger = min(S::RING - 2, nst - 1 - st);
+      if (younger >= 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * S::Loads));
+      else if (younger == 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(S::Loads));
+      else
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (st + S::RING - 1 < nst) dma(st + S::RING - 1, slot_of(st + S::RING - 1));
+    };
+    auto read_frags = [&](int t, uint4 (&a)[WN], uint4 (&bx)[XW]) {
+      const uint4 *L = lds + (size_t)(slot_of(t / S::KS) * S::KS + t % S::KS) * S::Frags * 64 + lane;
+  #pragma unroll
       for (int i = 0; i < WN; ++i) a[i] = L[wf(i) * 64];
-#pragma unroll
+  #pragma unroll
       for (int q = 0; q < XW; ++q) bx[q] = L[(S::Wf + wm * XW + q) * 64];
-#pragma unroll
+    };
+    auto mma = [&](const uint4 (&a)[WN], const uint4 (&bx)[XW]) {
+  #pragma unroll
       for (int i = 0; i < WN; ++i)
-#pragma unroll
+  #pragma unroll
         for (int q = 0; q < XW; ++q) acc[i][q] = mfma16x16x32(a[i], bx[q], acc[i][q]);
+    };
+    // One step: prepare step t+1 into (na, nb), multiply step t from (ca, cb).
+    auto step = [&](int t, const uint4 (&ca)[WN], const uint4 (&cb)[XW], uint4 (&na)[WN], uint4 (&nb)[XW]) {
+      const int tn = t + 1;
+      if (tn < nsteps) {
+        if (tn % S::KS == 0) enter_stage(tn / S::KS);
+        read_frags(tn, na, nb);
+      }
+      mma(ca, cb);
+    };
+
+  #pragma unroll
+    for (int st = 0; st < S::RING - 1; ++st)
+      if (st < nst) dma(st, st);
+    uint4 a0[WN], b0[XW], a1[WN], b1[XW];
+    // stage 0 (younger stages in flight as inside the loop)
+    {
+      const int younger = min(S::RING - 2, nst - 1);
+      if (younger >= 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * S::Loads));
+      else if (younger == 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(S::Loads));
+      else
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (S::RING - 1 < nst) dma(S::RING - 1, S::RING - 1);
     }
-    slot = slot == S::RING - 1 ? 0 : slot + 1;
+    read_frags(0, a0, b0);
+    int t = 0;
+    for (; t + 1 < nsteps; t += 2) {
+      step(t, a0, b0, a1, b1);
+      step(t + 1, a1, b1, a0, b0);
+    }
+    if (t < nsteps) mma(a0, b0);
+  } else {
+    const int nst = p.k / (32 * S::KS);
+  #pragma unroll
+    for (int s = 0; s < S::RING - 1; ++s)
+      if (s < nst) dma(s, s);
+    int slot = 0;
+    for (int s = 0; s < nst; ++s) {
+      // this wave's loads of stage s are done once at most the younger
+      // stages' are outstanding; the barrier makes every wave's visible and
+      // frees the slot of stage s-1 for stage s + RING - 1
+      const int younger = min(S::RING - 2, nst - 1 - s);
+      if (younger >= 2)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(2 * S::Loads));
+      else if (younger == 1)
+        __builtin_amdgcn_s_waitcnt(vmcnt_enc(S::Loads));
+      else
+        __builtin_amdgcn_s_waitcnt(kVmcnt0);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (s + S::RING - 1 < nst) dma(s + S::RING - 1, slot == 0 ? S::RING - 1 : slot - 1);
+  #pragma unroll
+      for (int j = 0; j < S::KS; ++j) {
+        const uint4 *L = lds + (size_t)(slot * S::KS + j) * S::Frags * 64 + lane;
+        uint4 a[WN], bx[XW];
+  #pragma unroll
+        for (int i = 0; i < WN; ++i) a[i] = L[wf(i) * 64];
+  #pragma unroll
+        for (int q = 0; q < XW; ++q) bx[q] = L[(S::Wf + wm * XW + q) * 64];
+  #pragma unroll
+        for (int i = 0; i < WN; ++i)
+  #pragma unroll
+          for (int q = 0; q < XW; ++q) acc[i][q] = mfma16x16x32(a[i], bx[q], acc[i][q]);
+      }
+      slot = slot == S::RING - 1 ? 0 : slot + 1;
+    }
   }
 
   // Epilogue: lane holds columns n0 .. n0+3 of row m for every fragment pair.
