@@ -349,9 +349,11 @@ int qdec_rownorm(const qdec_rownorm_args *a, qdec_stream_t stream) {
     return set_error(QDEC_EINVAL, "qdec_rownorm: rows %d k %d tiles %d", a->rows, a->k, a->tiles);
   if (!aligned16(a->x) || !aligned16(a->out) || (a->norm_w && !aligned16(a->norm_w)))
     return set_error(QDEC_EALIGN, "qdec_rownorm: pointers must be 16-byte aligned");
-  return launch_status(launch_rownorm_rows(a->x, a->norm_w, a->out, a->eps, a->rows, a->k, a->tiles,
-                                           (hipStream_t)stream),
-                       "qdec_rownorm");
+  const hipError_t e = pnorm_fits(a->k, a->rows)
+                          ? launch_pnorm(a->x, a->norm_w, a->out, a->eps, a->rows, a->k, a->tiles, (hipStream_t)stream)
+                          : launch_rownorm_rows(a->x, a->norm_w, a->out, a->eps, a->rows, a->k, a->tiles,
+                                                (hipStream_t)stream);
+  return launch_status(e, "qdec_rownorm");
 }
 
 int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {

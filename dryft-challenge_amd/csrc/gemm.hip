@@ -82,16 +82,6 @@ __device__ __forceinline__ void block_row_sums(float (&ss)[8], float *s_red, int
   __syncthreads();
 }
 
-// x' = norm_w * bf16(x * rstd) of 8 consecutive elements (one 16-byte vector).
-__device__ __forceinline__ uint4 norm8(const uint4 &xv, const uint4 &nv, float rs) {
-  float f[8], g[8];
-  unpack8(xv, f);
-  unpack8(nv, g);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) f[e] = g[e] * rbf(f[e] * rs);
-  return pack8(f);
-}
-
 // Activation vector (8 consecutive elements from k index kk) of row m,
 // merged from the attention chunk partials the previous launch left with
 // out_partials (attn_dev.h: per (sequence, kv head, chunk) acc [R][128],

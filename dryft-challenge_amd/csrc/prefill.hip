@@ -293,10 +293,9 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
 }
 
 // ------------------------------------------------------- head norm + RoPE
-// One workgroup per row: wave w normalises and rotates heads w, w+4, ...
-// (queries back into qkv, keys into the K cache); then the raw values go to
-// the channel-major V cache.
-__global__ void __launch_bounds__(256) pqk_kernel(const PqkParams p) {
+// Few rows: one workgroup per row, wave w normalising and rotating heads w,
+// w+4, ...; the values go to the V cache element by element.
+__global__ void __launch_bounds__(256) pqk_row_kernel(const PqkParams p) {
   constexpr int D = 128;
   const int m = blockIdx.x;
   const int b = m / p.t_rows, t = m - b * p.t_rows;
@@ -320,6 +319,121 @@ __global__ void __launch_bounds__(256) pqk_kernel(const PqkParams p) {
     const int kvh = i >> 7, ch = i & 127;
     p.v_cache[((size_t)b * p.nkv + kvh) * p.cap * D + ((size_t)(pos >> 3) * D + ch) * 8 + (pos & 7)] =
         row[(size_t)(p.nq + p.nkv + kvh) * D + ch];
+  }
+}
+
+// Many rows: a workgroup takes 8 consecutive positions of one sequence.  Wave w
+// normalises and rotates the 40 heads of rows 2w and 2w+1 (queries back into
+// qkv, keys into the K cache); then each thread moves the raw values of 4
+// (kv head, channel) pairs: 8 positions of one channel are one 16-byte
+// vector of the channel-major V cache when the group starts on a multiple of
+// 8 slots and is complete (element stores otherwise).
+constexpr int kPqRows = 8;
+
+__global__ void __launch_bounds__(256) pqk_kernel(const PqkParams p) {
+  constexpr int D = 128;
+  const int T = p.t_rows;
+  const int ngrp = (T + kPqRows - 1) / kPqRows;
+  const int b = blockIdx.x / ngrp, t0 = (blockIdx.x - b * ngrp) * kPqRows;
+  const int nrow = min(kPqRows, T - t0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int width = (p.nq + 2 * p.nkv) * D;
+  uint16_t *rows = p.qkv + (size_t)(b * T + t0) * width;
+  const uint32_t qw = *reinterpret_cast<const uint32_t *>(p.q_norm_w + 2 * lane);
+  const uint32_t kw = *reinterpret_cast<const uint32_t *>(p.k_norm_w + 2 * lane);
+#pragma unroll
+  for (int i = 0; i < kPqRows / 4; ++i) {
+    const int r = wave * (kPqRows / 4) + i;
+    if (r >= nrow) break;
+    const int pos = p.pos0 + t0 + r;
+    uint16_t *row = rows + (size_t)r * width;
+    const uint32_t cw = *reinterpret_cast<const uint32_t *>(p.cos_tab + (size_t)pos * D + 2 * lane);
+    const uint32_t sw = *reinterpret_cast<const uint32_t *>(p.sin_tab + (size_t)pos * D + 2 * lane);
+    for (int h = 0; h < p.nq + p.nkv; ++h) {
+      uint32_t *cell = reinterpret_cast<uint32_t *>(row + (size_t)h * D + 2 * lane);
+      const uint32_t o = head_norm_rope2(*cell, h < p.nq ? qw : kw, cw, sw, p.eps);
+      if (h < p.nq)
+        *cell = o;
+      else
+        *reinterpret_cast<uint32_t *>(p.k_cache + (((size_t)b * p.nkv + (h - p.nq)) * p.cap + pos) * D + 2 * lane) = o;
+    }
+  }
+  const int slot0 = p.pos0 + t0;
+  const bool whole = nrow == kPqRows && (slot0 & 7) == 0;
+  for (int i = threadIdx.x; i < p.nkv * D; i += blockDim.x) {
+    const int kvh = i >> 7, ch = i & 127;
+    const uint16_t *src = rows + (size_t)(p.nq + p.nkv + kvh) * D + ch;
+    uint16_t *vb = p.v_cache + ((size_t)b * p.nkv + kvh) * p.cap * D;
+    if (whole) {
+      uint16_t v[kPqRows];
+#pragma unroll
+      for (int r = 0; r < kPqRows; ++r) v[r] = src[(size_t)r * width];
+      uint4 o;
+      o.x = v[0] | ((uint32_t)v[1] << 16);
+      o.y = v[2] | ((uint32_t)v[3] << 16);
+      o.z = v[4] | ((uint32_t)v[5] << 16);
+      o.w = v[6] | ((uint32_t)v[7] << 16);
+      *reinterpret_cast<uint4 *>(vb + ((size_t)(slot0 >> 3) * D + ch) * 8) = o;
+    } else {
+      for (int r = 0; r < nrow; ++r) {
+        const int slot = slot0 + r;
+        vb[((size_t)(slot >> 3) * D + ch) * 8 + (slot & 7)] = src[(size_t)r * width];
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------ row norm
+// RMSNorm of 16 rows (one M tile) per workgroup into fragment order: thread
+// (row r, group g) holds k steps g, g+16, ... of row r in registers (read
+// once), the row's sum of squares is reduced over its 16 threads, and every
+// store is one lane's 16 bytes of a fragment -- the 16 threads of a group
+// write 256 contiguous bytes per vector.  Rows past `rows` are zeros.
+constexpr int kPnSteps = 8;  // k steps per thread: k up to 16 * 8 * 32 = 4096
+
+__global__ void __launch_bounds__(256) pnorm_kernel(const uint16_t *__restrict__ X, const uint16_t *__restrict__ norm_w,
+                                                    uint16_t *__restrict__ out, int k, float eps, int rows, int tiles) {
+  __shared__ float s_red[4][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = tid & 15, g = tid >> 4;
+  const int mt = blockIdx.x;
+  const int m = mt * 16 + r;
+  const int KS = k >> 5;
+  const bool real = m < rows;
+  const uint16_t *xrow = X + (size_t)(real ? m : 0) * k;
+  uint4 v[kPnSteps][4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPnSteps; ++i) {
+    const int ks = g + 16 * i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i][j] = (real && ks < KS) ? *reinterpret_cast<const uint4 *>(xrow + ks * 32 + j * 8) : zero4();
+      float f[8];
+      unpack8(v[i][j], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+    }
+  }
+  // the 16 threads of row r: lanes r + 16 * (g % 4) of wave g / 4
+  ss += shfl_xor(ss, 16);
+  ss += shfl_xor(ss, 32);
+  if (lane < 16) s_red[wave][lane] = ss;
+  __syncthreads();
+  const float tot = s_red[0][r] + s_red[1][r] + s_red[2][r] + s_red[3][r];
+  const float rs = 1.0f / sqrtf(tot / (float)k + eps);
+#pragma unroll
+  for (int i = 0; i < kPnSteps; ++i) {
+    const int ks = g + 16 * i;
+    if (ks >= KS) break;
+    uint16_t *blk = out + ((size_t)ks * tiles + mt) * 512;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint4 o = zero4();
+      if (real)
+        o = norm_w ? norm8(v[i][j], *reinterpret_cast<const uint4 *>(norm_w + ks * 32 + j * 8), rs) : v[i][j];
+      *reinterpret_cast<uint4 *>(blk + (r + 16 * j) * 8) = o;
+    }
   }
 }
 
@@ -562,8 +676,29 @@ hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s) {
   return p.tile_cols == 256 ? launch_pgemm_tile<8, 8>(p, flags, s) : launch_pgemm_tile<4, 8>(p, flags, s);
 }
 
+// Grouped row kernels from this many rows (below it one workgroup per row
+// or per 16-row tile leaves the GPU short of workgroups: a 512-token prompt
+// measured 10.0 ms with the per-row kernels and 11.8 with the grouped ones;
+// 32 x 1024-row chunks 5% faster with the grouped ones).
+constexpr int kGroupedRows = 4096;
+
 hipError_t launch_prefill_qk(const PqkParams &p, hipStream_t s) {
-  hipLaunchKernelGGL(pqk_kernel, dim3(p.batch * p.t_rows), dim3(256), 0, s, p);
+  if (p.batch * p.t_rows < kGroupedRows) {
+    hipLaunchKernelGGL(pqk_row_kernel, dim3(p.batch * p.t_rows), dim3(256), 0, s, p);
+    return hipSuccess;
+  }
+  const int ngrp = (p.t_rows + kPqRows - 1) / kPqRows;
+  hipLaunchKernelGGL(pqk_kernel, dim3(p.batch * ngrp), dim3(256), 0, s, p);
+  return hipSuccess;
+}
+
+bool pnorm_fits(int k, int rows) { return k <= 16 * kPnSteps * 32 && rows >= kGroupedRows; }
+
+hipError_t launch_pnorm(const void *x, const void *norm_w, void *out, float eps, int rows, int k, int tiles,
+                        hipStream_t s) {
+  hipLaunchKernelGGL(pnorm_kernel, dim3(tiles), dim3(256), 0, s, reinterpret_cast<const uint16_t *>(x),
+                     reinterpret_cast<const uint16_t *>(norm_w), reinterpret_cast<uint16_t *>(out), k, eps, rows,
+                     tiles);
   return hipSuccess;
 }
 

@@ -61,6 +61,17 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const uint4 &a, const uint4 &b, 
 
 __device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
 
+// x' = norm_w * bf16(x * rstd) of 8 consecutive elements (one 16-byte
+// vector), rounded to bf16 on packing.
+__device__ __forceinline__ uint4 norm8(const uint4 &xv, const uint4 &nv, float rs) {
+  float f[8], g[8];
+  unpack8(xv, f);
+  unpack8(nv, g);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = g[e] * rbf(f[e] * rs);
+  return pack8(f);
+}
+
 // Activations in MFMA fragment order: element (m, k) of a [rows, K] matrix
 // with nmt = ceil(rows / 16) M tiles lives in the 1 KiB block of (k step
 // k/32, M tile m/16), lane (m % 16) + 16 * ((k % 32) / 8), element k % 8 --

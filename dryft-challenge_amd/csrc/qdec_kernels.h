@@ -133,6 +133,11 @@ hipError_t launch_prefill_attn(const PattnParams &p, hipStream_t s);
 
 hipError_t launch_rownorm_rows(const void *x, const void *norm_w, void *out, float eps, int rows, int k,
                                int tiles, hipStream_t s);
+// One workgroup per 16-row tile (prefill.hip): for k up to 4096 and enough
+// rows to fill the GPU.
+bool pnorm_fits(int k, int rows);
+hipError_t launch_pnorm(const void *x, const void *norm_w, void *out, float eps, int rows, int k, int tiles,
+                        hipStream_t s);
 
 hipError_t launch_embed(const int64_t *ids, const void *emb, void *h, int rows, int hidden,
                         int vocab, hipStream_t s);

@@ -100,11 +100,12 @@ def pgemm(lib, xf, wp, rows, n, k, tiles, flags=0, res=None, out_frag=0, tile=(0
     return out.cpu()
 
 
-def test_rownorm_layout_and_norm(lib):
-    rows, k = 37, 2560
+@pytest.mark.parametrize("rows", [37, 5000])  # per-row kernel / 16-row tile kernel
+def test_rownorm_layout_and_norm(lib, rows):
+    k = 2560
     x = rnd(rows, k, scale=3, seed=1)
     w = bf16(1 + 0.1 * torch.randn(k, generator=torch.Generator().manual_seed(2))).to(torch.bfloat16)
-    tiles = 16
+    tiles = round_up(rows, ROW_TILE) // 16
     plain = to_frag(lib, x, tiles)
     full = frag_to_rows(plain, tiles * 16, k, tiles).cpu()
     assert torch.equal(full[:rows], x)
@@ -241,7 +242,10 @@ def prefill_oracle(c, B, T, pos0):
 
 
 @pytest.mark.parametrize("B,T,pos0,cap", [(1, 1, 0, 64), (1, 64, 0, 64), (2, 100, 0, 128), (2, 77, 37, 128),
-                                          (1, 300, 200, 512), (3, 129, 64, 224), (1, 33, 991, 1024)])
+                                          (1, 300, 200, 512), (3, 129, 64, 224), (1, 33, 991, 1024),
+                                          (33, 131, 21, 160), (32, 130, 0, 160)])
+# the last two take the grouped QK kernel (>= 4096 rows): unaligned groups, then
+# aligned ones with a ragged last group
 def test_prefill_qk_and_attention_vs_oracle(lib, B, T, pos0, cap):
     c = prefill_case(lib, B, T, pos0, cap, seed=B * 1000 + T + pos0)
     ref, q_ref, kc, vc = prefill_oracle(c, B, T, pos0)
