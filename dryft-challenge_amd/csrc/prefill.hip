@@ -461,22 +461,28 @@ __global__ void __launch_bounds__(256) pnorm_kernel(const uint16_t *__restrict__
 constexpr int kPaKFrags = 8, kPaVFrags = 8;
 constexpr int kPaBlockVec = (kPaKFrags + kPaVFrags) * 64;  // uint4 per staged block
 constexpr int kPaRing = 3;
-constexpr int kVmcnt4 = 4 | (7 << 4) | (15 << 8);
+constexpr int kPaWph = 2;  // waves per query head
 
-__global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
+template <int WPH>  // waves per query head: 1 (4 M tiles each) or 2 (2 M tiles each)
+__global__ void __launch_bounds__(256 * WPH, 1) pattn_kernel(const PattnParams p) {
   constexpr int D = 128;
+  constexpr int MT = 4 / WPH;                  // M tiles of 16 positions per wave
+  constexpr int NWV = 4 * WPH;                 // waves
+  constexpr int FPW = (kPaKFrags + kPaVFrags) / NWV;  // fragments each wave loads per block
   __shared__ uint4 lds[kPaRing * kPaBlockVec];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
+  const int head = wave & 3, half = wave >> 2;  // query head of the group, which 16*MT positions
   const int T = p.t_rows;
   const int nqb = (T + kPaRows - 1) / kPaRows;
   const int cells = p.batch * p.nkv;
   const int qb = nqb - 1 - (int)(blockIdx.x / cells);  // longest rows first
   const int cell = (int)(blockIdx.x % cells);
   const int b = cell / p.nkv, kvh = cell - b * p.nkv;
-  const int hq = kvh * 4 + wave;
+  const int hq = kvh * 4 + head;
   const int width = (p.nq + 2 * p.nkv) * D;
   const int t0 = qb * kPaRows;
+  const int tw = t0 + half * 16 * MT;  // this wave's first position
   const int tlast = min(T, t0 + kPaRows) - 1;
   const int last = p.pos0 + tlast;  // highest slot any row of the block sees
   const int nb = last / 32 + 1;
@@ -488,11 +494,11 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
   const bool rows_full = t0 + kPaRows - 1 <= tlast;  // all 64 rows are real
 
   // Queries as B operands: row col of M tile mt, channels 32s + 8*grp.
-  uint4 qf[4][4];
-  int qpos[4];
+  uint4 qf[MT][4];
+  int qpos[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int t = t0 + mt * 16 + col;
+  for (int mt = 0; mt < MT; ++mt) {
+    const int t = tw + mt * 16 + col;
     const bool valid = t <= tlast;
     qpos[mt] = valid ? p.pos0 + t : -1;
     const uint16_t *qrow = p.qkv + (size_t)(b * T + min(t, tlast)) * width + (size_t)hq * D + grp * 8;
@@ -500,8 +506,8 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
     for (int s = 0; s < 4; ++s) qf[mt][s] = valid ? ld16(qrow + s * 32) : zero4();
   }
 
-  // Block j into ring slot `slot`: this wave gathers K fragments wave and
-  // wave + 4 (index 2s + h) and V fragments wave and wave + 4.
+  // Block j into ring slot `slot`: this wave gathers K fragments wave + NWV*i
+  // (index 2s + h) and V fragments wave + NWV*i.
   const uint32_t lds0 = lds_addr(lds);
   const uint16_t *kg = kc + (size_t)(8 * (col >> 2) + (col & 3)) * D + 8 * grp;
   const uint16_t *vg = vc + (size_t)grp * D * 8 + col * 8;
@@ -509,21 +515,21 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
     const int s0 = j * 32;
     const uint32_t base = lds0 + (uint32_t)(slot * kPaBlockVec * 16);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int f = wave + 4 * i;
+    for (int i = 0; i < FPW / 2; ++i) {
+      const int f = wave + NWV * i;
       dma16(kg + (size_t)(s0 + 4 * (f & 1)) * D + 32 * (f >> 1), base + f * 1024);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int dt = wave + 4 * i;
+    for (int i = 0; i < FPW / 2; ++i) {
+      const int dt = wave + NWV * i;
       dma16(vg + (size_t)(s0 >> 3) * D * 8 + dt * 128, base + (kPaKFrags + dt) * 1024);
     }
   };
 
-  f32x4_t acc[4][8];
-  float m_run[4], l_run[4];
+  f32x4_t acc[MT][8];
+  float m_run[MT], l_run[MT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
+  for (int mt = 0; mt < MT; ++mt) {
     m_run[mt] = NEG_INF;
     l_run[mt] = 0.f;
 #pragma unroll
@@ -541,7 +547,7 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
     // are outstanding; the barrier makes every wave's visible and frees the
     // slot of block j-1 for block j+2
     if (j + 1 < nb)
-      __builtin_amdgcn_s_waitcnt(kVmcnt4);
+      __builtin_amdgcn_s_waitcnt(vmcnt_enc(FPW));
     else
       __builtin_amdgcn_s_waitcnt(kVmcnt0);
     __builtin_amdgcn_s_barrier();
@@ -598,7 +604,7 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
     // and leaves its rows unchanged (alpha 1, p 0).
     const bool masked = !(rows_full && s0 + 31 <= p.pos0 + t0);
 #pragma unroll
-    for (int m2 = 0; m2 < 4; m2 += 2) {
+    for (int m2 = 0; m2 < MT; m2 += 2) {
       f32x4_t sa[2], sbv[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) sa[u] = sbv[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -640,11 +646,11 @@ __global__ void __launch_bounds__(256, 1) pattn_kernel(const PattnParams p) {
   // Rows in fragment order for the O projection: lane holds channels
   // 16dt + 4*grp .. +3 of its row.
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    if (t0 + mt * 16 > tlast) continue;
+  for (int mt = 0; mt < MT; ++mt) {
+    if (tw + mt * 16 > tlast) continue;
     float l = l_run[mt] + shfl_xor(l_run[mt], 16);
     l += shfl_xor(l, 32);
-    const int t = t0 + mt * 16 + col;
+    const int t = tw + mt * 16 + col;
     if (t > tlast) continue;
     const int m = b * T + t;
 #pragma unroll
@@ -704,7 +710,7 @@ hipError_t launch_pnorm(const void *x, const void *norm_w, void *out, float eps,
 
 hipError_t launch_prefill_attn(const PattnParams &p, hipStream_t s) {
   const int nqb = (p.t_rows + kPaRows - 1) / kPaRows;
-  hipLaunchKernelGGL(pattn_kernel, dim3(nqb * p.batch * p.nkv), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(pattn_kernel<kPaWph>, dim3(nqb * p.batch * p.nkv), dim3(256 * kPaWph), 0, s, p);
   return hipSuccess;
 }
 
