@@ -364,9 +364,11 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
   // Workgroup tile (activation rows x weight rows): 256 x 256 reads a third
   // fewer LDS bytes per MFMA than 256 x 128 but makes half the workgroups;
   // 64 x 64 makes 8x the workgroups of 256 x 128 for few rows.  Picked by
-  // the launch size: 256 x 256 from 768 workgroups (three per CU; at 16K
-  // rows QKV +10%, gate/up +7%), 256 x 128 from 512, else 64 x 64 (a
-  // 512-token prompt: O and down would have 40 workgroups of 256 x 128).
+  // the launch size: 256 x 256 from 600 workgroups (at 16K rows QKV and
+  // gate/up ~+10%, down +6%, O even with 640 workgroups; at 8K rows O and
+  // down, 320 workgroups, are 10% faster on 256 x 128), 256 x 128 from 512,
+  // else 64 x 64 (a 512-token prompt: O and down would have 40 workgroups
+  // of 256 x 128).
   int trows = a->tile_rows, tcols = a->tile_cols;
   const bool pair_ok = (trows == 0 && tcols == 0) || (trows == 256 && (tcols == 128 || tcols == 256)) ||
                        (trows == 64 && tcols == 64);
@@ -375,7 +377,7 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
                      trows, tcols);
   if (trows == 0) {
     const int64_t row_tiles = a->tiles / 16;
-    if (a->n % 256 == 0 && (a->n / 256) * row_tiles >= 768) {
+    if (a->n % 256 == 0 && (a->n / 256) * row_tiles >= 600) {
       trows = 256, tcols = 256;
     } else if (a->n % 128 == 0 && (a->n / 128) * row_tiles >= 512) {
       trows = 256, tcols = 128;

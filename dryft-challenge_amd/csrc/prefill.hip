@@ -13,33 +13,41 @@ namespace qdec {
 namespace {
 
 // ------------------------------------------------------------------ product
-// A workgroup of 4 wavefronts computes a (32 XW) x (32 WN) tile of the
-// transposed product D = W . x^T: a weight fragment (16 weight rows x 32 k)
-// is the A operand and an activation fragment (32 k x 16 rows) the B operand
-// of v_mfma_f32_16x16x32_bf16, and both are one contiguous KiB in their
-// layouts.  Waves 2 x 2: wave (wn, wm) owns WN weight x XW activation
-// fragments.  Every fragment moves from global memory straight into LDS
+// A workgroup of 2 x NWM wavefronts computes a (16 NWM XW) x (32 WN) tile of
+// the transposed product D = W . x^T: a weight fragment (16 weight rows x 32
+// k) is the A operand and an activation fragment (32 k x 16 rows) the B
+// operand of v_mfma_f32_16x16x32_bf16, and both are one contiguous KiB in
+// their layouts.  Wave (wn, wm) owns WN weight x XW activation fragments.
+// Every fragment moves from global memory straight into LDS
 // (global_load_lds_dwordx4: one instruction per 1 KiB fragment, no
 // registers) through a ring of stage buffers, RING - 1 stages in flight
 // while one computes:
-//   256 x 128 (WN 4, XW 8): stages of two k steps (48 KiB), RING 3;
-//   256 x 256 (WN 8, XW 8): stages of one k step (32 KiB), RING 4 -- a
-//     third fewer LDS bytes per MFMA, half the workgroups;
-//   64 x 64 (WN 2, XW 2): stages of two k steps (16 KiB), RING 3 -- for
-//     few rows: 8x the workgroups of 256 x 128, several per CU.
-template <int WN, int XW>
+//   256 x 256 (8 waves of WN 8 x XW 4): stages of one k step (32 KiB),
+//     RING 4 -- a third fewer LDS bytes per MFMA than 256 x 128;
+//   256 x 128 (8 waves of WN 4 x XW 4): stages of two k steps (48 KiB),
+//     RING 3 -- twice the workgroups;
+//   64 x 64 (4 waves of WN 2 x XW 2): stages of two k steps (16 KiB),
+//     RING 3 -- for few rows: 8x the workgroups of 256 x 128, several per
+//     CU.
+// Eight waves of half the accumulators (~240 and ~100 registers) run two
+// per SIMD, so one wave's LDS reads overlap another's MFMAs: 5-15% over four
+// waves of twice the tile per wave.
+template <int WN, int XW, int NWM = 2>
 struct PgShape {
+  static constexpr int NW = 2 * NWM;                // waves: 2 along n x NWM along rows
   static constexpr int Wf = 2 * WN;                 // weight fragments per k step
-  static constexpr int Xf = 2 * XW;                 // activation fragments per k step
+  static constexpr int Xf = NWM * XW;               // activation fragments per k step
   static constexpr int KS = WN == 8 ? 1 : 2;        // k steps per stage
   static constexpr int RING = WN == 8 ? 4 : 3;      // stage buffers
   static constexpr int Frags = Wf + Xf;             // fragments per k step
   static constexpr int Stage = KS * Frags;          // fragments per stage
-  static constexpr int Loads = Stage / 4;           // loads per wave per stage
-  static constexpr int WQ = Wf / 4;                 // weight loads per wave per k step
-  static_assert(Wf % 4 == 0 && Xf % 4 == 0, "each wave loads whole fragments");
+  static constexpr int Loads = Stage / NW;          // loads per wave per stage
+  static constexpr int WQ = Wf / NW;                // weight loads per wave per k step
+  static_assert(Wf % NW == 0 && Xf % NW == 0, "each wave loads whole fragments");
 };
 constexpr int kPgGroupN = 4;  // column tiles walked together (x reuse in L2)
+constexpr int kPg256Xw = 4;   // 256 x 256 and 256 x 128 tiles: activation fragments per wave
+constexpr int kPg128Xw = 4;   //   (4: 8 waves; 8 would be 4 waves of twice the accumulators)
 
 __device__ __forceinline__ uint4 ld16(const uint16_t *p) { return *reinterpret_cast<const uint4 *>(p); }
 
@@ -76,9 +84,9 @@ __device__ __forceinline__ float max_xor16_32(float v) {
 constexpr int vmcnt_enc(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int kVmcnt0 = vmcnt_enc(0);
 
-template <uint32_t FLAGS, int WN, int XW>
-__global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
-  using S = PgShape<WN, XW>;
+template <uint32_t FLAGS, int WN, int XW, int NWM>
+__global__ void __launch_bounds__(128 * NWM, 1) pgemm_kernel(const PgemmParams p) {
+  using S = PgShape<WN, XW, NWM>;
   constexpr bool GLU = (FLAGS & QDEC_GLU) != 0;
   constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
   __shared__ uint4 lds[S::RING * S::Stage * 64];  // [ring slot][k step][fragment][lane]
@@ -108,11 +116,11 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
     else
       return tn * S::Wf + f;
   };
-  // Loads of one k step: this wave moves fragments wave + 4q (q < WQ:
+  // Loads of one k step: this wave moves fragments wave + NW q (q < WQ:
   // weights, then activations).
   const uint16_t *wb[S::WQ];
 #pragma unroll
-  for (int q = 0; q < S::WQ; ++q) wb[q] = p.w + (size_t)wtile(wave + 4 * q) * KS * 512 + lane * 8;
+  for (int q = 0; q < S::WQ; ++q) wb[q] = p.w + (size_t)wtile(wave + S::NW * q) * KS * 512 + lane * 8;
   const uint16_t *xb = p.x + (size_t)(tm * S::Xf + wave) * 512 + lane * 8;
   const size_t xks = (size_t)p.tiles * 512;  // elements per k step of x
   const uint32_t lds0 = lds_addr(lds);
@@ -122,9 +130,10 @@ __global__ void __launch_bounds__(256, 1) pgemm_kernel(const PgemmParams p) {
       const int ks = s * S::KS + j;
       const uint32_t dst = lds0 + (uint32_t)(((slot * S::KS + j) * S::Frags + wave) * 1024);
 #pragma unroll
-      for (int q = 0; q < S::WQ; ++q) dma16(wb[q] + (size_t)ks * 512, dst + q * 4 * 1024);
+      for (int q = 0; q < S::WQ; ++q) dma16(wb[q] + (size_t)ks * 512, dst + q * S::NW * 1024);
 #pragma unroll
-      for (int q = 0; q < S::Xf / 4; ++q) dma16(xb + ks * xks + q * 4 * 512, dst + (S::WQ + q) * 4 * 1024);
+      for (int q = 0; q < S::Xf / S::NW; ++q)
+        dma16(xb + ks * xks + q * S::NW * 512, dst + (S::WQ + q) * S::NW * 1024);
     }
   };
   // This wave's weight fragments (GLU: gate i pairs with up i + WN/2).
@@ -665,21 +674,22 @@ __global__ void __launch_bounds__(256 * WPH, 1) pattn_kernel(const PattnParams p
 
 }  // namespace
 
-template <int WN, int XW>
+template <int WN, int XW, int NWM>
 hipError_t launch_pgemm_tile(const PgemmParams &p, uint32_t flags, hipStream_t s) {
-  const dim3 grid(p.wg_n * (p.tiles / PgShape<WN, XW>::Xf)), block(256);
+  const dim3 grid(p.wg_n * (p.tiles / PgShape<WN, XW, NWM>::Xf)), block(128 * NWM);
   switch (flags) {
-    case 0u: hipLaunchKernelGGL((pgemm_kernel<0u, WN, XW>), grid, block, 0, s, p); break;
-    case QDEC_RES_OUT: hipLaunchKernelGGL((pgemm_kernel<QDEC_RES_OUT, WN, XW>), grid, block, 0, s, p); break;
-    case QDEC_GLU: hipLaunchKernelGGL((pgemm_kernel<QDEC_GLU, WN, XW>), grid, block, 0, s, p); break;
+    case 0u: hipLaunchKernelGGL((pgemm_kernel<0u, WN, XW, NWM>), grid, block, 0, s, p); break;
+    case QDEC_RES_OUT: hipLaunchKernelGGL((pgemm_kernel<QDEC_RES_OUT, WN, XW, NWM>), grid, block, 0, s, p); break;
+    case QDEC_GLU: hipLaunchKernelGGL((pgemm_kernel<QDEC_GLU, WN, XW, NWM>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;
 }
 
 hipError_t launch_pgemm(const PgemmParams &p, uint32_t flags, hipStream_t s) {
-  if (p.tile_rows == 64) return launch_pgemm_tile<2, 2>(p, flags, s);
-  return p.tile_cols == 256 ? launch_pgemm_tile<8, 8>(p, flags, s) : launch_pgemm_tile<4, 8>(p, flags, s);
+  if (p.tile_rows == 64) return launch_pgemm_tile<2, 2, 2>(p, flags, s);
+  return p.tile_cols == 256 ? launch_pgemm_tile<8, kPg256Xw, 256 / (16 * kPg256Xw)>(p, flags, s)
+                            : launch_pgemm_tile<4, kPg128Xw, 256 / (16 * kPg128Xw)>(p, flags, s);
 }
 
 // Grouped row kernels from this many rows (below it one workgroup per row

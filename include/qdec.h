@@ -287,7 +287,7 @@ int qdec_rownorm(const qdec_rownorm_args *a, qdec_stream_t stream);
 /* out = x @ W^T on the matrix cores for x in fragment order (`tiles` M
  * tiles, a multiple of 16), W tiled [n, k].  A workgroup computes tile_rows
  * x tile_cols of it: 256 x 128, 256 x 256 or 64 x 64 (0 x 0 picks by launch
- * size: 256 x 256 while it keeps 768 workgroups, 256 x 128 while 512, else
+ * size: 256 x 256 while it keeps 600 workgroups, 256 x 128 while 512, else
  * 64 x 64); n must be a multiple of tile_cols, k of 64.  flags:
  *   0            out = bf16(x @ W^T): [rows, n] row-major, or fragment order
  *                with out_frag;
