@@ -183,6 +183,22 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   const size_t up_off = (size_t)p.up_tiles * p.KS * 64;
   const int tile0 = tg * p.tiles_per_wg;
 
+  // RES_OUT with one tile and no k split: wave 0 loads its residual values
+  // first, so the epilogue does not wait on a dependent load after the last
+  // MFMA (the residual was written by an earlier launch).
+  const bool res_early = RES && p.tiles_per_wg == 1 && p.ksplit == 1;
+  uint2 res_v[MT];
+  if constexpr (RES) {
+    if (res_early && wave == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + col;
+        res_v[mt] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p.res) +
+                                                     (size_t)(m < rows ? m : 0) * p.n + tile0 * 16 + grp * 4);
+      }
+    }
+  }
+
   uint4 wb[NACC][NB];
   // Direct activations: the B fragment of ring slot r, loaded from global
   // (cache-resident x) right behind the slot's weight block.
@@ -544,7 +560,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
             }
         } else if constexpr (RES) {
           uint16_t *rp = reinterpret_cast<uint16_t *>(p.res) + (size_t)m * p.n + n0;
-          const uint2 r = *reinterpret_cast<const uint2 *>(rp);
+          const uint2 r = res_early ? res_v[mt] : *reinterpret_cast<const uint2 *>(rp);
           uint2 o;
           o.x = pack2(lo16(r.x) + rbf(acc[0][mt][0]), hi16(r.x) + rbf(acc[0][mt][1]));
           o.y = pack2(lo16(r.y) + rbf(acc[0][mt][2]), hi16(r.y) + rbf(acc[0][mt][3]));
