@@ -211,7 +211,10 @@ static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) 
   if (a->t_rows < 1 || a->t_rows > 16) return set_error(QDEC_EINVAL, "qdec_attn: t_rows %d not in [1, 16]", a->t_rows);
   if (a->cap < 32 || a->cap % 32) return set_error(QDEC_EINVAL, "qdec_attn: cap %d not a positive multiple of 32", a->cap);
   if (a->chunk < 32 || a->chunk % 32) return set_error(QDEC_EINVAL, "qdec_attn: chunk %d not a positive multiple of 32", a->chunk);
-  if (a->waves != 4) return set_error(QDEC_EINVAL, "qdec_attn: waves %d (the kernel runs 4 wavefronts)", a->waves);
+  if (a->waves != 4 && a->waves != 8)
+    return set_error(QDEC_EINVAL, "qdec_attn: waves %d (the kernel runs 4 or 8 wavefronts)", a->waves);
+  if (a->waves == 8 && a->t_rows > 8)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: 8 waves take at most 8 rows per sequence (t_rows %d)", a->t_rows);
   if (a->out_partials != 0 && a->out_partials != 1)
     return set_error(QDEC_EINVAL, "qdec_attn: out_partials %d not 0 or 1", a->out_partials);
   if (a->out_frag != 0 && a->out_frag != 1) return set_error(QDEC_EINVAL, "qdec_attn: out_frag %d not 0 or 1", a->out_frag);

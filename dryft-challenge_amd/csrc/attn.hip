@@ -1,7 +1,8 @@
 // GQA decode attention with the head RMSNorm, RoPE and KV-cache write fused
 // in, for t_rows query rows per sequence (1 = plain decode, K+1 = verify).
 //
-// Grid (chunk, kv head, sequence); a workgroup of NW wavefronts per cell.
+// Grid (chunk, kv head, sequence); a workgroup of NW = 4 or 8 wavefronts per
+// cell.
 //   1. Every wave builds the normalised, rotated queries of the G heads x
 //      t_rows rows in registers, already in the B-operand layout of
 //      v_mfma_f32_16x16x32_bf16 (query row r = G*t + g sits in MFMA column
@@ -33,11 +34,11 @@ namespace qdec {
 namespace {
 
 // Up to 32 query rows per kv head the body fits 256 registers without
-// spills: two workgroups per CU.
-template <int D, int G, int MTQ>
-__global__ void __launch_bounds__(256, MTQ <= 2 ? 2 : 1) attn_kernel(const AttnParams p) {
-  __shared__ __align__(16) unsigned char smem[kAttnLds];
-  attn_block<D, G, MTQ>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+// spills: two 4-wave workgroups per CU, or one of 8 waves.
+template <int D, int G, int MTQ, int NW>
+__global__ void __launch_bounds__(64 * NW, NW == 4 && MTQ <= 2 ? 2 : 1) attn_kernel(const AttnParams p) {
+  __shared__ __align__(16) unsigned char smem[AttnLds<NW>::bytes];
+  attn_block<D, G, MTQ, NW>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }
 
 }  // namespace
@@ -47,11 +48,19 @@ hipError_t launch_attn(const AttnParams &p, hipStream_t s) {
   const int mtq = (R + 15) / 16;
   dim3 grid(p.nchunks, p.nkv, p.batch);
   dim3 block(64 * p.waves);
+  if (p.waves == 8) {
+    switch (mtq) {
+      case 1: hipLaunchKernelGGL((attn_kernel<128, 4, 1, 8>), grid, block, 0, s, p); break;
+      case 2: hipLaunchKernelGGL((attn_kernel<128, 4, 2, 8>), grid, block, 0, s, p); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipSuccess;
+  }
   switch (mtq) {
-    case 1: hipLaunchKernelGGL((attn_kernel<128, 4, 1>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<128, 4, 2>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_kernel<128, 4, 3>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((attn_kernel<128, 4, 4>), grid, block, 0, s, p); break;
+    case 1: hipLaunchKernelGGL((attn_kernel<128, 4, 1, 4>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<128, 4, 2, 4>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((attn_kernel<128, 4, 3, 4>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<128, 4, 4, 4>), grid, block, 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;

@@ -1,10 +1,12 @@
 // Device body of the GQA decode attention with the head RMSNorm, RoPE and KV-cache write fused
 // in, for t_rows query rows per sequence (1 = plain decode, K+1 = verify).
 //
-// Grid (chunk, kv head, sequence); a workgroup of 4 wavefronts per cell.
+// Grid (chunk, kv head, sequence); a workgroup of NW = 4 or 8 wavefronts per
+// cell (the wave count, like the chunk, is part of the call: a row's
+// arithmetic depends on both, never on t_rows).
 //   1. Every wave issues the K/V loads of its first two 32-slot blocks, then
 //      the raw loads of its share of the query rows (row r = G*t + g goes to
-//      wave r % 4) and of the new key/value rows (t % 4), all before the
+//      wave r % NW) and of the new key/value rows (t % NW), all before the
 //      sequence length arrives (no address depends on it); a lane holds two
 //      channels of a row, so the head RMSNorm is one wave reduction and the
 //      rotate_half partner sits in lane ^ 32.  Normalised, rotated queries
@@ -13,7 +15,7 @@
 //      to the cache (nobody reads those cache slots in this launch).
 //   2. Each wave reads the queries back in the B-operand layout of
 //      v_mfma_f32_16x16x32_bf16 (query row r sits in MFMA column r % 16 of M
-//      tile r / 16) and walks its blocks (block j to wave j % 4, two blocks in
+//      tile r / 16) and walks its blocks (block j to wave j % NW, two blocks in
 //      flight): S^T = K . Q^T (two 16-slot MFMA tiles whose slot order makes
 //      the score registers exactly the B operand of the next product), online
 //      softmax in base 2, then O^T += V^T . P^T with V read from the
@@ -40,24 +42,27 @@
 namespace qdec {
 
 constexpr int kMaxT = 16;
-constexpr int kAttnWaves = 4;
 constexpr int kAttnRowStride = 128 + 8;  // bf16 per LDS row of queries / new keys (bank spread)
-// LDS layout (kAttnLds bytes).
-constexpr int kAttnKnOff = 0;                                    // new keys [kMaxT][row stride]
-constexpr int kAttnVpOff = kAttnKnOff + kMaxT * kAttnRowStride * 2;  // new values [3][128][8]
-constexpr int kAttnQOff = kAttnVpOff + 3 * 128 * 8 * 2;          // queries [64][row stride] or
-                                                                 // wave partials [4][8][64] f32x4
-constexpr int kAttnMOff = kAttnQOff + kAttnWaves * 8 * 64 * 16;  // wave row maxima [4][16]
-constexpr int kAttnLOff = kAttnMOff + kAttnWaves * 16 * 4;       // wave row sums [4][16]
-constexpr int kAttnFlagOff = kAttnLOff + kAttnWaves * 16 * 4;
-static_assert(64 * kAttnRowStride * 2 <= kAttnWaves * 8 * 64 * 16, "query rows fit the partials area");
-static_assert(kAttnLds == kAttnFlagOff + 16, "attention LDS size");
+// LDS layout of a workgroup of NW waves (bytes).
+template <int NW>
+struct AttnLds {
+  static constexpr int kn = 0;                             // new keys [kMaxT][row stride]
+  static constexpr int vp = kn + kMaxT * kAttnRowStride * 2;  // new values [3][128][8]
+  static constexpr int q = vp + 3 * 128 * 8 * 2;           // queries [64][row stride] or
+                                                           // wave partials [NW][8][64] f32x4
+  static constexpr int m = q + NW * 8 * 64 * 16;           // wave row maxima [NW][16]
+  static constexpr int l = m + NW * 16 * 4;                // wave row sums [NW][16]
+  static constexpr int flag = l + NW * 16 * 4;
+  static constexpr int bytes = flag + 16;
+  static_assert(64 * kAttnRowStride * 2 <= NW * 8 * 64 * 16, "query rows fit the partials area");
+};
 
-template <int D, int G, int MTQ>
+template <int D, int G, int MTQ, int NW>
 __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, const int kvh, const int b,
                                            unsigned char *smem) {
   static_assert(D == 128 && G == 4, "head_dim 128, 4 query heads per kv head");
-  constexpr int NW = kAttnWaves;
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  using LY = AttnLds<NW>;
   constexpr int DS = D / 32;              // MFMA k steps over the head dimension
   constexpr int DT = D / 16;              // 16-channel output tiles
   constexpr int DTW = DT / NW;            // output tiles each wave finishes
@@ -66,13 +71,13 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   constexpr int KPW = kMaxT / NW;         // new rows per wave, at most
   constexpr int RS = kAttnRowStride;
 
-  uint16_t *s_kn = reinterpret_cast<uint16_t *>(smem + kAttnKnOff);
-  uint16_t *s_vp = reinterpret_cast<uint16_t *>(smem + kAttnVpOff);
-  uint16_t *s_q = reinterpret_cast<uint16_t *>(smem + kAttnQOff);
-  f32x4_t *s_acc = reinterpret_cast<f32x4_t *>(smem + kAttnQOff);
-  float *s_m = reinterpret_cast<float *>(smem + kAttnMOff);
-  float *s_l = reinterpret_cast<float *>(smem + kAttnLOff);
-  uint32_t *s_flag = reinterpret_cast<uint32_t *>(smem + kAttnFlagOff);
+  uint16_t *s_kn = reinterpret_cast<uint16_t *>(smem + LY::kn);
+  uint16_t *s_vp = reinterpret_cast<uint16_t *>(smem + LY::vp);
+  uint16_t *s_q = reinterpret_cast<uint16_t *>(smem + LY::q);
+  f32x4_t *s_acc = reinterpret_cast<f32x4_t *>(smem + LY::q);
+  float *s_m = reinterpret_cast<float *>(smem + LY::m);
+  float *s_l = reinterpret_cast<float *>(smem + LY::l);
+  uint32_t *s_flag = reinterpret_cast<uint32_t *>(smem + LY::flag);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;

@@ -83,11 +83,6 @@ struct AttnParams {
 };
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 
-// LDS bytes of one attention block (attn_dev.h).
-// new keys 16 x (128 + 8) bf16, new values 3 x 128 x 8 bf16, queries / wave
-// partials 4 x 8 x 64 f32x4, wave maxima and sums 2 x 4 x 16 f32, a flag.
-constexpr int kAttnLds = 16 * 136 * 2 + 3 * 128 * 8 * 2 + 4 * 8 * 64 * 16 + 2 * 4 * 16 * 4 + 16;
-
 
 // ---- prefill (prefill.hip)
 // Product tiles of a workgroup (activation rows x weight rows): 256 x 128,

@@ -204,8 +204,10 @@ typedef struct qdec_attn_args {
   int32_t head_dim;     /* 128 */
   int32_t cap;          /* slots per sequence, multiple of 32 */
   int32_t chunk;        /* slots per workgroup, multiple of 32 */
-  int32_t waves;        /* wavefronts per workgroup: must be 4; blocks of 32
-                           slots are dealt to them round robin */
+  int32_t waves;        /* wavefronts per workgroup: 4, or 8 for t_rows <= 8;
+                           blocks of 32 slots are dealt to them round robin.
+                           A row's result depends on chunk and waves, never
+                           on t_rows */
   int32_t out_partials; /* 0: merged rows to out.  1: every chunk leaves its
                            unnormalised (acc, max, sum) in partial, out is not
                            written, and a qdec_gemm with x_attn = these

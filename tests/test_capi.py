@@ -110,6 +110,7 @@ def _attn(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(head_dim=64), -3), (dict(nq=16), -3), (dict(t_rows=17), -1), (dict(cap=100), -1),
     (dict(chunk=48), -1), (dict(waves=5), -1), (dict(waves=2), -1), (dict(out=None), -1), (dict(partial=None), -1), (dict(qkv=8), -2),
+    (dict(waves=8, t_rows=9), -3),
 ])
 def test_attn_validation(qlib, kw, code):
     assert qlib.so.qdec_attn(ctypes.byref(_attn(**kw)), None) == code

@@ -71,7 +71,7 @@ def run_state(engine, prompt, n):
     return torch.stack(toks, 1), torch.stack(logits, 1)
 
 
-@pytest.mark.parametrize("B,S,n,seed", [(1, 40, 10, 1), (3, 21, 8, 2)])
+@pytest.mark.parametrize("B,S,n,seed", [(1, 40, 10, 1), (3, 21, 8, 2), (8, 17, 5, 4)])
 def test_logits_and_tokens_vs_oracle(engine, oracle, B, S, n, seed):
     prompt = prompts(B, S, seed)
     toks, logits = run_state(engine, prompt, n)

@@ -18,6 +18,8 @@ qdec_prefill_attn) on the GPU.
 import pytest
 import torch
 
+from helpers import near_exact
+
 from oracle.qwen3_oracle import attention, bf16, head_norm_rope, rms_norm, rope_tables, silu_mul
 
 pytestmark = pytest.mark.gpu
@@ -166,20 +168,6 @@ def test_prefill_gemm_random_vs_fp32(lib, rows, n, k):
     ref = bf16(x.float() @ w.float().T)
     assert (out - ref).abs().max().item() <= 0.01 * ref.abs().max().item()
     assert (out == ref).float().mean().item() >= 0.95
-
-
-def near_exact(got, ref, frac=0.999):
-    """Nearly all values equal; the rest within one bf16 ulp of their head
-    row's largest value (a flipped rounding of a normalised channel moves
-    the RoPE sum by an ulp of its larger term)."""
-    got, ref = got.float(), ref.float()
-    assert torch.isfinite(got).all()
-    head_max = ref.reshape(*ref.shape[:-1], -1, D).abs().amax(-1, keepdim=True)
-    bound = (head_max * 2.0 ** -7).expand(*ref.shape[:-1], -1, D).reshape(ref.shape)
-    bad = ((got - ref).abs() > bound).nonzero()
-    assert bad.shape[0] == 0, (f"{bad.shape[0]} values off by more than an ulp, first {bad[:4].tolist()}, "
-                               f"max diff {(got - ref).abs().max().item()}")
-    assert (got == ref).float().mean().item() >= frac
 
 
 def v_layout(v):
