@@ -139,14 +139,15 @@ def role_plan(n, k, role):
     return ksplit, waves, tiles
 
 
-def attn_waves(batch, max_t):
+def attn_waves(batch):
     """Wavefronts per attention workgroup: 8 from batch 8, so all blocks of
     a 512-slot chunk (or two per wave of a whole-cache one) are in flight at
     once (MI355X, ms/step: batch 8 3.100 -> 3.076, batch 32 6.129 -> 6.098),
-    else 4.  A row's arithmetic depends on the count, so one state uses one
-    count for its plain and verify steps, and 8 waves take at most 8 rows
-    per sequence."""
-    return 8 if batch >= 8 and max_t <= 8 else 4
+    else 4.  A row's arithmetic depends on the count, so it is a function of
+    the batch alone: plain and speculative states of one batch agree.  8
+    waves take at most 8 rows per sequence, and a state of batch 8 or more
+    has at most GEMM_MAX_ROWS // 8 = 8."""
+    return 8 if batch >= 8 else 4
 
 
 def attn_chunk(batch, nkv, cap):
@@ -248,7 +249,8 @@ class DecodeState:
         dev, bf = model.device, torch.bfloat16
         L, H, D = c.n_layers, c.hidden, c.head_dim
         self.chunk = attn_chunk(batch, c.nkv, self.cap)
-        self.attn_waves = attn_waves(batch, self.max_t)
+        self.attn_waves = attn_waves(batch)
+        assert self.attn_waves == 4 or self.max_t <= 8
         cache_shape = (L, batch, c.nkv, self.cap, D)
         self.k_cache = torch.zeros(cache_shape, dtype=bf, device=dev)
         self.v_cache = torch.zeros(cache_shape, dtype=bf, device=dev)
