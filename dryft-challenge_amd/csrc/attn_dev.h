@@ -368,13 +368,22 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
           o.y = pack2(tot[2] / Lrow, tot[3] / Lrow);
           *reinterpret_cast<uint2 *>(out_at(b * T + t, (kvh * G + hq) * D + dt * 16 + grp * 4)) = o;
         } else {
-          store_coherent4(part + (size_t)r * D + dt * 16 + grp * 4, tot);
+          float *dst = part + (size_t)r * D + dt * 16 + grp * 4;
+          if (p.out_partials)  // read by the next launch only
+            *reinterpret_cast<f32x4_t *>(dst) = tot;
+          else
+            store_coherent4(dst, tot);
         }
       }
     }
     if (!direct && wave == 0 && grp == 0 && r < R) {
-      store_coherent(part + (size_t)R * D + r, M);
-      store_coherent(part + (size_t)R * D + R + r, Lrow);
+      if (p.out_partials) {
+        part[(size_t)R * D + r] = M;
+        part[(size_t)R * D + R + r] = Lrow;
+      } else {
+        store_coherent(part + (size_t)R * D + r, M);
+        store_coherent(part + (size_t)R * D + R + r, Lrow);
+      }
     }
   }
   if (direct || p.out_partials) return;  // done, or the consuming GEMM merges
