@@ -74,26 +74,62 @@ def step_bytes(model_cfg, weight_bytes, batch, pos):
     return weight_bytes + batch * per_tok * (pos + 1) + batch * per_tok
 
 
+ROLES = ("qkv", "attn", "o", "gate_up", "down", "lm")
+
+
 def time_gemm_role(engine, state, role, reps=5):
-    """Average duration (s) of one launch of ``role``'s GEMM, over all layers'
-    weights (so nothing is served from the 256 MB MALL), HIP events on the
-    engine's stream."""
+    """Average duration (s) of one launch of ``role``'s kernel (a GEMM, or
+    ``attn``: the decode attention as the step launches it), over all
+    layers' weights / caches (so nothing is served from the 256 MB MALL),
+    HIP events on the engine's stream."""
     import torch
     lib = engine.lib
     rows = state.batch
-    args = [state._gemm_args(role, i, rows) for i in range(engine.model.cfg.n_layers)]
+    n = engine.model.cfg.n_layers if role != "lm" else 1
+    if role == "attn":
+        pm = state._merge_in_o(1)
+        args = [state._attn_args(i, 1, partials=pm) for i in range(n)]
+        call = lib.attn
+    elif role == "o" and state._merge_in_o(1):  # merges the attention's chunk partials, as in the step
+        args = [state._gemm_args(role, i, rows, x_attn=state._attn_args(i, 1, partials=True)) for i in range(n)]
+        call = lib.gemm
+    else:
+        args = [state._gemm_args(role, i, rows) for i in range(n)]
+        call = lib.gemm
     s = torch.cuda.current_stream()
     for a in args:  # warm
-        lib.gemm(a, s.cuda_stream)
+        call(a, s.cuda_stream)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record(s)
     for _ in range(reps):
         for a in args:
-            lib.gemm(a, s.cuda_stream)
+            call(a, s.cuda_stream)
     e1.record(s)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / 1e3 / (reps * len(args))
+
+
+def read_ceiling(lib, device, gib=2, reps=5):
+    """Streaming-read bandwidth of this device (bytes/s): qdec_read_probe over
+    a buffer 8x the 256 MB memory-side cache, 16-byte non-temporal loads as
+    the decode kernels issue them; mean of ``reps`` launches timed with HIP
+    events on the current stream."""
+    import torch
+    buf = torch.empty(gib << 30, dtype=torch.uint8, device=device)
+    blocks = 8192
+    sink = torch.zeros(blocks, dtype=torch.int32, device=device)
+    s = torch.cuda.current_stream()
+    lib.read_probe(buf.data_ptr(), buf.numel(), sink.data_ptr(), blocks, s.cuda_stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for _ in range(reps):
+        lib.read_probe(buf.data_ptr(), buf.numel(), sink.data_ptr(), blocks, s.cuda_stream)
+    e1.record(s)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / 1e3 / reps
+    del buf
+    return (gib << 30) / sec
 
 
 def prefill_flops(mc, batch, prompt_len):
@@ -162,6 +198,19 @@ def spec_bench(eng, vocab, batch=4, prompt_len=1024, new_tokens=512, seed=5):
     stats = dict(eng.stats.get("spec", {}))
     n_draft = eng.shape.spec_k if eng.shape is not None else None
     n_tok = batch * (new_tokens - 1)
+    # How predictable the plain greedy stream is from its own history: the
+    # fraction of generated positions whose trailing 3-gram already occurred
+    # earlier in the sequence (prompt included).
+    plain_rows = list(map(list, zip(*res[False][0])))
+    rep = tot = 0
+    for b in range(batch):
+        seq = prompts[b] + plain_rows[b]
+        seen = {tuple(seq[j:j + 3]) for j in range(len(prompts[b]) - 2)}
+        for i in range(len(prompts[b]), len(seq)):
+            g3 = tuple(seq[i - 2:i + 1])
+            rep += g3 in seen
+            tot += 1
+            seen.add(g3)
     plain_tps, spec_tps = n_tok / res[False][1], n_tok / res[True][1]
     ceiling = spec_ceiling(eng, prompts, res[False][0], new_tokens, plain_tps)
     log(f"speculation ceiling (drafts = the plain run's tokens): {ceiling}")
@@ -177,6 +226,10 @@ def spec_bench(eng, vocab, batch=4, prompt_len=1024, new_tokens=512, seed=5):
             "plain_iterations": stats.get("plain_iterations"),
             "verify_cost_ratio": stats.get("cost_ratio"),
             "drafts_per_verify": n_draft,
+            "draft_hit_rate": round(stats.get("draft_hit_rate", float("nan")), 4),
+            "predicted_tokens_per_verify": round(stats.get("predicted_tokens_per_verify", float("nan")), 4),
+            "positions_scored": stats.get("positions_scored"),
+            "repeated_3gram_frac": round(rep / max(tot, 1), 4),
             "token_identical": res[False][0] == res[True][0],
             "ceiling": ceiling}
 
@@ -323,9 +376,11 @@ def cpu_baseline(ckpt, cfg, prompt_len, budget_s=25.0):
         what = "oracle restatement (torch CPU fp32 with bf16 rounding)"
     times.sort()
     med = times[len(times) // 2]
-    return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": threads, "kind": kind,
+    return {"value": round(1.0 / med, 4), "unit": "tok/s", "cores": threads, "host_cores": cores,
+            "torch_threads": torch.get_num_threads(), "kind": kind,
             "sample": f"{what}; batch 1, prefill {prompt_len} tokens (untimed), then {len(times)} greedy "
-                      f"decode steps, median {med:.3f} s/step; same seed-0 checkpoint as the GPU run"}
+                      f"decode steps, median {med:.3f} s/step; same seed-0 checkpoint as the GPU run; "
+                      f"{threads} threads of {cores} host cores in this process's affinity"}
 
 
 def main():
@@ -338,11 +393,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-spec", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
-    ap.add_argument("--pmc-role", choices=("qkv", "o", "gate_up", "down", "lm"),
-                    help="only launch this role's GEMM over every layer (6 rounds, rows = the "
-                         "config's batch), then a 512 MiB device copy as the counter calibration, "
-                         "for rocprofv3 --pmc")
-    ap.add_argument("--cpu-prompt", type=int, default=64)
+    ap.add_argument("--pmc-role", choices=ROLES + ("all",),
+                    help="only launch this role's kernel over every layer (6 rounds, rows = the "
+                         "config's batch; 'all' = every role in turn), then a 512 MiB device copy "
+                         "as the counter calibration, for rocprofv3 --pmc")
+    ap.add_argument("--cpu-prompt", type=int, default=512, help="prompt tokens of the CPU baseline's prefill "
+                    "(config 2's 512 by default)")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="REPS",
                     help="only prefill the config's prompts REPS times and print their timing (for profiling)")
     args = ap.parse_args()
@@ -381,7 +437,8 @@ def main():
         else:  # counters only: batched configs run on random activations, no prefill
             st.h.normal_(0.0, 1.0)
             st.act.normal_(0.0, 1.0)
-        time_gemm_role(eng, st, args.pmc_role, reps=5)
+        for role in (ROLES if args.pmc_role == "all" else (args.pmc_role,)):
+            time_gemm_role(eng, st, role, reps=5)
         src = torch.empty(512 << 20, dtype=torch.uint8, device=eng.device)
         dst = torch.empty_like(src)
         for _ in range(5):
@@ -426,6 +483,8 @@ def main():
     log(f"{args.steps} steps: {ms:.4f} ms/step (events {1e3 * gpu_s / args.steps:.4f}), "
         f"{tok_s:.1f} tok/s, {step_tbs:.3f} TB/s algorithmic")
 
+    ceiling = read_ceiling(eng.lib, eng.device)
+    log(f"streaming-read ceiling (2 GiB, non-temporal 16-byte loads): {ceiling / 1e12:.3f} TB/s")
     # dominant kernel: gate/up (NORM_IN + GLU), bytes = both weight halves +
     # activations in + act out.
     t_gu = time_gemm_role(eng, st, "gate_up")
@@ -433,7 +492,7 @@ def main():
     gu_gbs = gu_bytes / t_gu / 1e9
     log(f"gate_up GEMM: {t_gu * 1e6:.2f} us/launch, {gu_gbs:.1f} GB/s")
     roles = {}
-    for role in ("qkv", "o", "down", "lm"):
+    for role in ("qkv", "attn", "o", "down", "lm"):
         roles[role] = round(time_gemm_role(eng, st, role) * 1e6, 2)
     log(f"other roles us/launch: {roles}")
 
@@ -482,6 +541,8 @@ def main():
                    "parallelism": "single GPU"},
         "step_hbm": {"achieved_TBs": round(step_tbs, 4), "peak_TBs": HBM_PEAK_GBS / 1e3,
                      "frac": round(step_tbs * 1e3 / HBM_PEAK_GBS, 4),
+                     "measured_read_ceiling_TBs": round(ceiling / 1e12, 4),
+                     "frac_of_measured_ceiling": round(step_tbs * 1e12 / ceiling, 4),
                      "bytes_per_step_mean": int(total_bytes / len(positions))},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,

@@ -190,6 +190,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     p->a_nkv = xa->nkv;
     p->a_chunk = xa->chunk;
     p->a_nchunks = (xa->cap + xa->chunk - 1) / xa->chunk;
+    p->a_cap = xa->cap;
   }
   size_t pb = 0, cb = 0, xn_off = 0;
   gemm_scratch(a, *p, &pb, &cb, &xn_off);
@@ -276,6 +277,15 @@ int qdec_pack_tiles(const void *src, void *dst, int64_t n, int64_t k, qdec_strea
                      (long long)n, (long long)k);
   if (!aligned16(src) || !aligned16(dst)) return set_error(QDEC_EALIGN, "qdec_pack_tiles: pointers must be 16-byte aligned");
   return launch_status(launch_pack(src, dst, n, k, (hipStream_t)stream), "qdec_pack_tiles");
+}
+
+int qdec_read_probe(const void *buf, int64_t bytes, uint32_t *sink, int32_t blocks, qdec_stream_t stream) {
+  if (!buf || !sink) return set_error(QDEC_EINVAL, "qdec_read_probe: null pointer");
+  if (bytes <= 0 || bytes % 16 || blocks < 1)
+    return set_error(QDEC_EINVAL, "qdec_read_probe: bytes %lld (a positive multiple of 16), blocks %d",
+                     (long long)bytes, blocks);
+  if (!aligned16(buf)) return set_error(QDEC_EALIGN, "qdec_read_probe: buf must be 16-byte aligned");
+  return launch_status(launch_read(buf, bytes, sink, blocks, (hipStream_t)stream), "qdec_read_probe");
 }
 
 int qdec_embed(const qdec_embed_args *a, qdec_stream_t stream) {

@@ -143,7 +143,22 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
 
   const int L = p.lens[b];
   const int last = L + T - 1;
-  if (L < 0 || last >= p.cap) return;  // never index outside the cache slab
+  uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
+  // Output row m, column k (row-major, or fragment order for a direct GEMM).
+  auto out_at = [&](int m, int k) { return p.ofrag ? out + frag_off(m, k, p.ofrag) : out + (size_t)m * nq * D + k; };
+  if (L < 0 || last >= p.cap) {
+    // Never index outside the cache slab.  The rows of this (sequence, kv
+    // head) become NaN (written by chunk 0; with out_partials the consuming
+    // GEMM's merge makes the same check), so the step's argmax yields an
+    // out-of-vocabulary id instead of a token computed from stale data.
+    if (c == 0 && !p.out_partials) {
+      for (int i = threadIdx.x; i < R * (D / 4); i += blockDim.x) {
+        const int r = i / (D / 4), k4 = (i - r * (D / 4)) * 4;
+        *reinterpret_cast<uint2 *>(out_at(b * T + r / G, (kvh * G + r % G) * D + k4)) = make_uint2(0x7fc07fc0u, 0x7fc07fc0u);
+      }
+    }
+    return;
+  }
   if (c0 > last) return;
   const int n_active = last / p.chunk + 1;
   const int nb = (min(c1, last + 1) - c0 + 31) / 32;  // blocks in this chunk
@@ -321,9 +336,6 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   // caller asked for partials (a GEMM merging them in its prologue, with the
   // arithmetic of the merge below: one chunk gives tot * 1 / (Lrow * 1)).
   const bool direct = n_active == 1 && !p.out_partials;
-  uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
-  // Output row m, column k (row-major, or fragment order for a direct GEMM).
-  auto out_at = [&](int m, int k) { return p.ofrag ? out + frag_off(m, k, p.ofrag) : out + (size_t)m * nq * D + k; };
   const size_t cstride = (size_t)R * (D + 2);  // floats per chunk partial: acc [R][D], m [R], l [R]
   float *part_b = p.partial + ((size_t)b * nkv + kvh) * p.nchunks * cstride;
   float *part = part_b + (size_t)c * cstride;

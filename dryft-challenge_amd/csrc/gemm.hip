@@ -97,7 +97,12 @@ __device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk)
   const int r = t * G + (h - kvh * G);
   const size_t cstride = (size_t)R * (D + 2);
   const float *part_b = p.apart + ((size_t)b * p.a_nkv + kvh) * p.a_nchunks * cstride;
-  const int n_active = (p.alens[b] + T - 1) / p.a_chunk + 1;
+  const int L = p.alens[b];
+  // A length the attention rejected (it wrote no partials) gives NaN, never
+  // a merge of stale partials; the NaN reaches the argmax, whose pick is
+  // then an out-of-vocabulary id the host refuses.
+  if (L < 0 || L + T - 1 >= p.a_cap) return make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
+  const int n_active = min((L + T - 1) / p.a_chunk + 1, p.a_nchunks);
   const float NEG_INF = -__builtin_huge_valf();
   float mc[CB], lc[CB];
   f32x4_t a0[CB], a1[CB];
@@ -255,9 +260,25 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
     issue_first();
   } else if (p.xfast) {
     // Row m, vectors vr = tid + j*nthr of the workgroup's k range (per_row
-    // of them), loaded into registers before the first weights.
+    // of them), loaded into registers before the first weights.  (Attention
+    // partials are merged before the weights go out too: loads complete in
+    // issue order, so weights issued first would hold the merge back until
+    // they had all arrived -- O at batch 1 measured 9.3 against 8.3 us.)
     const int per_row = p.ksw * nw * 4;
+    const bool merge = !XD && !NORM && p.amerge;
     uint4 xr[FR][kFastVec];
+    // NORM_IN without GLU: this thread's norm-weight vectors, loaded with x
+    // (gate/up reads them after the weights instead: 8 more registers would
+    // cost it its third wave per SIMD).
+    constexpr bool NPRE = NORM && !GLU;
+    uint4 nr[NPRE ? kFastVec : 1];
+#pragma unroll
+    for (int j = 0; j < (NPRE ? kFastVec : 1); ++j) {
+      const int vr = tid + j * nthr;
+      nr[j] = (NPRE && vr < per_row)
+                  ? *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p.norm_w) + ks_wg * 32 + 8 * vr)
+                  : zero4();
+    }
 #pragma unroll
     for (int m = 0; m < FR; ++m)
 #pragma unroll
@@ -265,7 +286,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         const int vr = tid + j * nthr;
         const bool ok = m < rows && vr < per_row;
         const int mm = ok ? m : 0, vv = ok ? vr : 0;
-        if (!XD && !NORM && p.amerge) {
+        if (merge) {
           xr[m][j] = ok ? attn_merge8(p, mm, ks_wg * 32 + 8 * vv) : zero4();
         } else {
           const uint4 v = *reinterpret_cast<const uint4 *>(X + (size_t)mm * p.k + ks_wg * 32 + 8 * vv);
@@ -295,7 +316,9 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         const int vr = tid + j * nthr;
         if (m < rows && vr < per_row) {
           uint4 xv = xr[m][j];
-          if constexpr (NORM)
+          if constexpr (NPRE)
+            xv = norm8(xv, nr[j], s_rstd[m]);
+          else if constexpr (NORM)
             xv = norm8(xv, *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p.norm_w) + ks_wg * 32 + 8 * vr),
                        s_rstd[m]);
           *reinterpret_cast<uint4 *>(s_x + (size_t)m * xstride + 8 * vr) = xv;

@@ -53,7 +53,7 @@ struct GemmParams {
   int amerge;
   const float *apart;
   const int32_t *alens;
-  int a_t_rows, a_nkv, a_chunk, a_nchunks;
+  int a_t_rows, a_nkv, a_chunk, a_nchunks, a_cap;
   size_t lds_bytes;
 };
 bool gemm_flags_supported(uint32_t flags);
@@ -137,6 +137,7 @@ hipError_t launch_pnorm(const void *x, const void *norm_w, void *out, float eps,
 hipError_t launch_embed(const int64_t *ids, const void *emb, void *h, int rows, int hidden,
                         int vocab, hipStream_t s);
 hipError_t launch_pack(const void *src, void *dst, int64_t n, int64_t k, hipStream_t s);
+hipError_t launch_read(const void *buf, int64_t bytes, uint32_t *sink, int blocks, hipStream_t s);
 hipError_t launch_draft(const int64_t *hist, const int32_t *lens, int64_t *ids, int64_t *draft,
                         int batch, int cap, int primary, int backoff, int k, hipStream_t s);
 hipError_t launch_accept(const int64_t *out_tok, const int64_t *draft, int64_t *hist,

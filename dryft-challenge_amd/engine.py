@@ -38,7 +38,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 if _HERE not in sys.path:
     sys.path.insert(0, _HERE)
 
-from qdec import capi  # noqa: E402
+from qdec import capi, selfcheck  # noqa: E402
 from qdec.checkpoint import load_config, load_tensors  # noqa: E402
 from qdec.runtime import DecodeState, DeviceModel  # noqa: E402
 
@@ -108,6 +108,9 @@ class Engine:
         torch.cuda.set_device(self.device)
         self.lib = capi.lib()
         self.model = DeviceModel(cfg, tensors, self.device)
+        # Known-answer checks of every kernel family on this device, with the
+        # model's own weights and plans; raises on a mismatch (no fallback).
+        selfcheck.run(DecodeState(self.model, 1, 64, max_t=1))
         self.speculate = bool(speculate)
         self.spec_gate = True  # speculation falls back to plain steps when drafts do not pay
         self.use_graphs = use_graphs
@@ -159,7 +162,18 @@ class Engine:
 
     def _fetch(self, sh, step):
         sh.events[step].synchronize()
-        return sh.host[step].tolist()
+        return self._checked(sh.host[step].tolist())
+
+    def _checked(self, toks):
+        """Tokens as emitted, or an error if the device flagged invalid state
+        (capi.NAN_ID: an out-of-range token id or cache length made a row
+        NaN; the kernels never substitute a value)."""
+        vocab = self.model.cfg.vocab
+        for t in toks:
+            if not 0 <= t < vocab:
+                raise capi.QdecError("generate", -1, f"device emitted token id {t} (vocab {vocab}): an "
+                                     "out-of-range token id or cache length reached a kernel")
+        return toks
 
     def generate(self, input_ids: list[list[int]], max_new_tokens: int):
         """Greedy continuation of every sequence, one step at a time.
@@ -175,6 +189,8 @@ class Engine:
         if ids.dim() != 2 or ids.shape[1] < 1:
             raise ValueError("input_ids must be a non-empty list of equal-length lists")
         batch, prompt_len = ids.shape
+        if int(ids.min()) < 0 or int(ids.max()) >= self.model.cfg.vocab:
+            raise ValueError(f"input_ids must lie in [0, {self.model.cfg.vocab})")
         if self.speculate:
             yield from self._generate_spec(ids, steps)
             return

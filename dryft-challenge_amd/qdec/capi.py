@@ -15,6 +15,9 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(os.path.ab
                       "include", "qdec.h")
 
 NORM_IN, GLU, RES_OUT, ARGMAX = 1, 2, 4, 8
+# Greedy pick of a row whose logits are all NaN (QDEC_NAN_ID): the kernels turn
+# an out-of-range token id or cache length into NaN rows instead of guessing.
+NAN_ID = 2147483647
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
@@ -105,6 +108,8 @@ class Lib:
         so.qdec_tiled_offset.restype = ctypes.c_int64
         so.qdec_tiled_offset.argtypes = [ctypes.c_int64] * 3
         so.qdec_pack_tiles.argtypes = [P, P, ctypes.c_int64, ctypes.c_int64, P]
+        so.qdec_read_probe.argtypes = [P, ctypes.c_int64, P, I32, P]
+        so.qdec_read_probe.restype = ctypes.c_int
         for name, st in (("qdec_embed", EmbedArgs), ("qdec_gemm", GemmArgs), ("qdec_attn", AttnArgs),
                          ("qdec_ngram_draft", DraftArgs), ("qdec_spec_accept", AcceptArgs),
                          ("qdec_rownorm", RownormArgs), ("qdec_prefill_gemm", PgemmArgs),
@@ -136,6 +141,9 @@ class Lib:
 
     def pack_tiles(self, src, dst, n, k, stream):
         self._check("qdec_pack_tiles", self.so.qdec_pack_tiles(src, dst, n, k, stream))
+
+    def read_probe(self, buf, nbytes, sink, blocks, stream):
+        self._check("qdec_read_probe", self.so.qdec_read_probe(buf, nbytes, sink, blocks, stream))
 
     def embed(self, args, stream):
         self._check("qdec_embed", self.so.qdec_embed(ctypes.byref(args), stream))

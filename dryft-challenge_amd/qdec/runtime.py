@@ -80,7 +80,9 @@ class ModelConfig:
         self.eps = float(cfg.get("rms_norm_eps", 1e-6))
         rp = cfg.get("rope_parameters") or {}
         self.theta = float(rp.get("rope_theta", cfg.get("rope_theta", 10000.0)))
-        self.tied = bool(cfg.get("tie_word_embeddings", True))
+        # Transformers Qwen3Config default (configuration_qwen3.py:74): untied
+        # unless the config says otherwise.
+        self.tied = bool(cfg.get("tie_word_embeddings", False))
         self.n_qkv = (self.nq + 2 * self.nkv) * self.head_dim
 
     def check_supported(self):
@@ -187,6 +189,13 @@ class DeviceModel:
         def get(name):
             t = tensors[name]
             return t.to(device=dev, dtype=bf).contiguous()
+
+        # A tied checkpoint may still carry lm_head.weight; the engine streams
+        # the embedding for the lm_head, so the two must be the same matrix.
+        if "lm_head.weight" in tensors and not torch.equal(tensors["lm_head.weight"],
+                                                           tensors["model.embed_tokens.weight"]):
+            raise ValueError("config ties the embeddings but lm_head.weight differs from "
+                             "model.embed_tokens.weight")
 
         def pack(dst, src):
             n, k = src.shape

@@ -24,17 +24,26 @@ step bit for bit, so the emitted stream is exactly the plain greedy stream.
 Acceptance gate (the reference's rule at notes/attempts.md:396-404: keep
 speculating only while tokens per iteration beat the cost ratio).  A second
 graph runs the same iteration with ``k = 0`` -- a plain step that keeps the
-history.  The decoder measures the time ratio of the two graphs once, tracks
-the mean tokens emitted per sequence by recent verify iterations, and runs
-``k = 0`` iterations while that mean is below the ratio (plus a margin),
-probing with a few verify iterations after ``PROBE_EVERY`` plain ones (a
-gap that doubles while probes keep failing).  Both
-graphs emit greedy tokens, so the gate changes the speed, never the tokens.
+history.  The decoder measures the time ratio of the two graphs once and
+predicts, without spending a verify pass, what a verify iteration would
+yield: the host keeps an index of every sequence's n-grams (``NgramIndex``,
+the drafter's search rule restated over the tokens it has already received)
+and, for every position, compares the draft the device would have made there
+with the greedy tokens that actually followed.  Greedy decoding is
+deterministic and the history is the same in both modes, so that comparison
+is exactly the acceptance a verify iteration at that position would have
+had.  The decoder verifies while the mean over the recent positions beats
+the cost ratio by 5%, and runs ``k = 0`` iterations otherwise; there are no
+probe iterations.  Both graphs emit greedy tokens, so the gate changes the
+speed, never the tokens.
 
 The host only reads ``naccept`` and ``out_tok`` after each iteration, through
 a pinned ring and one event per iteration, with up to LOOKAHEAD iterations in
 flight.
 """
+
+import bisect
+import collections
 
 import torch
 
@@ -42,10 +51,95 @@ from . import capi
 
 LOOKAHEAD = 3
 MARGIN = 1.05       # verify must beat the cost ratio by 5%
-EMA = 0.25          # weight of the newest verify iteration in the running mean
-PROBE_EVERY = 32    # plain iterations before the first probe while the gate is shut
-PROBE_MAX = 512     # the gap doubles after every probe that does not reopen the gate
-PROBE_LEN = 3       # verify iterations per probe
+WINDOW = 64         # positions (over all sequences) in the predicted acceptance mean
+MIN_SAMPLES = 8     # positions needed before the gate may open
+
+
+class NgramIndex:
+    """One sequence's history on the host and, per n-gram length, the start
+    positions of every n-gram in it (appended in increasing order).
+
+    ``draft(L)`` returns the k drafts qdec_ngram_draft makes at length L
+    (``hist[L]`` = the current token): the most recent earlier occurrence of
+    the last ``primary`` tokens whose k-token continuation ends at or before
+    L, else the same for ``backoff`` tokens, else zeros (notes/v10/spec.py:
+    36-97).  Patterns are clamped at the start of the history as the kernel
+    clamps them."""
+
+    def __init__(self, primary, backoff, k):
+        self.ns, self.k = (primary, backoff), k
+        self.hist = []
+        self.starts = {n: {} for n in set(self.ns)}
+
+    def append(self, tok):
+        h = self.hist
+        h.append(tok)
+        i = len(h) - 1
+        for n, table in self.starts.items():
+            j = i - n + 1
+            if j >= 0:
+                table.setdefault(tuple(h[j:i + 1]), []).append(j)
+
+    def draft(self, L):
+        h = self.hist
+        for n in self.ns:
+            pattern = tuple(h[max(L - n + 1 + i, 0)] for i in range(n))
+            found = self.starts[n].get(pattern)
+            if found:
+                i = bisect.bisect_left(found, L - n - self.k + 2) - 1
+                if i >= 0:
+                    j = found[i]
+                    return h[j + n:j + n + self.k]
+        return [0] * self.k
+
+
+class AcceptancePredictor:
+    """For every position of every sequence, the tokens a verify iteration
+    started there would have emitted (1 + the leading drafts equal to the
+    greedy tokens that followed), known k tokens later; the mean over the
+    last WINDOW positions predicts the next verify iteration."""
+
+    def __init__(self, batch, primary, backoff, k):
+        self.k = k
+        self.index = [NgramIndex(primary, backoff, k) for _ in range(batch)]
+        self.pending = [collections.deque() for _ in range(batch)]
+        self.recent = collections.deque(maxlen=WINDOW)
+        self.positions = self.hits = 0
+        self.total = 0
+
+    def start(self, b, prompt, first):
+        """Sequence b's prompt (history only: no verify iteration starts
+        inside it) and the first generated token (position S, the first
+        place a verify iteration can start)."""
+        for t in prompt:
+            self.index[b].append(t)
+        self.extend(b, [first])
+
+    def extend(self, b, tokens):
+        """Append generated tokens of sequence b; every new length is a
+        position whose would-be verify iteration is scored k tokens later."""
+        ix, pend = self.index[b], self.pending[b]
+        for t in tokens:
+            ix.append(t)
+            L = len(ix.hist) - 1
+            while pend and pend[0][0] + self.k <= L:
+                L0, d = pend.popleft()
+                follow = ix.hist[L0 + 1:L0 + 1 + self.k]
+                a = 0
+                while a < self.k and d[a] == follow[a]:
+                    a += 1
+                self.recent.append(a + 1)
+                self.positions += 1
+                self.hits += a > 0
+                self.total += a + 1
+            pend.append((L, ix.draft(L)))
+
+    def predicted(self):
+        """Tokens per sequence a verify iteration is expected to emit (1.0
+        until MIN_SAMPLES positions are known)."""
+        if len(self.recent) < MIN_SAMPLES:
+            return 1.0
+        return sum(self.recent) / len(self.recent)
 
 
 class SpecDecoder:
@@ -135,9 +229,12 @@ class SpecDecoder:
         self.hist.zero_()
         self.hist[:, :S].copy_(prompt_d)
         self.hist[:, S].copy_(st.ids[:B])
-        first = st.ids[:B].to("cpu", non_blocking=False).tolist()
+        first = self.engine._checked(st.ids[:B].to("cpu", non_blocking=False).tolist())
         out = [[t] for t in first]
         counts = [1] * B
+        pred = AcceptancePredictor(B, self.primary, self.backoff, self.k)
+        for b, row in enumerate(prompt.tolist()):
+            pred.start(b, row, first[b])
         yield [out[b][0] for b in range(B)]
         emitted = 1
         ring = 2 * LOOKAHEAD + 2
@@ -148,26 +245,9 @@ class SpecDecoder:
         launched = done = 0
         n_verify = n_plain = 0
         verify_tokens = 0.0
-        mean_tokens = float(T)  # optimistic start: speculate first
-        plain_run = 0
-        probe_left = 0
-        probe_gap = PROBE_EVERY
 
         def choose():
-            nonlocal plain_run, probe_left, probe_gap
-            if probe_left > 0:
-                probe_left -= 1
-                return self.k
-            if mean_tokens >= ratio * MARGIN:
-                probe_gap = PROBE_EVERY
-                return self.k
-            plain_run += 1
-            if plain_run >= probe_gap:
-                plain_run = 0
-                probe_left = PROBE_LEN - 1
-                probe_gap = min(2 * probe_gap, PROBE_MAX)
-                return self.k
-            return 0
+            return self.k if pred.predicted() >= ratio * MARGIN else 0
 
         def launch(slot):
             k = choose()
@@ -190,7 +270,7 @@ class SpecDecoder:
             k = kinds[slot]
             Tk = k + 1
             acc = h_acc[slot].tolist()
-            tok = h_tok[slot].tolist()
+            tok = self.engine._checked(h_tok[slot, :B * (k + 1)].tolist())
             gained, live = 0, 0
             for b in range(B):
                 if counts[b] >= steps:
@@ -198,13 +278,13 @@ class SpecDecoder:
                 a = acc[b]
                 new = tok[b * Tk:b * Tk + a + 1]
                 out[b].extend(new)
+                pred.extend(b, new)
                 counts[b] += len(new)
                 gained += len(new)
                 live += 1
             if k:
                 n_verify += 1
                 if live:
-                    mean_tokens = (1 - EMA) * mean_tokens + EMA * (gained / live)
                     verify_tokens += gained / live
             else:
                 n_plain += 1
@@ -225,4 +305,9 @@ class SpecDecoder:
             "mean_accept_len": (steps - 1) / max(done, 1),
             "tokens_per_verify": verify_tokens / max(n_verify, 1),
             "cost_ratio": None if self.cost_ratio is None else round(self.cost_ratio, 4),
+            # every position's would-be verify iteration (host prediction, exact
+            # for greedy decoding): first draft right, and tokens it would emit
+            "draft_hit_rate": pred.hits / max(pred.positions, 1),
+            "predicted_tokens_per_verify": pred.total / max(pred.positions, 1),
+            "positions_scored": pred.positions,
         }

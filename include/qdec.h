@@ -56,6 +56,12 @@ extern "C" {
 #define QDEC_ELAUNCH (-4)      /* hipGetLastError after the launch */
 #define QDEC_ENODEV (-5)       /* no usable HIP device */
 
+/* Greedy pick of a row whose logits are all NaN.  Invalid inputs are never
+ * silently replaced: an out-of-range token id (qdec_embed) or cache length
+ * (qdec_attn, and the merge of x_attn) makes the affected rows NaN, which
+ * reaches the argmax as this out-of-vocabulary id; the host checks for it. */
+#define QDEC_NAN_ID 2147483647
+
 /* qdec_gemm flags */
 #define QDEC_NORM_IN 1u  /* x is the residual stream; RMSNorm(x) * norm_w feeds the product */
 #define QDEC_GLU 2u      /* w holds gate tiles then up tiles; out = silu(gate) * up */
@@ -85,10 +91,19 @@ int64_t qdec_tiled_offset(int64_t n, int64_t k, int64_t K);
 int qdec_pack_tiles(const void *src, void *dst, int64_t n, int64_t k,
                     qdec_stream_t stream);
 
+/* Measurement only, no counterpart in the reference: reads `bytes` of `buf`
+ * once, in 16-byte non-temporal loads as the decode kernels stream their
+ * weights, over `blocks` workgroups; `sink` ([blocks] uint32) is written only
+ * when the data hash takes one specific value.  Timing it over a buffer well
+ * beyond the 256 MB memory-side cache gives the streaming-read ceiling the
+ * decode roofline is compared with, beside the 8 TB/s HBM peak. */
+int qdec_read_probe(const void *buf, int64_t bytes, uint32_t *sink, int32_t blocks, qdec_stream_t stream);
+
 /* ------------------------------------------------------------- embedding */
 
 /* h[m, :] = E[ids[m], :] for m < rows.  E is the tiled [vocab, hidden]
- * embedding (the same buffer feeds the tied lm_head).
+ * embedding (the same buffer feeds the tied lm_head).  An id outside
+ * [0, vocab) reads nothing and makes row m NaN (QDEC_NAN_ID below).
  * Replaces fused.embed_ssq, engine/kernels/fused.py:341-357 (the sum of
  * squares it also produced is recomputed by each NORM_IN consumer). */
 typedef struct {
@@ -111,7 +126,8 @@ struct qdec_attn_args;  /* below: the attention call a GEMM may take its x from 
  *   NORM_IN : x' = bf16(norm_w * bf16(x * rsqrt(mean(x^2) + eps))) per row
  *   GLU     : out = bf16(bf16(silu(bf16(y_gate))) * bf16(y_up)), n = #act cols
  *   RES_OUT : res = bf16(res + bf16(y))   (in place; out unused)
- *   ARGMAX  : ids_out[m] = lowest index of max_n bf16(y[m, n]);
+ *   ARGMAX  : ids_out[m] = lowest index of max_n bf16(y[m, n]) (QDEC_NAN_ID
+ *             when every logit of the row is NaN);
  *             out (optional, may be NULL) receives the bf16 logits;
  *             lens_inc (optional) gets lens_inc[m] += 1 after the pick.
  * The summation order of every output element depends only on k, ksplit and
@@ -174,6 +190,8 @@ int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes,
  *   out  = softmax(q . K^T / sqrt(D)) . V over slots 0 .. lens[b] + t,
  *          fp32 scores and accumulation, probabilities rounded to bf16
  *          before the P.V product (flash-decoding), output rounded once.
+ * A length with lens[b] < 0 or lens[b] + t_rows > cap touches no cache
+ * memory; the rows of sequence b become NaN (QDEC_NAN_ID).
  * Slots are processed in chunks of `chunk` slots keyed to absolute slot
  * numbers, one workgroup per (chunk, kv head, sequence); the last workgroup
  * of a (sequence, kv head) to finish merges the chunk partials in chunk

@@ -203,11 +203,12 @@ class Qwen3Oracle:
             self.cos, self.sin = rope_tables(cap, self.d, self.theta, self.mode)
 
     # ------------------------------------------------------------- forward
-    def forward(self, ids, lens, kc, vc):
+    def forward(self, ids, lens, kc, vc, last=None):
         """Feed ``ids`` ``[B, T]``; row ``t`` of sequence ``b`` sits at
         position ``lens[b] + t`` and sees cache slots ``0 .. lens[b] + t``.
         Writes K/V of the new slots into ``kc``/``vc`` and returns the
-        logits ``[B, T, V]`` (bf16 values in fp32 in bf16 mode)."""
+        logits ``[B, T, V]`` (bf16 values in fp32 in bf16 mode), or only
+        those of the last ``last`` rows ``[B, last, V]``."""
         mode = self.mode
         B, T = ids.shape
         lens = torch.as_tensor(lens, dtype=torch.int64).reshape(B)
@@ -238,6 +239,8 @@ class Qwen3Oracle:
             x = rms_norm(h, ly["post"], self.eps, mode)
             a = silu_mul(linear(x, ly["g"], mode), linear(x, ly["u"], mode), mode)
             h = _r(h + linear(a, ly["dn"], mode), mode)
+        if last is not None:
+            h = h[:, T - last:]
         return linear(rms_norm(h, self.norm, self.eps, mode), self.lm, mode)
 
     # ------------------------------------------------------------- drivers
@@ -276,8 +279,7 @@ class Qwen3Oracle:
         N = generated.shape[1]
         seq = torch.cat([prompt, generated[:, :-1]], dim=1)
         kc, vc = self.new_cache(B, S + N)
-        logits = self.forward(seq, [0] * B, kc, vc)
-        return logits[:, S - 1:]
+        return self.forward(seq, [0] * B, kc, vc, last=N)
 
 
 def normalized_max_err(a, b):

@@ -71,8 +71,19 @@ def run_state(engine, prompt, n):
     return torch.stack(toks, 1), torch.stack(logits, 1)
 
 
-@pytest.mark.parametrize("B,S,n,seed", [(1, 40, 10, 1), (3, 21, 8, 2), (8, 17, 5, 4)])
+# The last two cases run the batched step of config 4 (>= 17 rows): attention
+# over one whole-cache chunk per (sequence, kv head) with 8 waves and its
+# output in fragment order, the O / down projections reading fragment order,
+# the normalisation pre-passes of QKV / gate/up / lm_head, SwiGLU written in
+# fragment order, and the 8-tile lm_head + argmax.
+@pytest.mark.parametrize("B,S,n,seed", [(1, 40, 10, 1), (3, 21, 8, 2), (8, 17, 5, 4), (32, 300, 4, 31),
+                                        (20, 150, 4, 32)])
 def test_logits_and_tokens_vs_oracle(engine, oracle, B, S, n, seed):
+    if B >= 17:
+        from qdec.runtime import FRAG_ROWS, DecodeState
+        st = DecodeState(engine.model, B, S + n + 18, max_t=16)
+        assert st.chunk == st.cap and st.attn_waves == 8 and B >= FRAG_ROWS
+        del st
     prompt = prompts(B, S, seed)
     toks, logits = run_state(engine, prompt, n)
     ref = oracle.teacher_forced(prompt, toks)  # [B, n, V]
@@ -182,3 +193,42 @@ def test_speculative_equals_plain_greedy(ckpt, engine):
             if not gate and B < 16:
                 assert stats["plain_iterations"] == 0
 
+
+
+def test_invalid_inputs_raise(engine):
+    """Out-of-range prompt ids are refused on the host; an out-of-range id
+    that reaches the device makes the step emit capi.NAN_ID, which the engine
+    refuses instead of yielding."""
+    from qdec import capi
+    from qdec.runtime import DecodeState
+    with pytest.raises(ValueError):
+        list(engine.generate([[1, 151936]], 2))
+    with pytest.raises(ValueError):
+        list(engine.generate([[-1, 5]], 2))
+    st = DecodeState(engine.model, 1, 64, max_t=1)
+    st.ids.fill_(10 ** 6)
+    st.lens.fill_(5)
+    st.run_step(t_rows=1)
+    torch.cuda.synchronize()
+    assert st.ids[0].item() == capi.NAN_ID
+    with pytest.raises(capi.QdecError):
+        engine._checked(st.ids[:1].tolist())
+
+
+def test_selfcheck_detects_a_wrong_answer(engine, monkeypatch):
+    """The load-time self-check passes on this device and fails loudly when a
+    kernel's answer is wrong (simulated on the host: the O projection's
+    launch is dropped, so the residual comes back unchanged)."""
+    from qdec import capi, selfcheck
+    from qdec.runtime import DecodeState
+    st = DecodeState(engine.model, 1, 64, max_t=1)
+    selfcheck.run(st)
+    real = st.lib.gemm
+
+    def drop_o(args, stream):
+        if not (args.flags == capi.RES_OUT and args.k == engine.model.cfg.nq * engine.model.cfg.head_dim):
+            real(args, stream)
+
+    monkeypatch.setattr(st.lib, "gemm", drop_o)
+    with pytest.raises(selfcheck.SelfCheckError, match="^self-check failed .*o:"):
+        selfcheck.run(st)

@@ -1,27 +1,27 @@
-"""The full Qwen3-4B shape (36 layers) on the GPU against the oracle and
-against Transformers.
+"""The full Qwen3-4B shape (36 layers) on the GPU, scored against fp32 truth.
 
-The 2-layer engine tests pin every kernel at full widths within 2e-2 of the
-row's max |logit|. Over the real depth, bf16 results computed in different
-summation orders drift apart. Measured with this test's prompt, as the
-normalised max logit error:
+the seed-0 random-init checkpoint (the one
+bench.py measures, written once to /tmp and reused), batch 1, a 512-token
+prompt drawn as bench.py draws it, then decode steps through the engine's
+own config-2 plan (capacity 512 + 256 + 2 -> 800, 96-slot attention chunks
+merged inside the O projection, 4 attention waves).
 
-| Depth | engine vs oracle | engine vs Transformers | oracle vs Transformers |
-|---|---:|---:|---:|
-| 2 layers | 0.009 | 0.015 | 0.015 |
-| 8 layers | 0.017 | 0.024 | 0.023 |
-| 36 layers | 0.036 | 0.040 | 0.041 |
+The reference point is the oracle in fp32 (``mode="fp32"``: no bf16 rounding
+anywhere), which tests/test_oracle.py pins to Transformers fp32 within 5e-7.
+Two bf16 implementations are scored against it teacher-forced on the
+engine's tokens:
 
-So no implementation with another summation order meets 2e-2 at 36 layers,
-not even the oracle against Transformers. The full-depth checks are:
-* the engine's logits are no further from the oracle than Transformers'
-  (bf16, eager attention, the same checkpoint) are;
-* every emitted token is within the reference contract's tie margin (2.0
-  logits) of the argmax of both replays (QWEN_ENGINE_CONTRACT.md:109-118).
-  With random-init weights, logits span about +-5, so near ties are common.
+* the engine (bf16 weights and activations, its own summation order);
+* Transformers in bf16 (sdpa attention, its default), the reference's
+  correctness oracle (engine/engine.py:218-236).
 
-The checkpoint is the same seed-0 random-init one as bench.py's, written
-once to /tmp and reused when present.
+The metric is the normalised max logit error (max |a - b| / max |b| per
+row).  At this depth bf16 rounding alone moves the logits by a few percent
+of their range, whoever computes them, so the north-star bound of 2e-2 is
+not met by either implementation; the assertion is that the engine is no
+further from fp32 truth than Transformers bf16 is, with a 25% margin.
+Every emitted token must also lie within the reference judge's tie margin
+(2.0 logits, QWEN_ENGINE_CONTRACT.md:109-118) of the fp32 argmax.
 """
 
 import time
@@ -34,7 +34,7 @@ from qdec.checkpoint import ensure_checkpoint, load_tensors, qwen3_config
 
 pytestmark = pytest.mark.gpu
 
-TOL = 2e-2
+MARGIN = 1.25     # engine error may be at most this multiple of Transformers-bf16's
 TIE_MARGIN = 2.0  # logits, the reference judge's tieMarginLogits
 CKPT = "/tmp/qdec_qwen3_4b_seed0"
 
@@ -48,9 +48,11 @@ def _deficit(ref, toks):
     return ref.amax(-1) - ref.gather(-1, toks[..., None]).squeeze(-1)
 
 
-def test_full_depth_logits_and_tokens():
+@pytest.mark.timeout(900)
+def test_full_depth_config2_vs_fp32():
     if not torch.cuda.is_available():
         pytest.fail("GPU tests need a HIP device")
+    from engine import spec_k
     from engine import Engine
     from qdec.runtime import DecodeState
 
@@ -60,10 +62,11 @@ def test_full_depth_logits_and_tokens():
     ensure_checkpoint(CKPT, cfg, seed=0)
     _say(f"checkpoint ready ({time.perf_counter() - t0:.0f}s)")
     eng = Engine(CKPT)
-    B, S, n = 2, 24, 5
-    g = torch.Generator().manual_seed(21)
+    B, S, N, n = 1, 512, 256, 9
+    g = torch.Generator().manual_seed(1)  # bench.py's config-2 prompt
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
-    st = DecodeState(eng.model, B, S + n + 18, max_t=16, keep_logits=True)
+    st = DecodeState(eng.model, B, S + N + 2 * (spec_k(B) + 1), max_t=16, keep_logits=True)
+    assert st.cap == 800 and st.chunk == 96 and st.attn_waves == 4 and st._merge_in_o(1)
     st.prefill(prompt.to(eng.device))
     toks, logits = [st.ids[:B].cpu()], [st.logits[:B].float().cpu()]
     for _ in range(n - 1):
@@ -72,29 +75,31 @@ def test_full_depth_logits_and_tokens():
         logits.append(st.logits[:B].float().cpu())
     torch.cuda.synchronize()
     toks, logits = torch.stack(toks, 1), torch.stack(logits, 1)
-    _say(f"engine decoded {n} steps ({time.perf_counter() - t0:.0f}s)")
+    _say(f"engine: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
     del st, eng
     torch.cuda.empty_cache()
 
-    oracle = Qwen3Oracle(cfg, load_tensors(CKPT), mode="bf16", attn="decode")
-    ref = oracle.teacher_forced(prompt, toks)
+    tensors = load_tensors(CKPT)
+    oracle = Qwen3Oracle(cfg, tensors, mode="fp32")
+    with torch.no_grad():
+        ref = oracle.teacher_forced(prompt, toks)
     del oracle
-    _say(f"oracle replayed ({time.perf_counter() - t0:.0f}s)")
+    _say(f"fp32 oracle replayed ({time.perf_counter() - t0:.0f}s)")
 
     from transformers import AutoModelForCausalLM
-    hf = AutoModelForCausalLM.from_pretrained(CKPT, dtype=torch.bfloat16, attn_implementation="eager",
+    hf = AutoModelForCausalLM.from_pretrained(CKPT, dtype=torch.bfloat16, attn_implementation="sdpa",
                                               local_files_only=True).eval()
     with torch.no_grad():
-        hf_logits = hf(input_ids=torch.cat([prompt, toks[:, :-1]], 1)).logits[:, S - 1:].float()
-    del hf
-    _say(f"transformers replayed ({time.perf_counter() - t0:.0f}s)")
+        hf_logits = hf(input_ids=torch.cat([prompt, toks[:, :-1]], 1), logits_to_keep=n).logits.float()
+    del hf, tensors
+    _say(f"transformers bf16 replayed ({time.perf_counter() - t0:.0f}s)")
 
-    err = normalized_max_err(logits, ref).max().item()
-    spread = normalized_max_err(hf_logits, ref).max().item()
-    _say(f"normalised max err: engine vs oracle {err:.4f}, transformers vs oracle {spread:.4f}")
-    assert err <= max(TOL, spread)
-    for name, r in (("oracle", ref), ("transformers", hf_logits)):
-        d = _deficit(r, toks)
-        _say(f"emitted tokens vs {name}: {int((d > 0).sum())} of {toks.numel()} below the argmax, "
-             f"by at most {d.max().item():.4f} logits")
-        assert d.max().item() <= TIE_MARGIN
+    err = normalized_max_err(logits, ref)
+    err_hf = normalized_max_err(hf_logits, ref)
+    _say(f"normalised max err vs fp32: engine {err.max().item():.4f} (mean {err.mean().item():.4f}), "
+         f"transformers bf16 {err_hf.max().item():.4f} (mean {err_hf.mean().item():.4f})")
+    assert err.max().item() <= MARGIN * err_hf.max().item()
+    d = _deficit(ref, toks)
+    _say(f"emitted tokens vs fp32 argmax: {int((d > 0).sum())} of {toks.numel()} below it, "
+         f"by at most {d.max().item():.4f} logits")
+    assert d.max().item() <= TIE_MARGIN

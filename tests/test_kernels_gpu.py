@@ -221,22 +221,30 @@ def test_gemm_split_multi_tile_vs_oracle(lib, role, rows):
     agree(out, ref, min_exact=0.97 if flags & capi.GLU else 0.98)
 
 
-def test_lmhead_argmax_and_ties(lib):
+@pytest.mark.parametrize("rows", [1, 5, 17, 32])
+def test_lmhead_argmax_and_ties(lib, rows):
     """Greedy pick over 151936 columns: the lowest index of the max bf16
-    logit, bit-exact; logits within tolerance of the oracle; lens advance."""
+    logit, bit-exact; logits within tolerance of the oracle; lens advance.
+    Tiles per workgroup as the engine plans them (qdec.runtime: the role plan
+    at one row, LM_TILES_BATCHED from two), so rows 17 and 32 run config 4's
+    two-M-tile NORM_IN|ARGMAX path with the normalisation pre-pass."""
     from qdec import capi
-    from qdec.runtime import role_plan
+    from qdec.runtime import LM_TILES_BATCHED, role_plan
     _, waves, tiles = role_plan(V, H, "lm")
-    rows = 5
-    x = rnd(rows, H, scale=2.0, seed=21)
+    if rows > 1:
+        tiles = LM_TILES_BATCHED
+    x = rnd(rows, H, scale=2.0, seed=21 + rows)
     E = rnd(V, H, scale=0.02, seed=22)
     # plant exact ties: duplicate rows -> identical logits at two indices.
     E[100000] = E[77]
     E[150000] = E[3]
     nw = bf16(1 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(23))).to(torch.bfloat16)
-    # make rows 0/1 pick the planted duplicates: x aligned with E[77] / E[3]
+    # make rows 0/1 (and the last row) pick the planted duplicates: x aligned
+    # with E[77] / E[3]
     x[0] = (E[77].float() * 200).to(torch.bfloat16)
-    x[1] = (E[3].float() * 200).to(torch.bfloat16)
+    x[rows - 1] = (E[3].float() * 200).to(torch.bfloat16)
+    if rows > 2:
+        x[1] = x[rows - 1]
     Et = pack(lib, E.to(DEV))
     g = Gemm(lib, capi.NORM_IN | capi.ARGMAX, V, H, waves=waves, tiles=tiles)
     logits = torch.zeros(rows, V, dtype=torch.bfloat16, device=DEV)
@@ -244,9 +252,11 @@ def test_lmhead_argmax_and_ties(lib):
     lens = torch.arange(rows, dtype=torch.int32, device=DEV)
     g(x.to(DEV), Et, out=logits, norm_w=nw.to(DEV), ids=ids, lens=lens)
     lg = logits.float().cpu()
-    assert ids.cpu().tolist() == argmax_lowest(lg).tolist()
-    assert ids.cpu().tolist()[:2] == [77, 3]
-    assert lens.cpu().tolist() == [1, 2, 3, 4, 5]
+    got = ids.cpu().tolist()
+    assert got == argmax_lowest(lg).tolist()
+    assert got[0] == 77 or rows == 1
+    assert got[rows - 1] == 3 and (rows < 3 or got[1] == 3)
+    assert lens.cpu().tolist() == list(range(1, rows + 1))
     ref = linear(rms_norm(x.float(), nw.float(), 1e-6), E.float())
     agree(lg, ref)
 
@@ -259,7 +269,7 @@ def v_layout(v):
     return v.reshape(*lead, cap // 8, 8, d).transpose(-1, -2).contiguous()
 
 
-def attn_case(lib, B, T, lens, cap, chunk, seed, waves=4):
+def attn_case(lib, B, T, lens, cap, chunk, seed, waves=4, out_frag=0, valid=True):
     from qdec import capi
     g = torch.Generator().manual_seed(seed)
     W = (NQ + 2 * NKV) * D
@@ -276,32 +286,36 @@ def attn_case(lib, B, T, lens, cap, chunk, seed, waves=4):
     dcos, dsin = cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
     dl = lens_t.to(DEV)
     dk, dv = kc.to(DEV).contiguous(), v_layout(vc).to(DEV)
-    out = torch.zeros(B * T, NQ * D, dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros((B * T + 15) // 16 * 16, NQ * D, dtype=torch.bfloat16, device=DEV)
     a.qkv, a.q_norm_w, a.k_norm_w, a.cos_tab, a.sin_tab, a.lens = (dq.data_ptr(), dqn.data_ptr(), dkn.data_ptr(),
                                                                  dcos.data_ptr(), dsin.data_ptr(), dl.data_ptr())
     a.k_cache, a.v_cache, a.out = dk.data_ptr(), dv.data_ptr(), out.data_ptr()
     a.eps, a.sm_scale = 1e-6, D ** -0.5
     a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = B, T, NQ, NKV, D, cap, chunk
-    a.waves = waves
+    a.waves, a.out_frag = waves, out_frag
     pb, cb = lib.attn_workspace(a)
     part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
     cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
     a.partial, a.counters = part.data_ptr(), cnt.data_ptr()
-    assert max(lens) + T <= cap
+    assert not valid or max(lens) + T <= cap
     lib.attn(a, stream())
     torch.cuda.synchronize()
     assert int(cnt.abs().sum()) == 0
-    return dict(qkv=qkv, qn=qn, kn=kn, kc=kc, vc=vc, cos=cos, sin=sin, lens=lens, out=out.cpu(),
+    rows = frag_to_rows(out, B * T, NQ * D) if out_frag else out[:B * T]
+    return dict(qkv=qkv, qn=qn, kn=kn, kc=kc, vc=vc, cos=cos, sin=sin, lens=lens, out=rows.cpu(),
                 k_after=dk.cpu(), v_after=dv.cpu())
 
 
 @pytest.mark.parametrize("waves", [4, 8])
-@pytest.mark.parametrize("B,lens,cap,chunk", [(1, [640], 800, 128), (1, [100], 800, 128), (3, [700, 31, 257], 800, 128),
+@pytest.mark.parametrize("B,lens,cap,chunk", [(1, [640], 800, 96), (1, [767], 800, 96), (1, [640], 800, 128),
+                                               (1, [100], 800, 128), (3, [700, 31, 257], 800, 128),
                                                (2, [200, 90], 256, 256), (1, [4000], 4384, 256)])
 def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chunk, waves):
     """Attention with out_partials + an O projection reading x_attn gives the
     same bits as the attention's own merged output fed to the O projection
-    (one chunk and several; the attention's out buffer is left untouched)."""
+    (one chunk and several; the attention's out buffer is left untouched).
+    The first cases are config 2's plan: 4 waves, 96-slot chunks of an
+    800-slot cache, 512..767 cached slots."""
     from qdec import capi
     from qdec.runtime import role_plan
     g = torch.Generator().manual_seed(sum(lens) + B)
@@ -316,7 +330,7 @@ def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chun
     dl = torch.tensor(lens, dtype=torch.int32, device=DEV)
     Wo = pack(lib, rnd(H, NQ * D, scale=0.02, seed=5).to(DEV))
     res0 = rnd(B, H, scale=2.0, seed=6).to(DEV)
-    ks, waves, _ = role_plan(H, NQ * D, "o")
+    ks, o_waves, _ = role_plan(H, NQ * D, "o")
     results = []
     for partials in (0, 1):
         kc, vc = kc0.to(DEV), vc0.to(DEV)
@@ -332,7 +346,7 @@ def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chun
         lib.attn(a, stream())
         res = res0.clone()
         o = capi.GemmArgs(x=out.data_ptr(), w=Wo.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=B, n=H, k=NQ * D,
-                          flags=capi.RES_OUT, ksplit=ks, waves=waves, tiles_per_wg=1)
+                          flags=capi.RES_OUT, ksplit=ks, waves=o_waves, tiles_per_wg=1)
         if partials:
             o.x_attn = ctypes.addressof(a)
         lib.gemm(o, stream())
@@ -469,6 +483,28 @@ def attn_oracle(c, B, T):
 ])
 def test_attention_vs_oracle(lib, B, T, lens, cap, chunk, waves):
     c = attn_case(lib, B, T, lens, cap, chunk, seed=B * 100 + T * 10 + lens[0], waves=waves)
+    check_attention(c, B, T, lens)
+
+
+# Config 4's decode attention as the engine plans it (qdec.runtime attn_chunk /
+# attn_waves / FRAG_ROWS for batch 32, capacity 4096 + 256 + 2 -> 4384): one
+# whole-cache chunk per (sequence, kv head), 8 waves, output in fragment order
+# for the O projection.  Lengths 4090..4100 as at the start of config 4's
+# decode (4096 cached), plus short and boundary ones; the verify-shaped
+# T = 2 case is batch 20's plan.
+C4_LENS = [4090 + i % 11 for i in range(27)] + [0, 31, 32, 1000, 4351]
+
+
+@pytest.mark.parametrize("B,T,lens,cap", [(32, 1, C4_LENS, 4384), (20, 2, C4_LENS[:17] + [5, 64, 4382], 4384)])
+def test_attention_config4_vs_oracle(lib, B, T, lens, cap):
+    from qdec.runtime import FRAG_ROWS, attn_chunk, attn_waves
+    chunk, waves = attn_chunk(B, NKV, cap), attn_waves(B)
+    assert chunk == cap and waves == 8 and B * T >= FRAG_ROWS
+    c = attn_case(lib, B, T, lens, cap, chunk, seed=4096 + B, waves=waves, out_frag=1)
+    check_attention(c, B, T, lens)
+
+
+def check_attention(c, B, T, lens):
     ref, kc, vc = attn_oracle(c, B, T)
     agree(c["out"], ref, min_exact=0.0, tol=0.02)
     # raw V bit-exact in the cache; new K (normed, rotated) equal but for rare
@@ -572,3 +608,153 @@ def test_draft_and_accept_vs_oracle(lib, K):
             h = list(hist[b])
             na, nl = accept_ref(out_tok[b * T:(b + 1) * T], exp_dr[b * K:(b + 1) * K], h, lens[b], K, stop)
             assert nacc[b].item() == na and dl[b].item() == nl and dh[b].cpu().tolist() == h
+
+
+# ------------------------------------------------------ invalid inputs, bands
+
+def test_invalid_length_and_id_give_nan_not_stale_output(lib):
+    """A cache length outside [0, cap - t_rows] touches no cache memory and
+    makes that sequence's rows NaN (the other sequences are unaffected); an
+    out-of-range token id makes its embedding row NaN.  Both reach the
+    argmax as capi.NAN_ID."""
+    from qdec import capi
+    B, T, cap, chunk = 3, 1, 256, 64
+    good = attn_case(lib, B, T, [100, 7, 50], cap, chunk, seed=91)
+    for bad_len in (cap, -1):
+        c = attn_case(lib, B, T, [100, bad_len, 50], cap, chunk, seed=91, valid=False)
+        out = c["out"].float()
+        assert bool(torch.isnan(out[1]).all())
+        assert torch.equal(out[[0, 2]], good["out"].float()[[0, 2]])
+        assert torch.equal(c["k_after"][1], c["kc"][1]) and torch.equal(c["v_after"][1], v_layout(c["vc"])[1])
+    vocab, hid = 512, 256
+    Et = pack(lib, rnd(vocab, hid, seed=92).to(DEV))
+    ids = torch.tensor([3, vocab, -5, 0], dtype=torch.int64, device=DEV)
+    h = torch.zeros(4, hid, dtype=torch.bfloat16, device=DEV)
+    lib.embed(capi.EmbedArgs(ids=ids.data_ptr(), emb=Et.data_ptr(), h=h.data_ptr(), rows=4, hidden=hid,
+                             vocab=vocab), stream())
+    torch.cuda.synchronize()
+    hn = torch.isnan(h.float()).all(1).cpu().tolist()
+    assert hn == [False, True, True, False]
+    # an all-NaN row picks NAN_ID
+    x = torch.full((2, H), float("nan"), dtype=torch.bfloat16)
+    x[1] = rnd(H, seed=93)
+    E = pack(lib, rnd(1024, H, scale=0.02, seed=94).to(DEV))
+    g = Gemm(lib, capi.NORM_IN | capi.ARGMAX, 1024, H, waves=4, tiles=4)
+    out_ids = torch.full((2,), -1, dtype=torch.int64, device=DEV)
+    g(x.to(DEV), E, norm_w=torch.ones(H, dtype=torch.bfloat16, device=DEV), ids=out_ids)
+    assert out_ids[0].item() == capi.NAN_ID and 0 <= out_ids[1].item() < 1024
+
+
+CANARY = -12345.0  # bf16-exact
+
+
+def banded(n_elems, dtype=torch.bfloat16, pad=4096, fill=CANARY):
+    """A buffer with canary bands of `pad` elements on both sides of an
+    n_elems-element window; returns (whole, window)."""
+    whole = torch.full((pad + n_elems + pad,), fill, dtype=dtype, device=DEV)
+    return whole, whole[pad:pad + n_elems]
+
+
+def bands_intact(whole, n_elems, pad=4096, fill=CANARY):
+    w = whole.cpu()
+    return bool((w[:pad] == fill).all()) and bool((w[pad + n_elems:] == fill).all())
+
+
+@pytest.mark.parametrize("rows", [1, 5, 17, 40])
+def test_gemm_epilogues_stay_in_bounds(lib, rows):
+    """GEMM outputs (row-major and fragment order with its padding rows),
+    residuals, argmax ids and the argmax / pre-pass workspace written into
+    the middle of larger buffers: nothing outside the window changes."""
+    from qdec import capi
+    from qdec.runtime import LM_TILES_BATCHED, role_plan
+    pg, pd = role_plan(I, H, "gate_up"), role_plan(H, I, "down")
+    x = rnd(rows, H, scale=3.0, seed=61).to(DEV)
+    Wgu = pack(lib, rnd(2 * I, H, scale=0.02, seed=62).to(DEV))
+    Wd = pack(lib, rnd(H, I, scale=0.02, seed=63).to(DEV))
+    nw = rnd(H, scale=0.2, seed=64).to(DEV)
+    frag = 1 if rows >= 17 else 0
+    act_elems = ((rows + 15) // 16 * 16 if frag else rows) * I
+    act_whole, act = banded(act_elems)
+    a = capi.GemmArgs(x=x.data_ptr(), w=Wgu.data_ptr(), out=act.data_ptr(), norm_w=nw.data_ptr(), eps=1e-6,
+                      rows=rows, n=I, k=H, flags=capi.NORM_IN | capi.GLU, ksplit=pg[0], waves=pg[1],
+                      tiles_per_wg=1, out_frag=frag)
+    pb, cb = lib.gemm_workspace(a)
+    ws_whole, ws = banded(max(pb, 4) // 4, dtype=torch.float32)
+    cnt_whole, cnt = banded(max(cb, 4) // 4, dtype=torch.int32, fill=0)
+    a.partial, a.counters = ws.data_ptr(), cnt.data_ptr()
+    lib.gemm(a, stream())
+    res_whole, res = banded(rows * H)
+    res.copy_(rnd(rows * H, scale=2.0, seed=65).to(DEV))
+    d = capi.GemmArgs(x=act.data_ptr(), w=Wd.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=rows, n=H, k=I,
+                      flags=capi.RES_OUT, ksplit=pd[0], waves=pd[1], tiles_per_wg=1, x_frag=frag,
+                      partial=ws.data_ptr(), counters=cnt.data_ptr())
+    assert lib.gemm_workspace(d)[0] <= max(pb, 4)
+    lib.gemm(d, stream())
+    # lm_head + argmax (argmax partials and, from 9 rows, the normalised rows in the workspace)
+    Vs = 4096
+    E = pack(lib, rnd(Vs, H, scale=0.02, seed=66).to(DEV))
+    ids_whole, ids = banded(rows, dtype=torch.int64, fill=-7)
+    lm = capi.GemmArgs(x=x.data_ptr(), w=E.data_ptr(), norm_w=nw.data_ptr(), ids_out=ids.data_ptr(), eps=1e-6,
+                       rows=rows, n=Vs, k=H, flags=capi.NORM_IN | capi.ARGMAX, ksplit=1, waves=4,
+                       tiles_per_wg=LM_TILES_BATCHED if rows > 1 else 4)
+    lpb, lcb = lib.gemm_workspace(lm)
+    lws_whole, lws = banded(max(lpb, 4) // 4, dtype=torch.float32)
+    lcnt_whole, lcnt = banded(max(lcb, 4) // 4, dtype=torch.int32, fill=0)
+    lm.partial, lm.counters = lws.data_ptr(), lcnt.data_ptr()
+    lib.gemm(lm, stream())
+    torch.cuda.synchronize()
+    assert bands_intact(act_whole, act_elems), "SwiGLU output"
+    assert bands_intact(res_whole, rows * H), "down residual"
+    assert bands_intact(ws_whole, max(pb, 4) // 4), "GEMM workspace"
+    assert bands_intact(cnt_whole, max(cb, 4) // 4, fill=0) and int(cnt.abs().sum()) == 0, "counters"
+    assert bands_intact(ids_whole, rows, fill=-7) and bool((ids >= 0).all()), "argmax ids"
+    assert bands_intact(lws_whole, max(lpb, 4) // 4), "argmax workspace"
+    assert bands_intact(lcnt_whole, max(lcb, 4) // 4, fill=0), "argmax counters"
+
+
+@pytest.mark.parametrize("B,T,lens,cap,chunk,waves,frag,partials", [
+    (1, 1, [640], 800, 96, 4, 0, 1), (3, 1, [700, 31, 257], 800, 128, 4, 0, 0),
+    (20, 1, [100 + 37 * i for i in range(20)], 896, 896, 8, 1, 0), (4, 4, [60, 0, 7, 100], 128, 64, 4, 0, 0)])
+def test_attention_stays_in_bounds(lib, B, T, lens, cap, chunk, waves, frag, partials):
+    """Attention output (row-major or fragment order), chunk partials and
+    counters written into the middle of larger buffers: the bands and every
+    cache slot outside the new ones stay untouched."""
+    from qdec import capi
+    g = torch.Generator().manual_seed(cap + B)
+    W = (NQ + 2 * NKV) * D
+    qkv = (torch.randn(B * T, W, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    qn = rnd(D, scale=0.2, seed=71).to(DEV)
+    kn = rnd(D, scale=0.2, seed=72).to(DEV)
+    kc_whole, kc = banded(B * NKV * cap * D)
+    vc_whole, vc = banded(B * NKV * cap * D)
+    kc.copy_(torch.randn(kc.numel(), generator=g).to(torch.bfloat16).to(DEV))
+    vc.copy_(torch.randn(vc.numel(), generator=g).to(torch.bfloat16).to(DEV))
+    kc0, vc0 = kc.clone(), vc.clone()
+    cos, sin = rope_tables(cap, D, 5e6, "bf16")
+    dcos, dsin = cos.to(torch.bfloat16).to(DEV), sin.to(torch.bfloat16).to(DEV)
+    dl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    rows = B * T
+    out_elems = ((rows + 15) // 16 * 16 if frag else rows) * NQ * D
+    out_whole, out = banded(out_elems)
+    a = capi.AttnArgs(qkv=qkv.data_ptr(), q_norm_w=qn.data_ptr(), k_norm_w=kn.data_ptr(), cos_tab=dcos.data_ptr(),
+                      sin_tab=dsin.data_ptr(), lens=dl.data_ptr(), k_cache=kc.data_ptr(), v_cache=vc.data_ptr(),
+                      out=out.data_ptr(), eps=1e-6, sm_scale=D ** -0.5, batch=B, t_rows=T, nq=NQ, nkv=NKV,
+                      head_dim=D, cap=cap, chunk=chunk, waves=waves, out_partials=partials, out_frag=frag)
+    pb, cb = lib.attn_workspace(a)
+    pw_whole, pw = banded(max(pb, 4) // 4, dtype=torch.float32)
+    cw_whole, cw = banded(max(cb, 4) // 4, dtype=torch.int32, fill=0)
+    a.partial, a.counters = pw.data_ptr(), cw.data_ptr()
+    lib.attn(a, stream())
+    torch.cuda.synchronize()
+    assert bands_intact(out_whole, out_elems), "attention output"
+    assert bands_intact(pw_whole, max(pb, 4) // 4), "chunk partials"
+    assert bands_intact(cw_whole, max(cb, 4) // 4, fill=0) and int(cw.abs().sum()) == 0, "counters"
+    assert bands_intact(kc_whole, kc.numel()) and bands_intact(vc_whole, vc.numel()), "cache slabs"
+    new = torch.zeros(B, NKV, cap, dtype=torch.bool)
+    for b, L in enumerate(lens):
+        new[b, :, L:L + T] = True
+    k_after = kc.view(B, NKV, cap, D).cpu()
+    assert torch.equal(k_after[~new], kc0.view(B, NKV, cap, D).cpu()[~new])
+    v_rows_after = vc.view(B, NKV, cap // 8, D, 8).transpose(-1, -2).reshape(B, NKV, cap, D).cpu()
+    v_rows_before = vc0.view(B, NKV, cap // 8, D, 8).transpose(-1, -2).reshape(B, NKV, cap, D).cpu()
+    assert torch.equal(v_rows_after[~new], v_rows_before[~new])
