@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "qdec_common.h"
 #include "qdec_kernels.h"
@@ -244,6 +245,55 @@ fill:
   return QDEC_OK;
 }
 
+// ------------------------------------------- attention without a workspace
+// qdec_attn_noalloc runs qdec_attn with its arrival counters and chunk
+// partials in this library-owned device array instead of caller buffers.
+// Every GPU holds its own copy until the process ends; its device address is
+// taken once per device with hipGetSymbolAddress and only that address is
+// used from the host (the array's name is a host-side stand-in).  Calls on
+// one GPU share it, so two such calls must not overlap (same stream, or
+// ordered streams); every kernel leaves the counters at zero again.
+static __device__ __align__(256) unsigned char scratch[QDEC_NOALLOC_COUNTER_BYTES + QDEC_NOALLOC_PARTIAL_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_ptr[kMaxDevices];
+
+__global__ void clear_kernel(uint4 *p, int n16) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += gridDim.x * blockDim.x) p[i] = zero4();
+}
+
+// Device address of `scratch` on the current device; the first call on a
+// device takes it and clears the counter region with a kernel on `s` (a
+// kernel, not a memset, so a first call under hipGraph capture records a
+// node that is safe to replay).
+int scratch_on_current_device(hipStream_t s, unsigned char **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return set_error(QDEC_ENODEV, "qdec_attn_noalloc: no current HIP device (or id >= %d)", kMaxDevices);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(QDEC_ELAUNCH, "qdec_attn_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                       hipGetErrorString(e));
+    hipLaunchKernelGGL(clear_kernel, dim3(16), dim3(256), 0, s, reinterpret_cast<uint4 *>(ptr),
+                       (int)(QDEC_NOALLOC_COUNTER_BYTES / 16));
+    const int rc = check_launch("qdec_attn_noalloc: clearing the scratch counters");
+    if (rc != QDEC_OK) return rc;
+    g_scratch_ptr[dev] = reinterpret_cast<unsigned char *>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return QDEC_OK;
+}
+
+}  // namespace
+
 }  // namespace qdec
 
 using namespace qdec;
@@ -332,6 +382,29 @@ int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream) {
   const int rc = plan_attn(a, &p, true);
   if (rc != QDEC_OK) return rc;
   return launch_status(launch_attn(p, (hipStream_t)stream), "qdec_attn");
+}
+
+int qdec_attn_noalloc(const qdec_attn_args *a, qdec_stream_t stream) {
+  if (!a) return set_error(QDEC_EINVAL, "qdec_attn_noalloc: null args");
+  if (a->out_partials)
+    return set_error(QDEC_EUNSUPPORTED,
+                     "qdec_attn_noalloc: out_partials leaves the partials for a later qdec_gemm; "
+                     "use qdec_attn with a caller workspace");
+  size_t pb = 0, cb = 0;
+  const int rc = qdec_attn_workspace(a, &pb, &cb);
+  if (rc != QDEC_OK) return rc;
+  if (pb > QDEC_NOALLOC_PARTIAL_BYTES || cb > QDEC_NOALLOC_COUNTER_BYTES)
+    return set_error(QDEC_EINVAL,
+                     "qdec_attn_noalloc: this call needs %zu B of chunk partials and %zu B of counters; the "
+                     "library scratch holds %u and %u (use qdec_attn with a caller workspace)",
+                     pb, cb, (unsigned)QDEC_NOALLOC_PARTIAL_BYTES, (unsigned)QDEC_NOALLOC_COUNTER_BYTES);
+  unsigned char *base = nullptr;
+  const int rs = scratch_on_current_device((hipStream_t)stream, &base);
+  if (rs != QDEC_OK) return rs;
+  qdec_attn_args b = *a;
+  b.counters = reinterpret_cast<uint32_t *>(base);
+  b.partial = reinterpret_cast<float *>(base + QDEC_NOALLOC_COUNTER_BYTES);
+  return qdec_attn(&b, stream);
 }
 
 int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream) {

@@ -18,6 +18,9 @@ NORM_IN, GLU, RES_OUT, ARGMAX = 1, 2, 4, 8
 # Greedy pick of a row whose logits are all NaN (QDEC_NAN_ID): the kernels turn
 # an out-of-range token id or cache length into NaN rows instead of guessing.
 NAN_ID = 2147483647
+# Library-owned scratch of qdec_attn_noalloc (QDEC_NOALLOC_*_BYTES).
+NOALLOC_PARTIAL_BYTES = 8 << 20
+NOALLOC_COUNTER_BYTES = 64 << 10
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
@@ -111,6 +114,7 @@ class Lib:
         so.qdec_read_probe.argtypes = [P, ctypes.c_int64, P, I32, P]
         so.qdec_read_probe.restype = ctypes.c_int
         for name, st in (("qdec_embed", EmbedArgs), ("qdec_gemm", GemmArgs), ("qdec_attn", AttnArgs),
+                         ("qdec_attn_noalloc", AttnArgs),
                          ("qdec_ngram_draft", DraftArgs), ("qdec_spec_accept", AcceptArgs),
                          ("qdec_rownorm", RownormArgs), ("qdec_prefill_gemm", PgemmArgs),
                          ("qdec_prefill_qk", PrefillQkArgs), ("qdec_prefill_attn", PrefillAttnArgs)):
@@ -153,6 +157,9 @@ class Lib:
 
     def attn(self, args, stream):
         self._check("qdec_attn", self.so.qdec_attn(ctypes.byref(args), stream))
+
+    def attn_noalloc(self, args, stream):
+        self._check("qdec_attn_noalloc", self.so.qdec_attn_noalloc(ctypes.byref(args), stream))
 
     def ngram_draft(self, args, stream):
         self._check("qdec_ngram_draft", self.so.qdec_ngram_draft(ctypes.byref(args), stream))

@@ -237,6 +237,19 @@ int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream);
 int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,
                         size_t *counter_bytes);
 
+/* qdec_attn with no workspace arguments: a->partial and a->counters are
+ * ignored; the chunk partials and arrival counters live in a device array
+ * the library owns (QDEC_NOALLOC_PARTIAL_BYTES + QDEC_NOALLOC_COUNTER_BYTES
+ * per GPU, held until the process ends).  Nothing is allocated or freed.
+ * A call whose qdec_attn_workspace exceeds either size, or that asks for
+ * out_partials, fails with an error.  All calls on one GPU share the array:
+ * calls that overlap in time on one GPU race.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under hipGraph
+ * capture, serving loops or harnesses that forbid hipMalloc). */
+#define QDEC_NOALLOC_PARTIAL_BYTES (8u << 20)
+#define QDEC_NOALLOC_COUNTER_BYTES (64u << 10)
+int qdec_attn_noalloc(const qdec_attn_args *a, qdec_stream_t stream);
+
 /* ------------------------------------------------ n-gram speculation */
 
 /* Suffix-match drafter over each sequence's own history hist[b, 0..lens[b]]

@@ -1,0 +1,96 @@
+"""qdec_attn_noalloc (library-owned scratch) against qdec_attn (caller
+workspace), through the C ABI: the same output and cache bits on two calls
+in a row, the second smaller, and a clear error for calls the scratch cannot
+hold."""
+
+import pytest
+import torch
+
+from qdec import capi
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+NQ, NKV, D = 32, 8, 128
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _case(B, T, lens, cap, chunk, waves, seed):
+    """Inputs of one attention call (device tensors) and its argument block."""
+    g = torch.Generator().manual_seed(seed)
+    W = (NQ + 2 * NKV) * D
+    t = dict(
+        qkv=(torch.randn(B * T, W, generator=g) * 2).to(torch.bfloat16),
+        qn=(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16),
+        kn=(1 + 0.2 * torch.randn(D, generator=g)).to(torch.bfloat16),
+        kc=torch.randn(B, NKV, cap, D, generator=g).to(torch.bfloat16),
+        vc=torch.randn(B, NKV, cap, D, generator=g).to(torch.bfloat16),
+    )
+    pos = torch.arange(cap, dtype=torch.float32)[:, None]
+    inv = 1.0 / (5e6 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = torch.cat([pos * inv, pos * inv], 1)
+    t["cos"], t["sin"] = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    t["lens"] = torch.tensor(lens, dtype=torch.int32)
+    t = {k: v.to(DEV) for k, v in t.items()}
+    a = capi.AttnArgs(eps=1e-6, sm_scale=D ** -0.5, batch=B, t_rows=T, nq=NQ, nkv=NKV, head_dim=D, cap=cap,
+                      chunk=chunk, waves=waves, out_partials=0, out_frag=0)
+    return t, a
+
+
+def _run(lib, t, a, noalloc):
+    """One call on fresh copies of the caches; returns (out, k cache, v cache)."""
+    kc, vc = t["kc"].clone(), t["vc"].clone()
+    out = torch.full((a.batch * a.t_rows, NQ * D), 3.0, dtype=torch.bfloat16, device=DEV)
+    a.qkv, a.q_norm_w, a.k_norm_w = t["qkv"].data_ptr(), t["qn"].data_ptr(), t["kn"].data_ptr()
+    a.cos_tab, a.sin_tab, a.lens = t["cos"].data_ptr(), t["sin"].data_ptr(), t["lens"].data_ptr()
+    a.k_cache, a.v_cache, a.out = kc.data_ptr(), vc.data_ptr(), out.data_ptr()
+    if noalloc:
+        a.partial, a.counters = None, None
+        lib.attn_noalloc(a, _stream())
+        torch.cuda.synchronize()
+        return out.cpu(), kc.cpu(), vc.cpu(), None
+    pb, cb = lib.attn_workspace(a)
+    part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
+    cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
+    a.partial, a.counters = part.data_ptr(), cnt.data_ptr()
+    lib.attn(a, _stream())
+    torch.cuda.synchronize()
+    return out.cpu(), kc.cpu(), vc.cpu(), cnt.cpu()
+
+
+def test_noalloc_attention_matches_workspace_attention():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    lib = capi.lib()
+    # first call: batch 4 at config 5's scale, 11 chunks, merged across
+    # workgroups through the arrival counters; second call smaller (fewer
+    # sequences, shorter cache, 2 rows per sequence, 8 waves).
+    for B, T, lens, cap, chunk, waves in ((4, 1, [1000, 1017, 31, 64], 1056, 96, 4),
+                                          (2, 2, [100, 7], 256, 64, 8)):
+        t, a = _case(B, T, lens, cap, chunk, waves, seed=B * 10 + T)
+        pb, cb = lib.attn_workspace(a)
+        assert 0 < pb <= capi.NOALLOC_PARTIAL_BYTES and 0 < cb <= capi.NOALLOC_COUNTER_BYTES
+        ref_out, ref_k, ref_v, cnt = _run(lib, t, a, noalloc=False)
+        assert int(cnt.abs().sum()) == 0
+        out, k, v, _ = _run(lib, t, a, noalloc=True)
+        print(f"B={B} T={T} cap={cap} chunk={chunk}: partials {pb} B, counters {cb} B", flush=True)
+        assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+        assert torch.equal(k.view(torch.int16), ref_k.view(torch.int16))
+        assert torch.equal(v.view(torch.int16), ref_v.view(torch.int16))
+        assert not bool((out == 3.0).all(dim=1).any()), "a row was left unwritten"
+
+
+def test_noalloc_attention_rejects_what_it_cannot_hold():
+    lib = capi.lib()
+    # 64 sequences x 4096 chunks of 32 slots: far more partials than the scratch
+    a = capi.AttnArgs(eps=1e-6, sm_scale=D ** -0.5, batch=64, t_rows=1, nq=NQ, nkv=NKV, head_dim=D, cap=131072,
+                      chunk=32, waves=4)
+    with pytest.raises(capi.QdecError, match="library scratch"):
+        lib.attn_noalloc(a, None)
+    a = capi.AttnArgs(eps=1e-6, sm_scale=D ** -0.5, batch=1, t_rows=1, nq=NQ, nkv=NKV, head_dim=D, cap=256,
+                      chunk=64, waves=4, out_partials=1)
+    with pytest.raises(capi.QdecError, match="out_partials"):
+        lib.attn_noalloc(a, None)
