@@ -46,7 +46,7 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
   if (a->flags & QDEC_ARGMAX) {
     pb = 2 * sizeof(float) * (size_t)(ntiles / a->tiles_per_wg) * a->rows;
     cb = sizeof(uint32_t);
-  } else if (a->ksplit > 1) {
+  } else if (a->ksplit > 1 && !a->parts_out) {
     pb = sizeof(float) * (size_t)a->ksplit * a->rows * a->n * ((a->flags & QDEC_GLU) ? 2 : 1);
     cb = sizeof(uint32_t) * (size_t)ntiles;
   }
@@ -84,8 +84,19 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     return set_error(QDEC_EINVAL, "qdec_gemm: x_frag %d / out_frag %d not 0 or 1", a->x_frag, a->out_frag);
   if (a->out_frag && (f & (QDEC_RES_OUT | QDEC_ARGMAX)))
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: out_frag with RES_OUT or ARGMAX");
-  if (a->x_frag && ((f & QDEC_NORM_IN) || a->x_attn || a->ksplit != 1))
-    return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_frag needs no NORM_IN, no x_attn and ksplit 1");
+  if (a->x_frag && ((f & QDEC_NORM_IN) || a->x_attn))
+    return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_frag needs no NORM_IN and no x_attn");
+  if (a->parts_out && (f != QDEC_RES_OUT || a->ksplit < 2))
+    return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: parts_out needs RES_OUT alone and ksplit > 1");
+  if (a->x_parts) {
+    if (!(f & QDEC_NORM_IN) || (f & QDEC_GLU) || a->ksplit != 1 || a->x_attn)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_parts needs NORM_IN without GLU, ksplit 1 and no x_attn");
+    if (a->x_nparts < 1 || a->x_nparts > 8) return set_error(QDEC_EINVAL, "qdec_gemm: x_nparts %d not in [1, 8]", a->x_nparts);
+    if (need_scratch && (!a->x_merged || a->x_merged == a->x))
+      return set_error(QDEC_EINVAL, "qdec_gemm: x_parts needs x_merged, a buffer other than x");
+    if ((reinterpret_cast<uintptr_t>(a->x_parts) & 15u) || (a->x_merged && !aligned16(a->x_merged)))
+      return set_error(QDEC_EALIGN, "qdec_gemm: x_parts and x_merged must be 16-byte aligned");
+  }
   const qdec_attn_args *xa = a->x_attn;
   if (xa) {
     if (f & QDEC_NORM_IN) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_attn with NORM_IN");
@@ -103,8 +114,8 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   if (need_scratch && !(f & (QDEC_RES_OUT | QDEC_ARGMAX)) && !a->out) return set_error(QDEC_EINVAL, "qdec_gemm: null out");
   if (need_scratch && arg && (!a->ids_out || !a->partial || !a->counters))
     return set_error(QDEC_EINVAL, "qdec_gemm: ARGMAX needs ids_out, partial and counters");
-  if (need_scratch && a->ksplit > 1 && (!a->partial || !a->counters))
-    return set_error(QDEC_EINVAL, "qdec_gemm: ksplit > 1 needs partial and counters");
+  if (need_scratch && a->ksplit > 1 && !a->parts_out && (!a->partial || !a->counters))
+    return set_error(QDEC_EINVAL, "qdec_gemm: ksplit > 1 needs partial and counters (or parts_out)");
   if (!aligned16(a->x) || !aligned16(a->w) || (a->out && !aligned16(a->out)) || (a->res && !aligned16(a->res)) ||
       (a->norm_w && !aligned16(a->norm_w)))
     return set_error(QDEC_EALIGN, "qdec_gemm: x, w, out, res and norm_w must be 16-byte aligned");
@@ -177,6 +188,25 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
       p->xt = mt;
       p->xpre = 1;
     }
+  }
+  // A pending split residual update is merged by the register-staged
+  // prologue at one row, else by the normalisation pre-pass (once per row;
+  // per workgroup it would re-read every partial for every row).
+  p->parts_out = a->parts_out;
+  p->xparts = a->x_parts;
+  p->xnparts = a->x_parts ? a->x_nparts : 0;
+  p->xmerged = reinterpret_cast<uint16_t *>(a->x_merged);
+  if (a->x_parts && !(a->rows == 1 && p->xfast && p->rw > 0 && a->x_nparts <= 4)) {
+    if (!ring_d || (a->tiles_per_wg != 1 && p->ksw % ring_d))
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_parts at %d rows needs the direct path, which this tile "
+                       "grouping does not allow", a->rows);
+    p->rw = ring_d;
+    p->xd = 1;
+    p->xfast = 0;
+    p->lds_all = 0;
+    p->lds_bytes = head + red_bytes;
+    p->xt = mt;
+    p->xpre = 1;
   }
   p->amerge = 0;
   p->apart = nullptr;

@@ -150,7 +150,34 @@ __device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk)
   return v;
 }
 
-template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows>
+// Residual vector (8 consecutive elements from k index kk) of row m with a
+// pending split update applied: bf16(x + bf16(((p0 + p1) + p2) + ...)), the
+// rounding of the RES_OUT epilogue, over the partials a split producer left
+// in p.xparts ([j][rows][k] fp32).
+__device__ __forceinline__ uint4 merge_res8(const float *__restrict__ parts, int nparts, int rows, int k, uint4 xv,
+                                            int m, int kk) {
+  const float *q = parts + (size_t)m * k + kk;
+  const size_t stride = (size_t)rows * k;
+  f32x4_t s0 = *reinterpret_cast<const f32x4_t *>(q), s1 = *reinterpret_cast<const f32x4_t *>(q + 4);
+  for (int j = 1; j < nparts; ++j) {
+    s0 += *reinterpret_cast<const f32x4_t *>(q + j * stride);
+    s1 += *reinterpret_cast<const f32x4_t *>(q + j * stride + 4);
+  }
+  uint4 o;
+  o.x = pack2(lo16(xv.x) + rbf(s0[0]), hi16(xv.x) + rbf(s0[1]));
+  o.y = pack2(lo16(xv.y) + rbf(s0[2]), hi16(xv.y) + rbf(s0[3]));
+  o.z = pack2(lo16(xv.z) + rbf(s1[0]), hi16(xv.z) + rbf(s1[1]));
+  o.w = pack2(lo16(xv.w) + rbf(s1[2]), hi16(xv.w) + rbf(s1[3]));
+  return o;
+}
+
+// Pending split residual updates merged from registers (one row): at most
+// this many partials (the down projection leaves four).
+constexpr int kMergeParts = 4;
+
+// XP: the instantiation that merges a pending split residual update into its
+// one register-staged row (FR = 1); 0 elsewhere.
+template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows, bool XP = false>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr bool NORM = (FLAGS & QDEC_NORM_IN) != 0;
@@ -293,7 +320,51 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
           xr[m][j] = ok ? v : zero4();
         }
       }
+    // XP: the raw partials of the pending residual update are loaded with x,
+    // before the weights, and merged after the weights went out (loads
+    // complete in issue order: merging first would hold the weights back).
+    f32x4_t xp[XP ? kFastVec : 1][XP ? kMergeParts : 1][2];
+    if constexpr (XP) {
+      static_assert(FR == 1 && NORM && !GLU, "one row, NORM_IN without GLU");
+#pragma unroll
+      for (int j = 0; j < kFastVec; ++j) {
+        const int vr = tid + j * nthr;
+        const float *q = p.xparts + ks_wg * 32 + 8 * (vr < per_row ? vr : 0);
+#pragma unroll
+        for (int part = 0; part < kMergeParts; ++part) {
+          const bool live = vr < per_row && part < p.xnparts;
+          const float *qp = q + (size_t)(live ? part : 0) * p.k;  // rows == 1: part stride is k
+          xp[j][part][0] = *reinterpret_cast<const f32x4_t *>(qp);
+          xp[j][part][1] = *reinterpret_cast<const f32x4_t *>(qp + 4);
+        }
+      }
+    }
     issue_first();
+    if constexpr (XP) {
+      // bf16(x + bf16(((p0 + p1) + p2) + p3)): merge_res8's order and rounding.
+#pragma unroll
+      for (int j = 0; j < kFastVec; ++j) {
+        const int vr = tid + j * nthr;
+        if (vr < per_row) {
+          f32x4_t s0 = xp[j][0][0], s1 = xp[j][0][1];
+#pragma unroll
+          for (int part = 1; part < kMergeParts; ++part)
+            if (part < p.xnparts) {
+              s0 += xp[j][part][0];
+              s1 += xp[j][part][1];
+            }
+          const uint4 xv = xr[0][j];
+          uint4 o;
+          o.x = pack2(lo16(xv.x) + rbf(s0[0]), hi16(xv.x) + rbf(s0[1]));
+          o.y = pack2(lo16(xv.y) + rbf(s0[2]), hi16(xv.y) + rbf(s0[3]));
+          o.z = pack2(lo16(xv.z) + rbf(s1[0]), hi16(xv.z) + rbf(s1[1]));
+          o.w = pack2(lo16(xv.w) + rbf(s1[2]), hi16(xv.w) + rbf(s1[3]));
+          xr[0][j] = o;
+          // the first workgroup (its range is the whole row: ksplit 1) keeps it
+          if (blk == 0) *reinterpret_cast<uint4 *>(p.xmerged + ks_wg * 32 + 8 * vr) = o;
+        }
+      }
+    }
     if constexpr (NORM) {
       float ss[8];
 #pragma unroll
@@ -530,6 +601,18 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       return p.ofrag ? o + frag_off(m, n, p.ofrag) : o + (size_t)m * p.n + n;
     };
 
+    // ---- k split left to the next NORM_IN call: raw partials, no epilogue.
+    if (RES && p.parts_out) {
+      if (wave == 0) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = mt * 16 + col;
+          if (m < rows)
+            *reinterpret_cast<f32x4_t *>(p.parts_out + ((size_t)split * rows + m) * p.n + n0) = acc[0][mt];
+        }
+      }
+      continue;
+    }
     // ---- k split across workgroups: partials, last arrival sums them.
     if (p.ksplit > 1) {
       if (wave == 0) {
@@ -682,7 +765,8 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 // bit-identical whichever path stages it.
 __global__ void __launch_bounds__(512) rownorm_kernel(const uint16_t *__restrict__ X, const uint16_t *__restrict__ norm_w,
                                                        uint16_t *__restrict__ xn, int k, float eps, int rows, int nmt,
-                                                       int do_norm) {
+                                                       int do_norm, const float *__restrict__ parts, int nparts,
+                                                       uint16_t *__restrict__ xmerged) {
   __shared__ float s_red[8 * 8];
   __shared__ float s_rstd[8];
   const int m = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x;
@@ -698,6 +782,15 @@ __global__ void __launch_bounds__(512) rownorm_kernel(const uint16_t *__restrict
     return;
   }
   const uint16_t *xrow = X + (size_t)m * k;
+  if (parts) {
+    // Apply the pending split residual update once, into xmerged; both
+    // loops below then read the merged row (each thread its own vectors).
+    uint16_t *mrow = xmerged + (size_t)m * k;
+    for (int v = tid; v < nvec; v += nthr)
+      *reinterpret_cast<uint4 *>(mrow + 8 * v) =
+          merge_res8(parts, nparts, rows, k, *reinterpret_cast<const uint4 *>(xrow + 8 * v), m, 8 * v);
+    xrow = mrow;
+  }
   if (!do_norm) {  // re-layout only
     for (int v = tid; v < nvec; v += nthr) *reinterpret_cast<uint4 *>(dst(v)) = *reinterpret_cast<const uint4 *>(xrow + 8 * v);
     return;
@@ -812,7 +905,8 @@ int gemm_ring_direct(int mt, uint32_t flags) {
 hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStream_t s) {
   const int nrow = p.xt ? p.xt * 16 : p.rows;
   hipLaunchKernelGGL(rownorm_kernel, dim3(nrow), block, 0, s, reinterpret_cast<const uint16_t *>(p.x),
-                     reinterpret_cast<const uint16_t *>(p.norm_w), p.xn, p.k, p.eps, p.rows, p.xt, do_norm ? 1 : 0);
+                     reinterpret_cast<const uint16_t *>(p.norm_w), p.xn, p.k, p.eps, p.rows, p.xt, do_norm ? 1 : 0,
+                     p.xparts, p.xnparts, p.xmerged);
   return hipSuccess;
 }
 
@@ -820,7 +914,7 @@ hipError_t launch_rownorm_rows(const void *x, const void *norm_w, void *out, flo
                                int tiles, hipStream_t s) {
   hipLaunchKernelGGL(rownorm_kernel, dim3(tiles * 16), dim3(256), 0, s, reinterpret_cast<const uint16_t *>(x),
                      reinterpret_cast<const uint16_t *>(norm_w), reinterpret_cast<uint16_t *>(out), k, eps, rows,
-                     tiles, norm_w ? 1 : 0);
+                     tiles, norm_w ? 1 : 0, nullptr, 0, nullptr);
   return hipSuccess;
 }
 
@@ -847,6 +941,20 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   }
   if (p.rw > 0) {
     if (mt != 1) return hipErrorInvalidValue;
+    if (p.xfast && p.xparts) {  // one row merging a pending split residual update
+      if (p.rows != 1 || p.xnparts > kMergeParts) return hipErrorInvalidValue;
+      if (flags == QDEC_NORM_IN && p.rw == 20)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN, 20, false, 1, true>), grid, block, lds, s, p);
+      else if (flags == QDEC_NORM_IN && p.rw == 16)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN, 16, false, 1, true>), grid, block, lds, s, p);
+      else if (flags == (QDEC_NORM_IN | QDEC_ARGMAX) && p.rw == 20)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_ARGMAX, 20, false, 1, true>), grid, block, lds, s, p);
+      else if (flags == (QDEC_NORM_IN | QDEC_ARGMAX) && p.rw == 16)
+        hipLaunchKernelGGL((gemm_kernel<1, QDEC_NORM_IN | QDEC_ARGMAX, 16, false, 1, true>), grid, block, lds, s, p);
+      else
+        return hipErrorInvalidValue;
+      return hipSuccess;
+    }
     if (p.xfast && p.rows > kFastRows) {  // 5..8 rows under NORM_IN (no GLU) from registers
       constexpr int R8 = kFastRowsNorm;
       if (flags == QDEC_NORM_IN && p.rw == 20)

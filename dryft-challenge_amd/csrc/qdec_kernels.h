@@ -54,6 +54,13 @@ struct GemmParams {
   const float *apart;
   const int32_t *alens;
   int a_t_rows, a_nkv, a_chunk, a_nchunks, a_cap;
+  // Split residual updates: a RES_OUT producer writes its k-split partials
+  // (parts_out); a NORM_IN consumer merges xnparts of them into x first
+  // (xparts) and writes the merged residual rows to xmerged.
+  float *parts_out;
+  const float *xparts;
+  int xnparts;
+  uint16_t *xmerged;
   size_t lds_bytes;
 };
 bool gemm_flags_supported(uint32_t flags);

@@ -43,7 +43,8 @@ class GemmArgs(ctypes.Structure):
     _fields_ = [("x", P), ("w", P), ("out", P), ("res", P), ("norm_w", P), ("partial", P),
                 ("counters", P), ("ids_out", P), ("lens_inc", P), ("eps", F32), ("rows", I32),
                 ("n", I32), ("k", I32), ("flags", ctypes.c_uint32), ("ksplit", I32), ("waves", I32),
-                ("tiles_per_wg", I32), ("x_attn", P), ("x_frag", I32), ("out_frag", I32)]
+                ("tiles_per_wg", I32), ("x_attn", P), ("x_frag", I32), ("out_frag", I32),
+                ("parts_out", P), ("x_parts", P), ("x_nparts", I32), ("x_merged", P)]
 
 
 class AttnArgs(ctypes.Structure):

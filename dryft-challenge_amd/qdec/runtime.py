@@ -59,6 +59,9 @@ MERGE_IN_O_MAX_BATCH = 4
 FRAG_ROWS = 17
 # Loss-free speculation needs identical arithmetic in the plain and verify
 # steps, so attention chunking depends on (batch, capacity) only.
+# k splits of the down projection from this batch size (see role_plan).
+DOWN_SPLIT = 4
+DOWN_SPLIT_MIN_BATCH = 16
 
 
 def round_up(x, m):
@@ -114,8 +117,8 @@ def rope_tables(cap, head_dim, theta):
     return emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
 
 
-def role_plan(n, k, role):
-    """(ksplit, waves, tiles_per_wg) of one projection role.
+def role_plan(n, k, role, batch=1):
+    """(ksplit, waves, tiles_per_wg) of one projection role at a batch size.
 
     Output tiles are 16 columns, one workgroup per tile (4 per workgroup for
     the lm_head), no k split across workgroups: a split's cross-workgroup
@@ -124,12 +127,23 @@ def role_plan(n, k, role):
     workgroup, which doubles the weight blocks each busy CU keeps in flight
     (O 7.6 -> 7.0 us, down 14.2 -> 13.5 us at batch 1).  The lm_head runs 4
     tiles per workgroup (137 us against 144 us with 8 and 146 us with 2,
-    non-temporal weight loads).  Only (n, k, role) decide it, never the row
-    count."""
+    non-temporal weight loads).  Only (n, k, role) and the batch decide it,
+    never the row count, so a verify pass over batch x (k + 1) rows sums
+    every element as the plain step of the same batch does."""
     ks = k // 32
     ntiles = n // 16
     ksplit = 1
     waves = 8 if ntiles <= 256 else 4
+    if (role == "down" and batch >= DOWN_SPLIT_MIN_BATCH and DOWN_SPLIT > 1 and ntiles <= 256
+            and ks % (DOWN_SPLIT * 4) == 0):
+        # Few tiles and a long k: split k in DOWN_SPLIT, four waves each, and
+        # leave the partials to the next NORM_IN call (x_parts), whose
+        # normalisation pre-pass merges them (Qwen3-4B: 640 workgroups instead
+        # of 160).  Measured on MI355X, ms per step: batch 32 3.69 -> 3.62;
+        # batch 8 3.01 -> 3.09 and batch 1 2.145 -> 2.155 (QKV then needs the
+        # pre-pass, or merges four partials per workgroup), so only from
+        # DOWN_SPLIT_MIN_BATCH.
+        return DOWN_SPLIT, 4, 1
     while ks % waves:
         waves //= 2
     tiles = 1
@@ -265,7 +279,17 @@ class DecodeState:
         self.v_cache = torch.zeros(cache_shape, dtype=bf, device=dev)
         self.layer_elems = batch * c.nkv * self.cap * D
         R = self.max_rows
-        self.h = torch.zeros((R, H), dtype=bf, device=dev)
+        # The residual stream alternates between two buffers: the down
+        # projection leaves its update as k-split partials (down_parts) and
+        # the next layer's QKV (or the lm_head) merges them into the other
+        # buffer while it reads the first.  Layer l's residual is
+        # hbuf[l % 2]; the embedding and the prefill hand-off write hbuf[0].
+        self.hbuf = torch.zeros((2, R, H), dtype=bf, device=dev)
+        self.h = self.hbuf[0]
+        self.plans = dict(model.plans)
+        self.plans["down"] = role_plan(H, c.inter, "down", batch)
+        ks, _, _ = self.plans["down"]
+        self.down_parts = torch.zeros((ks, R, H), dtype=torch.float32, device=dev) if ks > 1 else None
         self.qkv = torch.zeros((R, c.n_qkv), dtype=bf, device=dev)
         # attention -> O and gate/up -> down hand over in fragment order from
         # FRAG_ROWS rows: whole M tiles.
@@ -301,17 +325,39 @@ class DecodeState:
         activations (no arrival pass); bit-identical to the merged output."""
         return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH
 
-    def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None, x_attn=None):
+    def _hb(self, layer):
+        """Residual buffer of ``layer`` (hbuf[0] throughout when down does not
+        split: its RES_OUT epilogue then updates the residual in place)."""
+        return self.hbuf[layer % 2] if self.down_parts is not None else self.hbuf[0]
+
+    def _residual_in(self, a, layer, pending):
+        """x of a NORM_IN call at the start of ``layer`` (``layer`` =
+        n_layers: the lm_head): the previous layer's residual, with the down
+        projection's split update still to merge -- unless ``pending`` is
+        False: rows written directly into hbuf[0], as the prefill hand-off
+        does."""
+        if not pending:
+            a.x = self.hbuf[0].data_ptr()
+        elif layer > 0 and self.down_parts is not None:
+            a.x = self._hb(layer - 1).data_ptr()
+            a.x_parts, a.x_nparts = self.down_parts.data_ptr(), self.down_parts.shape[0]
+            a.x_merged = self._hb(layer).data_ptr()
+        else:
+            a.x = self._hb(layer).data_ptr()
+
+    def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None, x_attn=None, pending=True):
         m, c = self.model, self.model.cfg
-        ksplit, waves, tiles = m.plans[role]
+        ksplit, waves, tiles = self.plans[role]
         a = capi.GemmArgs()
         a.eps, a.rows, a.ksplit, a.waves, a.tiles_per_wg = c.eps, rows, ksplit, waves, 1
+        h = self._hb(layer)
         if role == "qkv":
-            a.x, a.w, a.out = self.h.data_ptr(), m.w_qkv[layer].data_ptr(), self.qkv.data_ptr()
+            self._residual_in(a, layer, pending)
+            a.w, a.out = m.w_qkv[layer].data_ptr(), self.qkv.data_ptr()
             a.norm_w = m.in_w[layer].data_ptr()
             a.n, a.k, a.flags = c.n_qkv, c.hidden, capi.NORM_IN
         elif role == "o":
-            a.x, a.w, a.res = self.attn_out.data_ptr(), m.w_o[layer].data_ptr(), self.h.data_ptr()
+            a.x, a.w, a.res = self.attn_out.data_ptr(), m.w_o[layer].data_ptr(), h.data_ptr()
             a.n, a.k, a.flags = c.hidden, c.nq * c.head_dim, capi.RES_OUT
             if x_attn is not None:
                 a.x_attn = ctypes.addressof(x_attn)
@@ -319,19 +365,30 @@ class DecodeState:
             else:
                 a.x_frag = 1 if rows >= FRAG_ROWS else 0
         elif role == "gate_up":
-            a.x, a.w, a.out = self.h.data_ptr(), m.w_gu[layer].data_ptr(), self.act.data_ptr()
+            a.x, a.w, a.out = h.data_ptr(), m.w_gu[layer].data_ptr(), self.act.data_ptr()
             a.norm_w = m.post_w[layer].data_ptr()
             a.n, a.k, a.flags = c.inter, c.hidden, capi.NORM_IN | capi.GLU
             a.out_frag = 1 if rows >= FRAG_ROWS else 0
         elif role == "down":
-            a.x, a.w, a.res = self.act.data_ptr(), m.w_down[layer].data_ptr(), self.h.data_ptr()
+            a.x, a.w, a.res = self.act.data_ptr(), m.w_down[layer].data_ptr(), h.data_ptr()
             a.n, a.k, a.flags = c.hidden, c.inter, capi.RES_OUT
             a.x_frag = 1 if rows >= FRAG_ROWS else 0
+            if self.down_parts is not None:
+                a.parts_out = self.down_parts.data_ptr()
         elif role == "lm":
-            a.x, a.w = self.h.data_ptr(), m.emb.data_ptr()
+            self._residual_in(a, c.n_layers, pending)
+            a.w = m.emb.data_ptr()
             a.norm_w = m.norm_w.data_ptr()
             a.n, a.k, a.flags = c.vocab, c.hidden, capi.NORM_IN | capi.ARGMAX
-            a.tiles_per_wg = LM_TILES_BATCHED if rows > 1 and (c.vocab // 16) % LM_TILES_BATCHED == 0 else tiles
+            # 8 tiles per workgroup from 2 rows; past two M tiles (33+ rows,
+            # verify passes only) one, so the direct path's ring fits the
+            # workgroup's k range (the grouping changes no sum).
+            if rows == 1:
+                a.tiles_per_wg = tiles
+            elif rows <= 32 and (c.vocab // 16) % LM_TILES_BATCHED == 0:
+                a.tiles_per_wg = LM_TILES_BATCHED
+            else:
+                a.tiles_per_wg = 1
             a.out = self.logits.data_ptr() if self.logits is not None else None
             a.ids_out = (ids_out if ids_out is not None else self.ids).data_ptr()
             a.lens_inc = lens_inc.data_ptr() if lens_inc is not None else None
@@ -533,5 +590,5 @@ class Prefill:
                 lib.prefill_gemm(g_dn, s)
         # The last position of every sequence: final norm, lm_head, argmax.
         st.h[:B].copy_(self.h[:B * T].view(B, T, H)[:, T - 1])
-        lib.gemm(st._gemm_args("lm", 0, B, ids_out=st.ids), s)
+        lib.gemm(st._gemm_args("lm", 0, B, ids_out=st.ids, pending=False), s)
         st.lens.fill_(S)

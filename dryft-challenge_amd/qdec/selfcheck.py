@@ -72,17 +72,29 @@ def run(state):
 
     # ---- projections, one row, the state's own plans
     for role in ("qkv", "o", "gate_up", "down", "lm"):
-        a = state._gemm_args(role, 0, 1)
+        a = state._gemm_args(role, 0, 1, pending=False)
         n, k = a.n, a.k
         x = one_hot(k, 1.0)
         src = {"qkv": state.h, "o": state.attn_out, "gate_up": state.h, "down": state.act, "lm": state.h}[role]
         src[:1, :k].copy_(x)
         w = {"qkv": m.w_qkv[0], "o": m.w_o[0], "gate_up": m.w_gu[0], "down": m.w_down[0], "lm": m.emb}[role]
+        if role == "down" and a.parts_out:
+            # split k, partials left for the next NORM_IN call: the split
+            # holding the one-hot column gives the weight column, the others 0
+            parts = state.down_parts
+            parts.fill_(float("nan"))
+            lib.gemm(a, s)
+            ks = parts.shape[0]
+            want = torch.zeros((ks, n), device=dev)
+            want[col // (k // ks)] = _tiled_column(w, n, k, col, dev)
+            if not torch.equal(parts[:, 0], want):
+                _fail(role, "split partials differ from the weight column")
+            continue
         if role in ("o", "down"):
             res0 = torch.linspace(-3, 3, n, device=dev).to(torch.bfloat16)[None]
-            state.h[:1].copy_(res0)
+            state._hb(0)[:1].copy_(res0)
             lib.gemm(a, s)
-            got = state.h[0].float()
+            got = state._hb(0)[0].float()
             want = _bf16(res0[0].float() + _tiled_column(w, n, k, col, dev))
             if not torch.equal(got, want):
                 _fail(role, f"{int((got != want).sum())} of {n} outputs differ from weight column + residual")
@@ -107,7 +119,7 @@ def run(state):
                 _fail(role, "SwiGLU outputs beyond one bf16 rounding step of the one-hot answer")
         else:
             ids = torch.full((1,), -1, dtype=torch.int64, device=dev)
-            a = state._gemm_args("lm", 0, 1, ids_out=ids)
+            a = state._gemm_args("lm", 0, 1, ids_out=ids, pending=False)
             lib.gemm(a, s)
             logits = _bf16(v * _tiled_column(w, n, k, col, dev))
             best = logits.max()

@@ -170,10 +170,25 @@ typedef struct {
    * last M tile are ignored.
    * x_frag = 1: x is in fragment order (as a call with out_frag = 1 or an
    * attention call with out_frag = 1 over the same rows wrote it).  Not with
-   * NORM_IN or x_attn; needs ksplit 1 (the call takes the direct path).
+   * NORM_IN or x_attn (the call takes the direct path).
    * out_frag = 1: out is written in fragment order (plain or GLU only). */
   int32_t x_frag;
   int32_t out_frag;
+  /* Residual update left to the next NORM_IN call (RES_OUT with ksplit > 1):
+   * each k split writes its fp32 partial sum of y to
+   * parts_out[split][rows][n]; res is not touched and no counters are used.
+   * The consumer passes the same buffer as x_parts. */
+  float *parts_out;
+  /* NORM_IN: the residual x still owes a RES_OUT update held in k-split
+   * partials x_parts[j][rows][k], j < x_nparts (1..8).  The call first forms
+   * x = bf16(x + bf16(((p0 + p1) + p2) + ...)) per element -- the rounding a
+   * RES_OUT call applies -- uses it as its input and writes it to x_merged
+   * ([rows, k] bf16, not x itself: other workgroups of the call still read
+   * x).  Needs ksplit 1 and a plan that stages x from registers (few rows)
+   * or through the normalisation pre-pass (QDEC_EUNSUPPORTED otherwise). */
+  const float *x_parts;
+  int32_t x_nparts;
+  void *x_merged;
 } qdec_gemm_args;
 int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream);
 /* Scratch sizes (bytes) a qdec_gemm call with these arguments needs. */

@@ -610,6 +610,70 @@ def test_draft_and_accept_vs_oracle(lib, K):
             assert nacc[b].item() == na and dl[b].item() == nl and dh[b].cpu().tolist() == h
 
 
+# --------------------------------------------- split residual update pipeline
+
+@pytest.mark.parametrize("rows", [1, 3, 9, 17, 32])
+def test_down_split_merged_by_next_norm_in_call(lib, rows):
+    """The engine's down projection (k split 4 ways, partials left in
+    parts_out) followed by the next layer's QKV and the lm_head merging them
+    (x_parts): the merged residual equals bf16(res + bf16(act . Wd^T)) within
+    one rounding, the QKV output matches the oracle on it, and every merged
+    row and output is bit-identical to the one-row call's (a verify pass
+    reproduces plain decode)."""
+    from qdec import capi
+    from qdec.runtime import LM_TILES_BATCHED, role_plan
+    pd, pq = role_plan(H, I, "down", batch=32), role_plan(6144, H, "qkv")
+    assert pd[0] > 1
+    big = 32
+    act_all = rnd(big, I, scale=1.0, seed=81)
+    res_all = rnd(big, H, scale=2.0, seed=82)
+    Wd = rnd(H, I, scale=0.02, seed=83)
+    Wq = rnd(6144, H, scale=0.02, seed=84)
+    E = rnd(2048, H, scale=0.02, seed=85)
+    nw = bf16(1 + 0.2 * torch.randn(H, generator=torch.Generator().manual_seed(86))).to(torch.bfloat16)
+    Wdt, Wqt, Et = pack(lib, Wd.to(DEV)), pack(lib, Wq.to(DEV)), pack(lib, E.to(DEV))
+
+    def run(idx):
+        R = len(idx)
+        act, res = act_all[idx].contiguous().to(DEV), res_all[idx].contiguous().to(DEV)
+        parts = torch.full((pd[0], R, H), float("nan"), dtype=torch.float32, device=DEV)
+        d = capi.GemmArgs(x=act.data_ptr(), w=Wdt.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=R, n=H, k=I,
+                          flags=capi.RES_OUT, ksplit=pd[0], waves=pd[1], tiles_per_wg=1,
+                          parts_out=parts.data_ptr())
+        lib.gemm(d, stream())
+        merged = torch.zeros(R, H, dtype=torch.bfloat16, device=DEV)
+        out = torch.zeros(R, 6144, dtype=torch.bfloat16, device=DEV)
+        g = Gemm(lib, capi.NORM_IN, 6144, H, ksplit=pq[0], waves=pq[1])
+        q = capi.GemmArgs(x=res.data_ptr(), w=Wqt.data_ptr(), out=out.data_ptr(), norm_w=nw.to(DEV).data_ptr(),
+                          eps=1e-6, rows=R, n=6144, k=H, flags=capi.NORM_IN, ksplit=pq[0], waves=pq[1],
+                          tiles_per_wg=1, x_parts=parts.data_ptr(), x_nparts=pd[0], x_merged=merged.data_ptr(),
+                          partial=g.partial.data_ptr(), counters=g.counters.data_ptr())
+        nwd = nw.to(DEV)
+        q.norm_w = nwd.data_ptr()
+        lib.gemm(q, stream())
+        merged2 = torch.zeros(R, H, dtype=torch.bfloat16, device=DEV)
+        ids = torch.full((R,), -1, dtype=torch.int64, device=DEV)
+        lm = capi.GemmArgs(x=res.data_ptr(), w=Et.data_ptr(), norm_w=nwd.data_ptr(), ids_out=ids.data_ptr(), eps=1e-6,
+                           rows=R, n=2048, k=H, flags=capi.NORM_IN | capi.ARGMAX, ksplit=1, waves=4,
+                           tiles_per_wg=LM_TILES_BATCHED if R > 1 else 4, x_parts=parts.data_ptr(),
+                           x_nparts=pd[0], x_merged=merged2.data_ptr(),
+                           partial=g.partial.data_ptr(), counters=g.counters.data_ptr())
+        lib.gemm(lm, stream())
+        torch.cuda.synchronize()
+        assert torch.equal(merged, merged2)
+        return merged.cpu(), out.cpu(), ids.cpu()
+
+    idx = list(range(rows)) if rows < big else list(range(big))
+    merged, out, ids = run(idx)
+    want_h = bf16(res_all[idx].float() + linear(act_all[idx].float(), Wd.float()))
+    agree(merged, want_h, min_exact=0.98)
+    agree(out, linear(rms_norm(merged.float(), nw.float(), 1e-6), Wq.float()), min_exact=0.98)
+    one_m, one_o, one_i = run([idx[-1]])
+    assert torch.equal(one_m[0].view(torch.int16), merged[-1].view(torch.int16))
+    assert torch.equal(one_o[0].view(torch.int16), out[-1].view(torch.int16))
+    assert one_i[0] == ids[-1]
+
+
 # ------------------------------------------------------ invalid inputs, bands
 
 def test_invalid_length_and_id_give_nan_not_stale_output(lib):
@@ -686,10 +750,21 @@ def test_gemm_epilogues_stay_in_bounds(lib, rows):
     res_whole, res = banded(rows * H)
     res.copy_(rnd(rows * H, scale=2.0, seed=65).to(DEV))
     d = capi.GemmArgs(x=act.data_ptr(), w=Wd.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=rows, n=H, k=I,
-                      flags=capi.RES_OUT, ksplit=pd[0], waves=pd[1], tiles_per_wg=1, x_frag=frag,
-                      partial=ws.data_ptr(), counters=cnt.data_ptr())
-    assert lib.gemm_workspace(d)[0] <= max(pb, 4)
+                      flags=capi.RES_OUT, ksplit=pd[0], waves=pd[1], tiles_per_wg=1, x_frag=frag)
+    dpb, dcb = lib.gemm_workspace(d)
+    dws_whole, dws = banded(max(dpb, 4) // 4, dtype=torch.float32)
+    dcnt_whole, dcnt = banded(max(dcb, 4) // 4, dtype=torch.int32, fill=0)
+    d.partial, d.counters = dws.data_ptr(), dcnt.data_ptr()
     lib.gemm(d, stream())
+    # the down call leaving its k-split partials (as the engine runs it from batch 16)
+    ps = role_plan(H, I, "down", batch=32)
+    parts_elems = ps[0] * rows * H
+    parts_whole, parts = banded(parts_elems, dtype=torch.float32)
+    d2 = capi.GemmArgs(x=act.data_ptr(), w=Wd.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=rows, n=H, k=I,
+                       flags=capi.RES_OUT, ksplit=ps[0], waves=ps[1], tiles_per_wg=1, x_frag=frag,
+                       parts_out=parts.data_ptr())
+    assert lib.gemm_workspace(d2) == (0, 0)
+    lib.gemm(d2, stream())
     # lm_head + argmax (argmax partials and, from 9 rows, the normalised rows in the workspace)
     Vs = 4096
     E = pack(lib, rnd(Vs, H, scale=0.02, seed=66).to(DEV))
@@ -705,6 +780,8 @@ def test_gemm_epilogues_stay_in_bounds(lib, rows):
     torch.cuda.synchronize()
     assert bands_intact(act_whole, act_elems), "SwiGLU output"
     assert bands_intact(res_whole, rows * H), "down residual"
+    assert bands_intact(dws_whole, max(dpb, 4) // 4) and bands_intact(dcnt_whole, max(dcb, 4) // 4, fill=0)
+    assert bands_intact(parts_whole, parts_elems), "down split partials"
     assert bands_intact(ws_whole, max(pb, 4) // 4), "GEMM workspace"
     assert bands_intact(cnt_whole, max(cb, 4) // 4, fill=0) and int(cnt.abs().sum()) == 0, "counters"
     assert bands_intact(ids_whole, rows, fill=-7) and bool((ids >= 0).all()), "argmax ids"
