@@ -60,6 +60,9 @@ CONFIGS = {
     "c2": (1, 512, 256, "qwen3-4b bf16 bs1 prompt512 new256"),
     "c3": (8, 1024, 512, "qwen3-4b bf16 bs8 prompt1024 new512"),
     "c4": (32, 4096, 256, "qwen3-4b bf16 bs32 prompt4096 new256"),
+    # config 5's batch and prompt length through plain decode (its motif
+    # prompts and speculative decoding run in the `speculation` object)
+    "c5": (4, 1024, 512, "qwen3-4b bf16 bs4 prompt1024 new512"),
 }
 
 
@@ -77,20 +80,21 @@ def step_bytes(model_cfg, weight_bytes, batch, pos):
 ROLES = ("qkv", "attn", "o", "gate_up", "down", "lm")
 
 
-def time_gemm_role(engine, state, role, reps=5):
+def time_gemm_role(engine, state, role, reps=5, t_rows=1):
     """Average duration (s) of one launch of ``role``'s kernel (a GEMM, or
     ``attn``: the decode attention as the step launches it), over all
     layers' weights / caches (so nothing is served from the 256 MB MALL),
-    HIP events on the engine's stream."""
+    HIP events on the engine's stream.  ``t_rows`` > 1: the verify pass's
+    calls (batch x t_rows rows)."""
     import torch
     lib = engine.lib
-    rows = state.batch
+    rows = state.batch * t_rows
     n = engine.model.cfg.n_layers if role != "lm" else 1
     if role == "attn":
-        pm = state._merge_in_o(1)
-        args = [state._attn_args(i, 1, partials=pm) for i in range(n)]
+        pm = state._merge_in_o(t_rows)
+        args = [state._attn_args(i, t_rows, partials=pm) for i in range(n)]
         call = lib.attn
-    elif role == "o" and state._merge_in_o(1):  # merges the attention's chunk partials, as in the step
+    elif role == "o" and state._merge_in_o(t_rows):  # merges the attention's chunk partials, as in the step
         args = [state._gemm_args(role, i, rows, x_attn=state._attn_args(i, 1, partials=True)) for i in range(n)]
         call = lib.gemm
     else:
@@ -397,6 +401,8 @@ def main():
                     help="only launch this role's kernel over every layer (6 rounds, rows = the "
                          "config's batch; 'all' = every role in turn), then a 512 MiB device copy "
                          "as the counter calibration, for rocprofv3 --pmc")
+    ap.add_argument("--pmc-t-rows", type=int, default=1,
+                    help="with --pmc-role: rows per sequence of every call (a verify pass: drafts + 1)")
     ap.add_argument("--cpu-prompt", type=int, default=512, help="prompt tokens of the CPU baseline's prefill "
                     "(config 2's 512 by default)")
     ap.add_argument("--prefill-only", type=int, default=0, metavar="REPS",
@@ -432,13 +438,10 @@ def main():
         print(json.dumps({"prefill": pf, "config": desc}), flush=True)
         return
     if args.pmc_role:
-        if B == 1:
-            st.prefill(prompt.to(eng.device))
-        else:  # counters only: batched configs run on random activations, no prefill
-            st.h.normal_(0.0, 1.0)
-            st.act.normal_(0.0, 1.0)
+        # the config's real prompt, so the attention reads a real cache length
+        st.prefill(prompt.to(eng.device))
         for role in (ROLES if args.pmc_role == "all" else (args.pmc_role,)):
-            time_gemm_role(eng, st, role, reps=5)
+            time_gemm_role(eng, st, role, reps=5, t_rows=args.pmc_t_rows)
         src = torch.empty(512 << 20, dtype=torch.uint8, device=eng.device)
         dst = torch.empty_like(src)
         for _ in range(5):
@@ -547,7 +550,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
                      "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a "
-                                       "512 MiB copy (profiles/gate_up_hbm_traffic_bs1.md)",
+                                       "512 MiB copy (profiles/gate_up_hbm_traffic_bs1.md; every role: "
+                                       "profiles/decode_hbm_traffic_all_roles.md)",
                      "kernel": "gemm_kernel<1, NORM_IN|GLU> (gate/up, 9728x2x2560)",
                      "algorithmic_bytes_per_launch": gu_bytes,
                      "avg_launch_us": round(t_gu * 1e6, 3)},
