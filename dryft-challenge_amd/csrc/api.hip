@@ -156,9 +156,20 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   // written to the workspace by a pre-pass; passes only when neither fits.
   p->rw = 0;
   p->xd = 0;
+  p->tw = 1;
   p->xn = nullptr;
   const int ring = gemm_ring(p->ksw, f);
-  const int ring_d = gemm_ring_direct(mt, f);
+  // Direct path: two tiles per wave at two M tiles when the workgroup's
+  // tiles pair up, without GLU (sums unchanged: every tile keeps its own
+  // MFMA chain).  gate/up stays at one: at 32 rows its four weight streams
+  // per wave cost a third wave per SIMD (30.4 against 28.4 us).
+  int tw = (mt == 2 && !glu && a->tiles_per_wg % 2 == 0 && (a->ksplit == 1 || a->parts_out)) ? 2 : 1;
+  int ring_d = gemm_ring_direct(mt, f, tw, p->ksw, a->tiles_per_wg / tw);
+  if (!ring_d && tw == 2) {
+    tw = 1;
+    ring_d = gemm_ring_direct(mt, f, 1, p->ksw, a->tiles_per_wg);
+  }
+  const size_t lds_direct = head + red_bytes * tw;
   // Past its register-staged rows a NORM_IN call does better on the direct
   // path: one normalisation pre-pass instead of every workgroup reading
   // whole rows for the statistics and then again for staging (gate/up at 8
@@ -166,22 +177,23 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   const bool stage_norm = !(f & QDEC_NORM_IN) || a->rows < (glu ? kGemmDirectGluRows : kGemmDirectNormRows);
   if (a->x_frag) {
     // x already in fragment order: the direct path reads it as it is.
-    if (!ring_d || (a->tiles_per_wg != 1 && p->ksw % ring_d))
-      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_frag: no direct ring for rows %d", a->rows);
+    if (!ring_d) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_frag: no direct ring for rows %d", a->rows);
     p->rw = ring_d;
     p->xd = 1;
+    p->tw = tw;
     p->xt = mt;
     p->xfast = 0;
     p->lds_all = 0;
-    p->lds_bytes = head + red_bytes;
+    p->lds_bytes = lds_direct;
   } else if (mt == 1 && lds_all && ring && stage_norm) {
     p->rw = ring;
-  } else if (a->ksplit == 1 && ring_d && (a->tiles_per_wg == 1 || p->ksw % ring_d == 0)) {
+  } else if (a->ksplit == 1 && ring_d) {
     p->rw = ring_d;
     p->xd = 1;
+    p->tw = tw;
     p->xfast = 0;
     p->lds_all = 0;
-    p->lds_bytes = head + red_bytes;
+    p->lds_bytes = lds_direct;
     // The pre-pass writes x in fragment order (normalised under NORM_IN):
     // row-major fragments would cost a cache access per lane.
     if ((f & QDEC_NORM_IN) || a->rows >= kGemmRetileRows) {
@@ -197,14 +209,15 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->xnparts = a->x_parts ? a->x_nparts : 0;
   p->xmerged = reinterpret_cast<uint16_t *>(a->x_merged);
   if (a->x_parts && !(a->rows == 1 && p->xfast && p->rw > 0 && a->x_nparts <= 4)) {
-    if (!ring_d || (a->tiles_per_wg != 1 && p->ksw % ring_d))
+    if (!ring_d)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_parts at %d rows needs the direct path, which this tile "
                        "grouping does not allow", a->rows);
     p->rw = ring_d;
     p->xd = 1;
+    p->tw = tw;
     p->xfast = 0;
     p->lds_all = 0;
-    p->lds_bytes = head + red_bytes;
+    p->lds_bytes = lds_direct;
     p->xt = mt;
     p->xpre = 1;
   }

@@ -177,7 +177,11 @@ constexpr int kMergeParts = 4;
 
 // XP: the instantiation that merges a pending split residual update into its
 // one register-staged row (FR = 1); 0 elsewhere.
-template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows, bool XP = false>
+// TW: output tiles per wave on the direct path.  Each activation fragment a
+// wave loads then feeds TW tiles' MFMAs, so from two M tiles the activation
+// reads per weight byte halve at TW = 2 and the ring's registers go to
+// weights instead (a tile's sums are the same whatever TW is).
+template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows, bool XP = false, int TW = 1>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr bool NORM = (FLAGS & QDEC_NORM_IN) != 0;
@@ -185,6 +189,10 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   constexpr bool RES = (FLAGS & QDEC_RES_OUT) != 0;
   constexpr bool ARG = (FLAGS & QDEC_ARGMAX) != 0;
   constexpr int NACC = GLU ? 2 : 1;
+  static_assert(TW == 1 || XD, "several tiles per wave: direct path only");
+  // Weight streams and accumulators per wave: tile tw's gate (or only)
+  // stream at tw * NACC, its up stream at tw * NACC + 1.
+  constexpr int NA = NACC * TW;
   constexpr bool WIN = RW > 0;
   static_assert(!WIN || MT == 1 || XD, "LDS-staged windows serve one M tile");
   static_assert(!XD || (WIN && !NORM), "direct activations: window path, x already normalised");
@@ -231,7 +239,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
     }
   }
 
-  uint4 wb[NACC][NB];
+  uint4 wb[NA][NB];
   // Direct activations: the B fragment of ring slot r, loaded from global
   // (cache-resident x) right behind the slot's weight block.
   uint4 xb[XD ? MT : 1][XD ? NB : 1];
@@ -249,6 +257,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   }
   // Weight block of k step i (relative to the wave's range) of `tile`.
   auto wptr = [&](int tile, int i) { return W + ((size_t)tile * p.KS + ks_wave + i) * 64 + lane; };
+  const size_t tstride = (size_t)p.KS * 64;  // between consecutive tiles' blocks
   // Passes: straight-line loads of one pass; indices past the pass are clamped
   // to its last block (a redundant, cache-served load) instead of branched
   // around, so all of them stay in flight together.
@@ -267,8 +276,11 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
 #pragma unroll
       for (int r = 0; r < NB; ++r) {
         const int rr = min(r, p.ksw - 1);  // a range shorter than the ring repeats its last block
-        wb[0][r] = ldw(q + rr * 64);
-        if constexpr (GLU) wb[1][r] = ldw(q + rr * 64 + up_off);
+#pragma unroll
+        for (int tw = 0; tw < TW; ++tw) {
+          wb[tw * NACC][r] = ldw(q + tw * tstride + rr * 64);
+          if constexpr (GLU) wb[tw * NACC + 1][r] = ldw(q + tw * tstride + rr * 64 + up_off);
+        }
         if constexpr (XD) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
@@ -450,11 +462,11 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   }
 
   bool have_w = true;  // wb holds the next pass's weights already (pass path)
-  for (int tt = 0; tt < p.tiles_per_wg; ++tt) {
-    const int tile = tile0 + tt;
-    f32x4_t acc[NACC][MT];
+  for (int tt = 0; tt < p.tiles_per_wg; tt += TW) {
+    const int tile = tile0 + tt;  // this wave's tiles: tile .. tile + TW - 1
+    f32x4_t acc[NA][MT];
 #pragma unroll
-    for (int a = 0; a < NACC; ++a)
+    for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[a][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
@@ -462,7 +474,7 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       // B operand rows: lane col < rows reads its row, the others read row 0
       // and use zeros.
       const uint16_t *xs = s_x + (size_t)(xrow_ok ? col : 0) * xstride + wave * p.ksw * 32 + grp * 8;
-      const bool more_tiles = tt + 1 < p.tiles_per_wg;
+      const bool more_tiles = tt + TW < p.tiles_per_wg;
       if constexpr (!XD) {
         // Slot r always holds k step r (mod RW): refill with k step i + RW of
         // this tile while it exists, else the same offset into the next tile;
@@ -490,11 +502,11 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         }
       } else {
         // Direct activations: the same ring, and a ragged last chunk when RW
-        // does not divide the range (one tile per workgroup then).  Every tile
-        // spans the same k range of x.
+        // does not divide the range (one group of TW tiles per workgroup
+        // then).  Every tile spans the same k range of x.
         for (int i0 = 0; i0 < p.ksw; i0 += RW) {
           const bool same_tile = i0 + RW < p.ksw;
-          const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + 1, i0 + RW - p.ksw);
+          const uint4 *qn = same_tile ? wptr(tile, i0 + RW) : wptr(tile + TW, i0 + RW - p.ksw);
 #pragma unroll
           for (int r = 0; r < RW; ++r) {
             const int i = i0 + r;
@@ -503,11 +515,14 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
               for (int mt = 0; mt < MT; ++mt) {
                 const uint4 b = (mt * 16 + col < rows) ? xb[mt][r] : zero4();
 #pragma unroll
-                for (int a = 0; a < NACC; ++a) acc[a][mt] = mfma16x16x32(wb[a][r], b, acc[a][mt]);
+                for (int a = 0; a < NA; ++a) acc[a][mt] = mfma16x16x32(wb[a][r], b, acc[a][mt]);
               }
               if (i + RW < p.ksw || (!same_tile && more_tiles)) {
-                wb[0][r] = ldw(qn + r * 64);
-                if constexpr (GLU) wb[1][r] = ldw(qn + r * 64 + up_off);
+#pragma unroll
+                for (int tw = 0; tw < TW; ++tw) {
+                  wb[tw * NACC][r] = ldw(qn + tw * tstride + r * 64);
+                  if constexpr (GLU) wb[tw * NACC + 1][r] = ldw(qn + tw * tstride + r * 64 + up_off);
+                }
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
                   xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + (size_t)((i + RW) % p.ksw) * xkstep);
@@ -572,20 +587,20 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       float4 *red = reinterpret_cast<float4 *>(smem + p.lds_red_off);
       if (wave > 0) {
 #pragma unroll
-        for (int a = 0; a < NACC; ++a)
+        for (int a = 0; a < NA; ++a)
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
-            red[(((wave - 1) * NACC + a) * MT + mt) * 64 + lane] =
+            red[(((wave - 1) * NA + a) * MT + mt) * 64 + lane] =
                 make_float4(acc[a][mt][0], acc[a][mt][1], acc[a][mt][2], acc[a][mt][3]);
       }
       __syncthreads();
       if (wave == 0) {
         for (int w2 = 1; w2 < nw; ++w2) {
 #pragma unroll
-          for (int a = 0; a < NACC; ++a)
+          for (int a = 0; a < NA; ++a)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-              const float4 r = red[(((w2 - 1) * NACC + a) * MT + mt) * 64 + lane];
+              const float4 r = red[(((w2 - 1) * NA + a) * MT + mt) * 64 + lane];
               acc[a][mt][0] += r.x;
               acc[a][mt][1] += r.y;
               acc[a][mt][2] += r.z;
@@ -595,100 +610,107 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
       }
     }
 
-    const int n0 = tile * 16 + grp * 4;  // first of this lane's 4 output columns
     auto out_at = [&](int m, int n) {
       uint16_t *o = reinterpret_cast<uint16_t *>(p.out);
       return p.ofrag ? o + frag_off(m, n, p.ofrag) : o + (size_t)m * p.n + n;
     };
+#pragma unroll
+    for (int tw = 0; tw < TW; ++tw) {
+      const int ct = tile + tw;           // output tile
+      const int n0 = ct * 16 + grp * 4;   // first of this lane's 4 output columns
 
-    // ---- k split left to the next NORM_IN call: raw partials, no epilogue.
-    if (RES && p.parts_out) {
+      // ---- k split left to the next NORM_IN call: raw partials, no epilogue.
+      if (RES && p.parts_out) {
+        if (wave == 0) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int m = mt * 16 + col;
+            if (m < rows)
+              *reinterpret_cast<f32x4_t *>(p.parts_out + ((size_t)split * rows + m) * p.n + n0) = acc[tw * NACC][mt];
+          }
+        }
+        continue;
+      }
+      // ---- k split across workgroups: partials, last arrival sums them.
+      if (p.ksplit > 1) {
+        if (wave == 0) {
+#pragma unroll
+          for (int a = 0; a < NACC; ++a)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const int m = mt * 16 + col;
+              if (m < rows)
+                store_coherent4(p.partial + ((size_t)(a * p.ksplit + split) * rows + m) * p.n + n0, acc[tw * NACC + a][mt]);
+            }
+        }
+        // Not the last split of this tile: go on with the next tile.
+        if (!arrive_last(p.counters + ct, (uint32_t)p.ksplit, s_flag)) continue;
+        if (wave == 0) {
+#pragma unroll
+          for (int a = 0; a < NACC; ++a)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const int m = mt * 16 + col;
+              if (m < rows) {
+                f32x4_t t = load_coherent4(p.partial + ((size_t)(a * p.ksplit) * rows + m) * p.n + n0);
+                for (int s = 1; s < p.ksplit; ++s)
+                  t += load_coherent4(p.partial + ((size_t)(a * p.ksplit + s) * rows + m) * p.n + n0);
+                acc[tw * NACC + a][mt] = t;
+              }
+            }
+        }
+      }
+
+      // ---- epilogues (wave 0 holds the finished tile).
       if (wave == 0) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const int m = mt * 16 + col;
-          if (m < rows)
-            *reinterpret_cast<f32x4_t *>(p.parts_out + ((size_t)split * rows + m) * p.n + n0) = acc[0][mt];
-        }
-      }
-      continue;
-    }
-    // ---- k split across workgroups: partials, last arrival sums them.
-    if (p.ksplit > 1) {
-      if (wave == 0) {
+          if (m >= rows) continue;
+          const f32x4_t g4 = acc[tw * NACC][mt];
+          if constexpr (ARG) {
+            float v[4];
 #pragma unroll
-        for (int a = 0; a < NACC; ++a)
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const int m = mt * 16 + col;
-            if (m < rows) store_coherent4(p.partial + ((size_t)(a * p.ksplit + split) * rows + m) * p.n + n0, acc[a][mt]);
-          }
-      }
-      // Not the last split of this tile: go on with the workgroup's next tile.
-      if (!arrive_last(p.counters + tile, (uint32_t)p.ksplit, s_flag)) continue;
-      if (wave == 0) {
-#pragma unroll
-        for (int a = 0; a < NACC; ++a)
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            const int m = mt * 16 + col;
-            if (m < rows) {
-              f32x4_t t = load_coherent4(p.partial + ((size_t)(a * p.ksplit) * rows + m) * p.n + n0);
-              for (int s = 1; s < p.ksplit; ++s)
-                t += load_coherent4(p.partial + ((size_t)(a * p.ksplit + s) * rows + m) * p.n + n0);
-              acc[a][mt] = t;
+            for (int i = 0; i < 4; ++i) v[i] = rbf(g4[i]);
+            if (p.out) {
+              uint2 o;
+              o.x = pack2(v[0], v[1]);
+              o.y = pack2(v[2], v[3]);
+              *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
             }
-          }
-      }
-    }
-
-    // ---- epilogues (wave 0 holds the finished tile).
-    if (wave == 0) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + col;
-        if (m >= rows) continue;
-        if constexpr (ARG) {
-          float v[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = rbf(acc[0][mt][i]);
-          if (p.out) {
+            for (int i = 0; i < 4; ++i)
+              if (v[i] > best_v[mt]) {
+                best_v[mt] = v[i];
+                best_i[mt] = n0 + i;
+              }
+          } else if constexpr (RES) {
+            uint16_t *rp = reinterpret_cast<uint16_t *>(p.res) + (size_t)m * p.n + n0;
+            const uint2 r = res_early ? res_v[mt] : *reinterpret_cast<const uint2 *>(rp);
             uint2 o;
-            o.x = pack2(v[0], v[1]);
-            o.y = pack2(v[2], v[3]);
-            *reinterpret_cast<uint2 *>(reinterpret_cast<uint16_t *>(p.out) + (size_t)m * p.n + n0) = o;
-          }
+            o.x = pack2(lo16(r.x) + rbf(g4[0]), hi16(r.x) + rbf(g4[1]));
+            o.y = pack2(lo16(r.y) + rbf(g4[2]), hi16(r.y) + rbf(g4[3]));
+            *reinterpret_cast<uint2 *>(rp) = o;
+          } else if constexpr (GLU) {
+            const f32x4_t u4 = acc[tw * NACC + 1][mt];
+            float o4[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (v[i] > best_v[mt]) {
-              best_v[mt] = v[i];
-              best_i[mt] = n0 + i;
+            for (int i = 0; i < 4; ++i) {
+              const float g = rbf(g4[i]);
+              const float u = rbf(u4[i]);
+              const float sg = rbf(g / (1.0f + expf(-g)));
+              o4[i] = sg * u;
             }
-        } else if constexpr (RES) {
-          uint16_t *rp = reinterpret_cast<uint16_t *>(p.res) + (size_t)m * p.n + n0;
-          const uint2 r = res_early ? res_v[mt] : *reinterpret_cast<const uint2 *>(rp);
-          uint2 o;
-          o.x = pack2(lo16(r.x) + rbf(acc[0][mt][0]), hi16(r.x) + rbf(acc[0][mt][1]));
-          o.y = pack2(lo16(r.y) + rbf(acc[0][mt][2]), hi16(r.y) + rbf(acc[0][mt][3]));
-          *reinterpret_cast<uint2 *>(rp) = o;
-        } else if constexpr (GLU) {
-          float o4[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float g = rbf(acc[0][mt][i]);
-            const float u = rbf(acc[1][mt][i]);
-            const float s = rbf(g / (1.0f + expf(-g)));
-            o4[i] = s * u;
+            uint2 o;
+            o.x = pack2(o4[0], o4[1]);
+            o.y = pack2(o4[2], o4[3]);
+            *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
+          } else {
+            uint2 o;
+            o.x = pack2(g4[0], g4[1]);
+            o.y = pack2(g4[2], g4[3]);
+            *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
           }
-          uint2 o;
-          o.x = pack2(o4[0], o4[1]);
-          o.y = pack2(o4[2], o4[3]);
-          *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
-        } else {
-          uint2 o;
-          o.x = pack2(acc[0][mt][0], acc[0][mt][1]);
-          o.y = pack2(acc[0][mt][2], acc[0][mt][3]);
-          *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
         }
       }
     }
@@ -862,14 +884,24 @@ int gemm_ring(int ksw, uint32_t flags) {
 
 namespace {
 
-template <int MT, int RW>
+template <int MT, int RW, int TW = 1>
 hipError_t launch_direct(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   switch (flags & ~QDEC_NORM_IN) {
-    case 0u: hipLaunchKernelGGL((gemm_kernel<MT, 0u, RW, true>), grid, block, lds, s, p); break;
-    case QDEC_RES_OUT: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT, RW, true>), grid, block, lds, s, p); break;
-    case QDEC_ARGMAX: hipLaunchKernelGGL((gemm_kernel<MT, QDEC_ARGMAX, RW, true>), grid, block, lds, s, p); break;
+    case 0u: hipLaunchKernelGGL((gemm_kernel<MT, 0u, RW, true, kFastRows, false, TW>), grid, block, lds, s, p); break;
+    case QDEC_RES_OUT:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT, RW, true, kFastRows, false, TW>), grid, block, lds, s, p);
+      break;
+    case QDEC_ARGMAX:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_ARGMAX, RW, true, kFastRows, false, TW>), grid, block, lds, s, p);
+      break;
     default: return hipErrorInvalidValue;
   }
+  return hipSuccess;
+}
+
+template <int MT, int RWG, int TW = 1>
+hipError_t launch_direct_glu(const GemmParams &p, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  hipLaunchKernelGGL((gemm_kernel<MT, QDEC_GLU, RWG, true, kFastRows, false, TW>), grid, block, lds, s, p);
   return hipSuccess;
 }
 
@@ -877,27 +909,47 @@ template <int MT, int RW, int RWG>
 hipError_t launch_direct_mt(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
   if (flags & QDEC_GLU) {
     if (p.rw != RWG) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemm_kernel<MT, QDEC_GLU, RWG, true>), grid, block, lds, s, p);
-    return hipSuccess;
+    return launch_direct_glu<MT, RWG>(p, grid, block, lds, s);
   }
   if (p.rw != RW) return hipErrorInvalidValue;
   return launch_direct<MT, RW>(p, flags, grid, block, lds, s);
 }
 
+// Two tiles per wave, two M tiles, no GLU: the rings gemm_ring_direct offers.
+hipError_t launch_direct_tw2(const GemmParams &p, uint32_t flags, dim3 grid, dim3 block, size_t lds, hipStream_t s) {
+  if (flags & QDEC_GLU) return hipErrorInvalidValue;
+  switch (p.rw) {
+    case 5: return launch_direct<2, 5, 2>(p, flags, grid, block, lds, s);
+    case 8: return launch_direct<2, 8, 2>(p, flags, grid, block, lds, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 }  // namespace
 
-int gemm_ring_direct(int mt, uint32_t flags) {
-  // (weights + mt activation fragments) x 4 registers per ring slot stays
-  // near 128 registers.  GLU at two M tiles: 5 slots keep the kernel at
-  // three waves per SIMD, so all 608 gate/up workgroups of Qwen3-4B are
-  // resident at once (8 slots: two per SIMD, a second round of 96; batch 32
-  // on MI355X 3.788 -> 3.770 ms per step).
+int gemm_ring_direct(int mt, uint32_t flags, int tw, int ksw, int groups) {
+  // (tw weight streams + mt activation fragments) x 4 registers per ring
+  // slot stays near 128 registers.  GLU at two M tiles and one tile per
+  // wave: 5 slots keep the kernel at three waves per SIMD, so all 608
+  // gate/up workgroups of Qwen3-4B are resident at once (8 slots: two per
+  // SIMD, a second round of 96; batch 32 on MI355X 3.788 -> 3.770 ms per
+  // step).  Two tiles per wave (no GLU): 5 slots, three waves per SIMD (8
+  // slots take two; QKV at 32 rows 15.3 vs 15.6 us, down 15.0 vs 15.3).  A
+  // wave with several groups of tiles keeps slot r on k step r (mod RW) in
+  // every group, so RW must then divide its k steps; with one group the last
+  // chunk may be ragged.
   const bool glu = (flags & QDEC_GLU) != 0;
+  auto fits = [&](int rw) { return (groups == 1 || ksw % rw == 0) ? rw : 0; };
+  if (tw == 2) {
+    if (mt != 2 || glu) return 0;
+    return fits(5) ? 5 : fits(8);
+  }
+  if (tw != 1) return 0;
   switch (mt) {
-    case 1: return glu ? 10 : 20;
-    case 2: return glu ? 5 : 10;
-    case 3: return glu ? 6 : 8;
-    case 4: return glu ? 4 : 8;
+    case 1: return fits(glu ? 10 : 20);
+    case 2: return fits(glu ? 5 : 10);
+    case 3: return fits(glu ? 6 : 8);
+    case 4: return fits(glu ? 4 : 8);
     default: return 0;
   }
 }
@@ -931,6 +983,8 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
       if (e != hipSuccess) return e;
       q.x = p.xn;
     }
+    if (p.tw == 2) return mt == 2 ? launch_direct_tw2(q, flags, grid, block, lds, s) : hipErrorInvalidValue;
+    if (p.tw != 1) return hipErrorInvalidValue;
     switch (mt) {
       case 1: return launch_direct_mt<1, 20, 10>(q, flags, grid, block, lds, s);
       case 2: return launch_direct_mt<2, 10, 5>(q, flags, grid, block, lds, s);

@@ -47,6 +47,7 @@ struct GemmParams {
   uint16_t *xn;  // xd: pre-pass copy of x (normalised under NORM_IN) in the workspace
   int xt;        // > 0: xd reads x (or xn) in fragment order with this many M tiles
   int xpre;      // xd: run the pre-pass into xn first
+  int tw;        // xd: output tiles per wave (1, or 2 at two M tiles)
   int ofrag;     // > 0: out is written in fragment order with this many M tiles
   // Activations merged from attention chunk partials (x_attn): layout of
   // attn_dev.h, head_dim 128, 4 query heads per kv head.
@@ -66,7 +67,7 @@ struct GemmParams {
 bool gemm_flags_supported(uint32_t flags);
 bool gemm_fast_path(const GemmParams &p, uint32_t flags);
 int gemm_ring(int ksw, uint32_t flags);
-int gemm_ring_direct(int mt, uint32_t flags);
+int gemm_ring_direct(int mt, uint32_t flags, int tw, int ksw, int groups);
 hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStream_t s);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 

@@ -62,6 +62,12 @@ FRAG_ROWS = 17
 # k splits of the down projection from this batch size (see role_plan).
 DOWN_SPLIT = 4
 DOWN_SPLIT_MIN_BATCH = 16
+# Output tiles per workgroup of QKV and down at two M tiles (FRAG_ROWS..32
+# rows).  Paired tiles run two per wave, so each activation fragment a wave
+# loads feeds both (the sums do not change).  MI355X, 32 rows, us per launch
+# (one tile / two): QKV 18.6 / 15.3 with 8 waves (pre-pass included), down
+# 16.1 / 15.0; gate/up (28.4 / 30.4) and O (10.5 / 13.5) keep one.
+WIDE_TILES = 2
 
 
 def round_up(x, m):
@@ -144,6 +150,9 @@ def role_plan(n, k, role, batch=1):
         # pre-pass, or merges four partials per workgroup), so only from
         # DOWN_SPLIT_MIN_BATCH.
         return DOWN_SPLIT, 4, 1
+    if role == "qkv" and batch >= FRAG_ROWS:
+        # two tiles per wave (WIDE_TILES): 192 workgroups, 8 waves each
+        waves = 8
     while ks % waves:
         waves //= 2
     tiles = 1
@@ -288,6 +297,7 @@ class DecodeState:
         self.h = self.hbuf[0]
         self.plans = dict(model.plans)
         self.plans["down"] = role_plan(H, c.inter, "down", batch)
+        self.plans["qkv"] = role_plan(c.n_qkv, H, "qkv", batch)
         ks, _, _ = self.plans["down"]
         self.down_parts = torch.zeros((ks, R, H), dtype=torch.float32, device=dev) if ks > 1 else None
         self.qkv = torch.zeros((R, c.n_qkv), dtype=bf, device=dev)
@@ -375,6 +385,8 @@ class DecodeState:
             a.x_frag = 1 if rows >= FRAG_ROWS else 0
             if self.down_parts is not None:
                 a.parts_out = self.down_parts.data_ptr()
+        if role in ("qkv", "down") and FRAG_ROWS <= rows <= 32 and (a.n // 16) % WIDE_TILES == 0:
+            a.tiles_per_wg = WIDE_TILES
         elif role == "lm":
             self._residual_in(a, c.n_layers, pending)
             a.w = m.emb.data_ptr()

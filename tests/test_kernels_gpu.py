@@ -674,6 +674,78 @@ def test_down_split_merged_by_next_norm_in_call(lib, rows):
     assert one_i[0] == ids[-1]
 
 
+@pytest.mark.parametrize("rows", [17, 24, 32])
+@pytest.mark.parametrize("role", ["qkv", "o", "gate_up", "down", "down_split", "lm"])
+def test_two_tiles_per_wave_bitexact(lib, role, rows):
+    """At two M tiles a workgroup with an even number of output tiles runs two
+    per wave (each activation fragment feeds both; gate/up keeps one per wave
+    and runs its two in turn): every output bit, the split partials and the
+    argmax equal the one-tile-per-workgroup call's, for each role in the
+    engine's layouts and batch-32 plans (fragment-order activations into O
+    and down, SwiGLU written in fragment order, the normalisation pre-pass of
+    QKV, the 8-tile lm_head)."""
+    from qdec import capi
+    from qdec.runtime import LM_TILES_BATCHED, WIDE_TILES, role_plan
+    assert WIDE_TILES == 2
+    n, k, flags, r = {"qkv": (6144, H, capi.NORM_IN, "qkv"), "o": (H, 4096, capi.RES_OUT, "o"),
+                      "gate_up": (I, H, capi.NORM_IN | capi.GLU, "gate_up"), "down": (H, I, capi.RES_OUT, "down"),
+                      "down_split": (H, I, capi.RES_OUT, "down"), "lm": (V, H, capi.NORM_IN | capi.ARGMAX, "lm")}[role]
+    ks, waves, _ = role_plan(n, k, r, batch=1 if role == "down" else 32)
+    assert (ks > 1) == (role == "down_split")
+    seed = (zlib.crc32(role.encode()) + 5 * rows) % 1000
+    mt_rows = (rows + 15) // 16 * 16
+    frag = role in ("o", "down", "down_split")
+    # fragment order covers whole M tiles (lanes past the last row use zeros)
+    x = rnd(mt_rows if frag else rows, k, scale=1.0 if frag else 3.0, seed=seed).to(DEV)
+    W = pack(lib, rnd(2 * n if flags & capi.GLU else n, k, scale=0.02, seed=seed + 1).to(DEV))
+    nw = (1 + 0.2 * rnd(k, seed=seed + 2).float()).to(torch.bfloat16).to(DEV)
+    res0 = rnd(rows, n, scale=2.0, seed=seed + 3).to(DEV)
+    ws = Gemm(lib, flags, n, k)
+
+    def run(tiles):
+        a = capi.GemmArgs(x=x.data_ptr(), w=W.data_ptr(), eps=1e-6, rows=rows, n=n, k=k, flags=flags, ksplit=ks,
+                          waves=waves, tiles_per_wg=tiles, partial=ws.partial.data_ptr(),
+                          counters=ws.counters.data_ptr())
+        outs = []
+        if frag:
+            a.x_frag = 1
+            res = res0.clone()
+            a.res = res.data_ptr()
+            outs.append(res)
+            if ks > 1:
+                parts = torch.full((ks, rows, n), float("nan"), dtype=torch.float32, device=DEV)
+                a.parts_out = parts.data_ptr()
+                outs.append(parts)
+        else:
+            a.norm_w = nw.data_ptr()
+            out = torch.zeros(mt_rows if flags & capi.GLU else rows, n, dtype=torch.bfloat16, device=DEV)
+            a.out = out.data_ptr()
+            outs.append(out)
+            if flags & capi.GLU:
+                a.out_frag = 1
+            if flags & capi.ARGMAX:
+                ids = torch.full((rows,), -1, dtype=torch.int64, device=DEV)
+                a.ids_out = ids.data_ptr()
+                outs.append(ids)
+        pb, _ = lib.gemm_workspace(a)
+        assert pb <= ws.partial.numel() * 4
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        assert int(ws.counters.abs().sum()) == 0
+        return [t.cpu() for t in outs]
+
+    wide = LM_TILES_BATCHED if role == "lm" else WIDE_TILES
+    one, two = run(1), run(wide)
+    for t1, t2 in zip(one, two):
+        if t1.dtype == torch.bfloat16:
+            t1, t2 = t1.view(torch.int16), t2.view(torch.int16)
+        elif t1.dtype == torch.float32:
+            t1, t2 = t1.view(torch.int32), t2.view(torch.int32)
+        assert torch.equal(t1, t2)
+    if role == "down_split":
+        assert not torch.isnan(two[1]).any()  # every partial written
+
+
 # ------------------------------------------------------ invalid inputs, bands
 
 def test_invalid_length_and_id_give_nan_not_stale_output(lib):
