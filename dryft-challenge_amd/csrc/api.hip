@@ -44,8 +44,9 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
   const int ntiles = a->n / 16;
   size_t pb = 0, cb = 0;
   if (a->flags & QDEC_ARGMAX) {
-    pb = 2 * sizeof(float) * (size_t)(ntiles / a->tiles_per_wg) * a->rows;
-    cb = sizeof(uint32_t);
+    // one row: a key per workgroup; more: the arrival counter, then the keys
+    if (a->rows == 1) pb = sizeof(uint64_t) * (size_t)(ntiles / a->tiles_per_wg);
+    cb = 8 + sizeof(uint64_t) * kArgSlots * (size_t)a->rows;
   } else if (a->ksplit > 1 && !a->parts_out) {
     pb = sizeof(float) * (size_t)a->ksplit * a->rows * a->n * ((a->flags & QDEC_GLU) ? 2 : 1);
     cb = sizeof(uint32_t) * (size_t)ntiles;
@@ -112,8 +113,10 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   if (need_scratch && (f & QDEC_NORM_IN) && !a->norm_w) return set_error(QDEC_EINVAL, "qdec_gemm: NORM_IN needs norm_w");
   if (need_scratch && (f & QDEC_RES_OUT) && !a->res) return set_error(QDEC_EINVAL, "qdec_gemm: RES_OUT needs res");
   if (need_scratch && !(f & (QDEC_RES_OUT | QDEC_ARGMAX)) && !a->out) return set_error(QDEC_EINVAL, "qdec_gemm: null out");
-  if (need_scratch && arg && (!a->ids_out || !a->partial || !a->counters))
-    return set_error(QDEC_EINVAL, "qdec_gemm: ARGMAX needs ids_out, partial and counters");
+  if (need_scratch && arg && (!a->ids_out || !a->counters || (a->rows == 1 && !a->partial)))
+    return set_error(QDEC_EINVAL, "qdec_gemm: ARGMAX needs ids_out, counters and (one row) partial");
+  if (arg && ((reinterpret_cast<uintptr_t>(a->counters) & 7u) || (reinterpret_cast<uintptr_t>(a->partial) & 7u)))
+    return set_error(QDEC_EALIGN, "qdec_gemm: ARGMAX needs 8-byte aligned counters and partial");
   if (need_scratch && a->ksplit > 1 && !a->parts_out && (!a->partial || !a->counters))
     return set_error(QDEC_EINVAL, "qdec_gemm: ksplit > 1 needs partial and counters (or parts_out)");
   if (!aligned16(a->x) || !aligned16(a->w) || (a->out && !aligned16(a->out)) || (a->res && !aligned16(a->res)) ||

@@ -64,13 +64,7 @@ __device__ __forceinline__ void block_row_sums(float (&ss)[8], float *s_red, int
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    float v = ss[j];
-    v += shfl_xor(v, 32);
-    v += shfl_xor(v, 16);
-    v += shfl_xor(v, 8);
-    v += shfl_xor(v, 4);
-    v += shfl_xor(v, 2);
-    v += shfl_xor(v, 1);
+    const float v = wave_sum(ss[j]);
     if (lane == 0) s_red[wave * 8 + j] = v;
   }
   __syncthreads();
@@ -717,9 +711,22 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   }
 
   if constexpr (ARG) {
-    // Reduce the 4 column groups of each row, lowest index on equal values.
-    float *pv = p.partial;                                          // [G][rows]
-    int *pi = reinterpret_cast<int *>(p.partial + (size_t)nblk * rows);  // [G][rows]
+    // Each row's best over the workgroup's 4 column groups (lowest index on
+    // equal values) as a 64-bit key (argmax_key: the maximum key is the
+    // argmax), then the row maxima over all workgroups:
+    //  * one row: every workgroup stores its key in the partial workspace
+    //    and the workgroup that arrives last scans them;
+    //  * more rows: every workgroup folds its keys into kArgSlots keys per
+    //    row (slot = workgroup mod kArgSlots, so concurrent workgroups do not
+    //    queue on one address) with device-scope atomic max, kept in the
+    //    counters workspace after the arrival counter and zero between
+    //    calls; the last arriver takes the maximum of each row's slots (a
+    //    scan of rows x workgroups partials would be one serial pass per
+    //    row: 72 us of the lm_head's 213 at 32 rows on MI355X; the atomics
+    //    cost 9 us at one row against the scan's 1).
+    static_assert(kArgSlots == 16, "one 16-lane row of slots per row");
+    uint64_t *keys = reinterpret_cast<uint64_t *>(p.counters + 2);  // [rows][kArgSlots]
+    uint64_t *pk = reinterpret_cast<uint64_t *>(p.partial);         // [nblk], one row
     if (wave == 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
@@ -734,49 +741,58 @@ __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
         }
         const int m = mt * 16 + col;
         if (grp == 0 && m < rows) {
-          store_coherent(pv + (size_t)blk * rows + m, best_v[mt]);
-          store_coherent_i(pi + (size_t)blk * rows + m, best_i[mt]);
+          const uint64_t key = argmax_key(best_v[mt], best_i[mt]);
+          if (rows == 1)
+            st64_dev(pk + blk, key);
+          else
+            __hip_atomic_fetch_max(keys + (size_t)m * kArgSlots + (blk & (kArgSlots - 1)), key, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
     if (!arrive_last(p.counters, (uint32_t)nblk, s_flag)) return;
-    float *sv = s_red;                             // [waves]
-    int *si = reinterpret_cast<int *>(s_red + 8);  // [waves]
-    for (int m = 0; m < rows; ++m) {
-      float bv = -__builtin_huge_valf();
-      int bi = 0x7fffffff;
-      for (int g = tid; g < nblk; g += nthr) {
-        const float v = load_coherent(pv + (size_t)g * rows + m);
-        const int i = load_coherent_i(pi + (size_t)g * rows + m);
-        if (v > bv || (v == bv && i < bi)) {
-          bv = v;
-          bi = i;
-        }
-      }
+    if (rows == 1) {
+      uint64_t b4[4] = {0ull, 0ull, 0ull, 0ull};
+      for (int g = tid; g < nblk; g += 4 * nthr) {
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off, kWave);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
+        for (int u = 0; u < 4; ++u) {
+          const int gu = g + u * nthr;
+          const uint64_t kk = gu < nblk ? ld64_dev(pk + gu) : 0ull;
+          b4[u] = kk > b4[u] ? kk : b4[u];
         }
       }
-      if (lane == 0) {
-        sv[wave] = bv;
-        si[wave] = bi;
-      }
+      uint64_t best = b4[0] > b4[1] ? b4[0] : b4[1];
+      const uint64_t b23 = b4[2] > b4[3] ? b4[2] : b4[3];
+      best = row16_max(b23 > best ? b23 : best);
+      uint64_t *s_key = reinterpret_cast<uint64_t *>(s_red);  // [waves][4]
+      if ((lane & 15) == 0) s_key[wave * 4 + (lane >> 4)] = best;
       __syncthreads();
       if (tid == 0) {
-        for (int w2 = 1; w2 < nw; ++w2)
-          if (sv[w2] > bv || (sv[w2] == bv && si[w2] < bi)) {
-            bv = sv[w2];
-            bi = si[w2];
-          }
-        p.ids_out[m] = (int64_t)bi;
-        if (p.lens_inc) p.lens_inc[m] += 1;
+        for (int i = 1; i < 4 * nw; ++i) best = s_key[i] > best ? s_key[i] : best;
+        p.ids_out[0] = (int64_t)argmax_index(best);
+        if (p.lens_inc) p.lens_inc[0] += 1;
       }
-      __syncthreads();
+      return;
+    }
+    // A wave takes 4 rows per pass (16 lanes, one slot each), four passes'
+    // loads in flight at once.
+    for (int j0 = 0; j0 * nw * 4 < rows; j0 += 4) {
+      uint64_t kv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = ((j0 + j) * nw + wave) * 4 + (lane >> 4);
+        kv[j] = m < rows ? ld64_dev(keys + (size_t)m * kArgSlots + (lane & 15)) : 0ull;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = ((j0 + j) * nw + wave) * 4 + (lane >> 4);
+        if (m < rows) st64_dev(keys + (size_t)m * kArgSlots + (lane & 15), 0ull);
+        const uint64_t best = row16_max(kv[j]);
+        if ((lane & 15) == 0 && m < rows) {
+          p.ids_out[m] = (int64_t)argmax_index(best);
+          if (p.lens_inc) p.lens_inc[m] += 1;
+        }
+      }
     }
   }
 }

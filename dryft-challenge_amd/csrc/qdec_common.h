@@ -155,8 +155,61 @@ __device__ __forceinline__ bool arrive_last(uint32_t *counter, uint32_t expected
   return *lds_flag != 0u;
 }
 
+// Argmax as an unsigned maximum: the high word orders fp32 values (non-NaN;
+// -0 counts as +0), the low word is the complement of the index, so equal
+// values keep the lowest index.  A row whose every value is -inf or NaN
+// keeps its initial (-inf, 0x7fffffff) and decodes to that index.
+__device__ __forceinline__ uint64_t argmax_key(float v, int idx) {
+  uint32_t b = __float_as_uint(v == 0.f ? 0.f : v);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)b << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ int argmax_index(uint64_t key) { return (int)(0xffffffffu - (uint32_t)key); }
+
 // Cross-lane helpers (wave64).
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, kWave); }
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, true);
+  return ((uint64_t)hi << 32) | lo;
+}
+// Maximum over each 16-lane row of the wave (all lanes active), in every
+// lane of the row.
+__device__ __forceinline__ uint64_t row16_max(uint64_t v) {
+  uint64_t o = dpp_u64<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = o > v ? o : v;
+  o = dpp_u64<0x4E>(v);            // quad_perm [2,3,0,1]
+  v = o > v ? o : v;
+  o = dpp_u64<0x141>(v);           // row_half_mirror
+  v = o > v ? o : v;
+  o = dpp_u64<0x140>(v);           // row_mirror
+  return o > v ? o : v;
+}
+
+// v of the lane chosen by DPP control CTRL (every lane active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Sum over the 64 lanes of a wave (all active), the same bits in every lane,
+// without a round trip through the LDS crossbar: partners lane^1 and lane^2
+// (quad permutations), then the lane mirrored within 8 and within 16 --
+// after the quad steps every quad holds its quad sum, so the mirrored lane
+// holds the lane^4 (then lane^8) partner's value -- then the four 16-lane row
+// sums as (r0 + r1) + (r2 + r3).  The pairing of a full xor butterfly.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
 
 // Per-head RMSNorm (weight w) and RoPE of one 128-channel head row spread
 // over a wavefront: this lane holds channels 2*lane and 2*lane+1 (raw, w,
@@ -168,13 +221,7 @@ __device__ __forceinline__ uint32_t head_norm_rope2(uint32_t raw, uint32_t w, ui
                                                     float eps) {
   const int lane = threadIdx.x & 63;
   const float x0 = lo16(raw), x1 = hi16(raw);
-  float ss = x0 * x0 + x1 * x1;
-  ss += shfl_xor(ss, 32);
-  ss += shfl_xor(ss, 16);
-  ss += shfl_xor(ss, 8);
-  ss += shfl_xor(ss, 4);
-  ss += shfl_xor(ss, 2);
-  ss += shfl_xor(ss, 1);
+  const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float rstd = 1.0f / sqrtf(ss / 128.0f + eps);
   const float y0 = rbf(lo16(w) * rbf(x0 * rstd));
   const float y1 = rbf(hi16(w) * rbf(x1 * rstd));

@@ -142,8 +142,9 @@ typedef struct {
   void *out;            /* [rows, n] bf16 (plain, GLU, optional with ARGMAX) */
   void *res;            /* [rows, n] bf16 residual (RES_OUT) */
   const void *norm_w;   /* [k] bf16 (NORM_IN) */
-  float *partial;       /* split-K / argmax scratch (qdec_gemm_workspace) */
-  uint32_t *counters;   /* zeroed arrival counters (qdec_gemm_workspace) */
+  float *partial;       /* split-K / pre-pass scratch (qdec_gemm_workspace) */
+  uint32_t *counters;   /* zeroed arrival counters and argmax keys (qdec_gemm_workspace;
+                           8-byte aligned with ARGMAX); zero again on return */
   int64_t *ids_out;     /* [rows] (ARGMAX) */
   int32_t *lens_inc;    /* [rows] or NULL (ARGMAX) */
   float eps;

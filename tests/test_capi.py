@@ -90,7 +90,10 @@ def test_gemm_workspace_sizes(qlib):
     assert pb == 2 * 3 * 2560 * 4 and cb == 160 * 4
     pb, cb = qlib.gemm_workspace(_gemm(flags=capi.NORM_IN | capi.ARGMAX, n=151936, k=2560, rows=2,
                                        tiles_per_wg=4))
-    assert pb == 2 * 4 * (9496 // 4) * 2 and cb == 4
+    assert pb == 0 and cb == 8 + 8 * 16 * 2  # arrival counter, 16 64-bit argmax keys per row
+    pb, cb = qlib.gemm_workspace(_gemm(flags=capi.NORM_IN | capi.ARGMAX, n=151936, k=2560, rows=1,
+                                       tiles_per_wg=4))
+    assert pb == 8 * (9496 // 4) and cb == 8 + 8 * 16  # one row: a 64-bit key per workgroup
     pb, cb = qlib.gemm_workspace(_gemm(flags=capi.NORM_IN, n=6144, k=2560))
     assert pb == 0 and cb == 0
 

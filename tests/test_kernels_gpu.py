@@ -837,7 +837,7 @@ def test_gemm_epilogues_stay_in_bounds(lib, rows):
                        parts_out=parts.data_ptr())
     assert lib.gemm_workspace(d2) == (0, 0)
     lib.gemm(d2, stream())
-    # lm_head + argmax (argmax partials and, from 9 rows, the normalised rows in the workspace)
+    # lm_head + argmax (argmax keys in the counters and, from 9 rows, the normalised rows in the workspace)
     Vs = 4096
     E = pack(lib, rnd(Vs, H, scale=0.02, seed=66).to(DEV))
     ids_whole, ids = banded(rows, dtype=torch.int64, fill=-7)
@@ -858,7 +858,7 @@ def test_gemm_epilogues_stay_in_bounds(lib, rows):
     assert bands_intact(cnt_whole, max(cb, 4) // 4, fill=0) and int(cnt.abs().sum()) == 0, "counters"
     assert bands_intact(ids_whole, rows, fill=-7) and bool((ids >= 0).all()), "argmax ids"
     assert bands_intact(lws_whole, max(lpb, 4) // 4), "argmax workspace"
-    assert bands_intact(lcnt_whole, max(lcb, 4) // 4, fill=0), "argmax counters"
+    assert bands_intact(lcnt_whole, max(lcb, 4) // 4, fill=0) and int(lcnt.abs().sum()) == 0, "argmax counters"
 
 
 @pytest.mark.parametrize("B,T,lens,cap,chunk,waves,frag,partials", [
