@@ -820,6 +820,76 @@ __global__ void __launch_bounds__(512) rownorm_kernel(const uint16_t *__restrict
     return;
   }
   const uint16_t *xrow = X + (size_t)m * k;
+  if (nvec <= 2 * nthr && nparts <= kMergeParts) {
+    // The whole row in registers, two vectors per thread: every load (x,
+    // the pending partials, the norm weights) is issued before the first is
+    // used, and the row is read once.  Same statistic order and roundings
+    // as the loop below.
+    uint4 xv[2], wv[2];
+    f32x4_t pv[2][kMergeParts][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int v = tid + j * nthr;
+      const int vv = v < nvec ? v : 0;
+      xv[j] = *reinterpret_cast<const uint4 *>(xrow + 8 * vv);
+      if (parts) {
+        const float *q = parts + (size_t)m * k + 8 * vv;
+#pragma unroll
+        for (int part = 0; part < kMergeParts; ++part) {
+          const float *qp = q + (size_t)(part < nparts ? part : 0) * rows * k;
+          pv[j][part][0] = *reinterpret_cast<const f32x4_t *>(qp);
+          pv[j][part][1] = *reinterpret_cast<const f32x4_t *>(qp + 4);
+        }
+      }
+      wv[j] = do_norm ? *reinterpret_cast<const uint4 *>(norm_w + 8 * vv) : zero4();
+    }
+    float ss[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss[j] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int v = tid + j * nthr;
+      if (v >= nvec) continue;
+      if (parts) {
+        // bf16(x + bf16(((p0 + p1) + p2) + p3)): merge_res8's order and rounding
+        f32x4_t s0 = pv[j][0][0], s1 = pv[j][0][1];
+#pragma unroll
+        for (int part = 1; part < kMergeParts; ++part)
+          if (part < nparts) {
+            s0 += pv[j][part][0];
+            s1 += pv[j][part][1];
+          }
+        const uint4 x = xv[j];
+        uint4 o;
+        o.x = pack2(lo16(x.x) + rbf(s0[0]), hi16(x.x) + rbf(s0[1]));
+        o.y = pack2(lo16(x.y) + rbf(s0[2]), hi16(x.y) + rbf(s0[3]));
+        o.z = pack2(lo16(x.z) + rbf(s1[0]), hi16(x.z) + rbf(s1[1]));
+        o.w = pack2(lo16(x.w) + rbf(s1[2]), hi16(x.w) + rbf(s1[3]));
+        xv[j] = o;
+        *reinterpret_cast<uint4 *>(xmerged + (size_t)m * k + 8 * v) = o;
+      }
+      float f[8];
+      unpack8(xv[j], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss[0] += f[e] * f[e];
+    }
+    if (!do_norm) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int v = tid + j * nthr;
+        if (v < nvec) *reinterpret_cast<uint4 *>(dst(v)) = xv[j];
+      }
+      return;
+    }
+    block_row_sums(ss, s_red, 1, s_rstd, 0, k, eps);
+    const float rs = s_rstd[0];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int v = tid + j * nthr;
+      if (v < nvec) *reinterpret_cast<uint4 *>(dst(v)) = norm8(xv[j], wv[j], rs);
+    }
+    return;
+  }
   if (parts) {
     // Apply the pending split residual update once, into xmerged; both
     // loops below then read the merged row (each thread its own vectors).
