@@ -185,12 +185,28 @@ def attn_chunk(batch, nkv, cap):
     slots (10.4 us at 128 vs 12.0 us at 256 for 640 cached slots; 21.5 vs
     17.1 us at 4000; with two attention workgroups per CU a batch-1 step at
     512..766 cached slots takes 2.187 ms at 96, 2.203 at 128, 2.250 at 64,
-    2.241 at 192; at batch 8, 512 stays ahead of 256, 384 and 768)."""
+    2.241 at 192; at batch 8, 512 stays ahead of 256, 384 and 768).
+
+    From batch 8 (8-wave workgroups, one per CU) every workgroup of the
+    launch should be resident at once: 512-slot chunks (all 16 blocks in
+    flight, two per wave) while batch x kv heads x chunks fits the 256 CUs,
+    else the cache in as many equal chunks as fit, down to one.  Attention
+    alone, 8 kv heads, us per launch: batch 16 at 4200 cached slots 69.0 in
+    one chunk, 50.5 in two (57.4 in four, 64.8 in three); batch 16 at 1300
+    slots 25.4 / 23.5; batch 12 at 1300 slots 24.4 in one, 33.0 in 512-slot
+    chunks (288 workgroups: two rounds) and 21.8 in two; batch 10 at 1300
+    slots 32.4 in 512-slot chunks, 19.1 in 544; batch 8 at 4200 slots 46.2
+    in 512-slot chunks, 30.3 in 1120; batch 20, 24 and 32 stay faster in one
+    chunk (71.6, 74.9, 86.7 against 86.8, 89.2, 97.5 in two)."""
     cap = round_up(cap, 32)
+    if batch >= 8:
+        pairs = batch * nkv
+        if pairs * -(-cap // 512) <= 256:
+            return min(cap, 512)
+        n_chunks = max(1, 256 // pairs)
+        return round_up(-(-cap // n_chunks), 32)
     if batch * nkv >= 128:
         return cap
-    if batch >= 8:
-        return min(cap, 512)
     return min(cap, 96 if batch == 1 and cap <= 1024 else 256)
 
 

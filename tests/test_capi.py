@@ -138,7 +138,7 @@ def test_other_validation(qlib):
 
 
 def test_role_plans_do_not_depend_on_rows():
-    from qdec.runtime import attn_chunk, role_plan
+    from qdec.runtime import attn_chunk, role_plan, round_up
     for role, n, k in (("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 9728, 2560),
                        ("down", 2560, 9728), ("lm", 151936, 2560)):
         ks, w, t = role_plan(n, k, role)
@@ -158,6 +158,15 @@ def test_role_plans_do_not_depend_on_rows():
     for b, cap in ((1, 800), (4, 1568), (32, 4384)):
         c = attn_chunk(b, 8, cap)
         assert c % 32 == 0 and 64 <= c <= cap
+    # from batch 8 every workgroup resident at once (8 kv heads, 256 CUs)
+    assert attn_chunk(8, 8, 1568) == 512 and attn_chunk(32, 8, 4384) == 4384
+    assert attn_chunk(16, 8, 4384) == 2208 and attn_chunk(16, 8, 1568) == 800
+    assert attn_chunk(12, 8, 1568) == 800 and attn_chunk(20, 8, 4384) == 4384
+    for b in range(8, 65):
+        for cap in (64, 544, 1568, 4384, 8192):
+            c = attn_chunk(b, 8, cap)
+            assert c % 32 == 0 and c <= round_up(cap, 32)
+            assert b * 8 * -(-round_up(cap, 32) // c) <= max(256, b * 8)
 
 
 def _pgemm(**kw):
