@@ -51,23 +51,25 @@ PREFILL_ROW_TILE = 256
 LM_TILES_BATCHED = 8
 # Plain decode up to this batch merges attention chunks in the O projection.
 MERGE_IN_O_MAX_BATCH = 4
-# From this many rows per call (two M tiles) the attention output and the
-# SwiGLU output are written in MFMA fragment order and read that way by the O
-# and down projections: one contiguous KiB per fragment load and no re-layout
-# pre-pass (same-box A/B: batch 32 3.86 vs 4.09 ms per step; at batch 8, one
-# M tile, row-major stays faster, 3.18 vs 3.23 ms).
-FRAG_ROWS = 17
+# From this many rows per call the attention output and the SwiGLU output
+# are written in MFMA fragment order and read that way by the O and down
+# projections: one contiguous KiB per fragment load and no re-layout
+# pre-pass.  Same-box A/B, ms per step (1024-token prompts): batch 16 3.61
+# with fragment order from 17 rows, 3.11 from 9; batch 12 3.18 / 3.15;
+# batch 8 (8-row plain steps) 2.96 / 2.95; batch 32 3.86 vs 4.09 row-major.
+FRAG_ROWS = 9
 # Loss-free speculation needs identical arithmetic in the plain and verify
 # steps, so attention chunking depends on (batch, capacity) only.
 # k splits of the down projection from this batch size (see role_plan).
 DOWN_SPLIT = 4
 DOWN_SPLIT_MIN_BATCH = 16
-# Output tiles per workgroup of QKV and down at two M tiles (FRAG_ROWS..32
+# Output tiles per workgroup of QKV and down at two M tiles (WIDE_MIN_ROWS..32
 # rows).  Paired tiles run two per wave, so each activation fragment a wave
 # loads feeds both (the sums do not change).  MI355X, 32 rows, us per launch
 # (one tile / two): QKV 18.6 / 15.3 with 8 waves (pre-pass included), down
 # 16.1 / 15.0; gate/up (28.4 / 30.4) and O (10.5 / 13.5) keep one.
 WIDE_TILES = 2
+WIDE_MIN_ROWS = 17
 
 
 def round_up(x, m):
@@ -150,7 +152,7 @@ def role_plan(n, k, role, batch=1):
         # pre-pass, or merges four partials per workgroup), so only from
         # DOWN_SPLIT_MIN_BATCH.
         return DOWN_SPLIT, 4, 1
-    if role == "qkv" and batch >= FRAG_ROWS:
+    if role == "qkv" and batch >= WIDE_MIN_ROWS:
         # two tiles per wave (WIDE_TILES): 192 workgroups, 8 waves each
         waves = 8
     while ks % waves:
@@ -401,7 +403,7 @@ class DecodeState:
             a.x_frag = 1 if rows >= FRAG_ROWS else 0
             if self.down_parts is not None:
                 a.parts_out = self.down_parts.data_ptr()
-        if role in ("qkv", "down") and FRAG_ROWS <= rows <= 32 and (a.n // 16) % WIDE_TILES == 0:
+        if role in ("qkv", "down") and WIDE_MIN_ROWS <= rows <= 32 and (a.n // 16) % WIDE_TILES == 0:
             a.tiles_per_wg = WIDE_TILES
         elif role == "lm":
             self._residual_in(a, c.n_layers, pending)
