@@ -40,7 +40,7 @@ if _HERE not in sys.path:
 
 from qdec import capi, selfcheck  # noqa: E402
 from qdec.checkpoint import load_config, load_tensors  # noqa: E402
-from qdec.runtime import DecodeState, DeviceModel  # noqa: E402
+from qdec.runtime import DecodeState, DeviceModel, max_rows_per_seq  # noqa: E402
 
 # Decode steps queued ahead of the one being handed to the caller (as the
 # reference, engine/engine.py:66); one before the first token.
@@ -55,8 +55,9 @@ def spec_k(batch):
     """Drafts per sequence per verify iteration: up to SPEC_K_MAX, and few
     enough that the batch's verify rows fit one 16-row MFMA tile (the GEMMs'
     fast path), so a verify iteration costs about a plain step.  0 = no
-    speculation at this batch size."""
-    return max(0, min(SPEC_K_MAX, 16 // batch - 1))
+    speculation at this batch size.  The verify pass's k + 1 rows per
+    sequence also stay within what the state's attention takes."""
+    return max(0, min(SPEC_K_MAX, 16 // batch - 1, max_rows_per_seq(batch) - 1))
 
 
 def _log(message):

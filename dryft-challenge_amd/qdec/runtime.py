@@ -166,15 +166,32 @@ def role_plan(n, k, role, batch=1):
     return ksplit, waves, tiles
 
 
+# From this batch the attention runs 8 waves per workgroup with the
+# residency chunking of attn_chunk.
+ATTN8_MIN_BATCH = 6
+# Rows per sequence an 8-wave attention workgroup takes (two M tiles of
+# query rows per kv head).
+ATTN8_MAX_T = 8
+
+
 def attn_waves(batch):
-    """Wavefronts per attention workgroup: 8 from batch 8, so all blocks of
-    a 512-slot chunk (or two per wave of a whole-cache one) are in flight at
-    once (MI355X, ms/step: batch 8 3.100 -> 3.076, batch 32 6.129 -> 6.098),
-    else 4.  A row's arithmetic depends on the count, so it is a function of
-    the batch alone: plain and speculative states of one batch agree.  8
-    waves take at most 8 rows per sequence, and a state of batch 8 or more
-    has at most GEMM_MAX_ROWS // 8 = 8."""
-    return 8 if batch >= 8 else 4
+    """Wavefronts per attention workgroup: 8 from ATTN8_MIN_BATCH, so all
+    blocks of a 512-slot chunk (or two per wave of a whole-cache one) are in
+    flight at once (MI355X, ms/step: batch 8 3.100 -> 3.076, batch 32 6.129
+    -> 6.098; with 1024-token prompts batch 6 2.970 -> 2.893 and batch 7
+    3.070 -> 2.978, but batch 5 2.717 -> 2.790 and batch 4 2.58 -> 2.65), else
+    4.  A row's arithmetic depends on the count, so it is a function of the
+    batch alone: plain and speculative states of one batch agree.  8 waves
+    take at most ATTN8_MAX_T rows per sequence (max_rows_per_seq)."""
+    return 8 if batch >= ATTN8_MIN_BATCH else 4
+
+
+def max_rows_per_seq(batch, requested=ATTN_MAX_T):
+    """Rows per sequence a state of ``batch`` runs per call (verify passes,
+    prefill through the decode kernels): at most ``requested``, ATTN_MAX_T,
+    GEMM_MAX_ROWS in all, and ATTN8_MAX_T when the attention runs 8 waves."""
+    cap = ATTN8_MAX_T if attn_waves(batch) == 8 else ATTN_MAX_T
+    return max(1, min(requested, cap, GEMM_MAX_ROWS // batch))
 
 
 def attn_chunk(batch, nkv, cap):
@@ -189,7 +206,7 @@ def attn_chunk(batch, nkv, cap):
     512..766 cached slots takes 2.187 ms at 96, 2.203 at 128, 2.250 at 64,
     2.241 at 192; at batch 8, 512 stays ahead of 256, 384 and 768).
 
-    From batch 8 (8-wave workgroups, one per CU) every workgroup of the
+    From ATTN8_MIN_BATCH (8-wave workgroups, one per CU) every workgroup of the
     launch should be resident at once: 512-slot chunks (all 16 blocks in
     flight, two per wave) while batch x kv heads x chunks fits the 256 CUs,
     else the cache in as many equal chunks as fit, down to one.  Attention
@@ -201,7 +218,7 @@ def attn_chunk(batch, nkv, cap):
     in 512-slot chunks, 30.3 in 1120; batch 20, 24 and 32 stay faster in one
     chunk (71.6, 74.9, 86.7 against 86.8, 89.2, 97.5 in two)."""
     cap = round_up(cap, 32)
-    if batch >= 8:
+    if batch >= ATTN8_MIN_BATCH:
         pairs = batch * nkv
         if pairs * -(-cap // 512) <= 256:
             return min(cap, 512)
@@ -292,7 +309,7 @@ class DecodeState:
         self.model, self.lib = model, model.lib
         self.batch = batch
         self.cap = round_up(capacity, 32)
-        self.max_t = max(1, min(max_t, ATTN_MAX_T, GEMM_MAX_ROWS // batch))
+        self.max_t = max_rows_per_seq(batch, max_t)
         if batch > GEMM_MAX_ROWS:
             raise ValueError(f"batch {batch} > {GEMM_MAX_ROWS} rows per step")
         self.max_rows = batch * self.max_t

@@ -162,7 +162,7 @@ def test_role_plans_do_not_depend_on_rows():
     assert attn_chunk(8, 8, 1568) == 512 and attn_chunk(32, 8, 4384) == 4384
     assert attn_chunk(16, 8, 4384) == 2208 and attn_chunk(16, 8, 1568) == 800
     assert attn_chunk(12, 8, 1568) == 800 and attn_chunk(20, 8, 4384) == 4384
-    for b in range(8, 65):
+    for b in range(6, 65):
         for cap in (64, 544, 1568, 4384, 8192):
             c = attn_chunk(b, 8, cap)
             assert c % 32 == 0 and c <= round_up(cap, 32)

@@ -14,12 +14,12 @@ sys.path.insert(0, os.path.join(ROOT, "dryft-challenge_amd"))
 @pytest.mark.parametrize("batch", list(range(1, 65)))
 def test_attention_waves_fit_every_state_of_a_batch(batch):
     from engine import spec_k
-    from qdec.runtime import ATTN_MAX_T, GEMM_MAX_ROWS, attn_waves
+    from qdec.runtime import attn_waves, max_rows_per_seq
     waves = attn_waves(batch)
     assert waves in (4, 8)
 
     def max_t(requested):  # DecodeState's clamp
-        return max(1, min(requested, ATTN_MAX_T, GEMM_MAX_ROWS // batch))
+        return max_rows_per_seq(batch, requested)
 
     k = spec_k(batch)
     plain, spec = max_t(16), max_t(k + 1 if k else 16)
