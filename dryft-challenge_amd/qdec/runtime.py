@@ -226,7 +226,23 @@ def attn_chunk(batch, nkv, cap):
         return round_up(-(-cap // n_chunks), 32)
     if batch * nkv >= 128:
         return cap
-    return min(cap, 96 if batch == 1 and cap <= 1024 else 256)
+    # Below ATTN8_MIN_BATCH (4 waves, two workgroups per CU): 96 slots at
+    # batch 1 up to 1024 slots, else about an eighth of the cache -- at batch
+    # 1 at least 160 slots and at most the larger of 320 and a sixteenth,
+    # from batch 2 at least 256.  Whole step, ms (batch 1): 1024-token
+    # prompts 2.212 at 256, 2.157 at 192; 2048 tokens 2.279 at 256, 2.222 at
+    # 288, 2.234 at 320; 4096 tokens 2.397 at 256, 2.310 at 320 (2.330 at
+    # 384, 2.375 at 448); 8192 tokens 2.553 at 320, 2.513 at 512, 2.562 at
+    # 768; 512 tokens 2.125 at 96, 2.136 at 128, 2.158 at 192.  Batch 2 at
+    # 4096 tokens 2.823 at 256, 2.499 at 576; batch 3 at 2048 tokens 2.768
+    # at 256, 2.517 at 320; batch 4 at 4096 tokens 3.602 at 256, 2.859 at
+    # 576, at 1024 tokens 2.59 at 256 against 2.60-2.97 at 128-512.
+    if batch == 1 and cap <= 1024:
+        return min(cap, 96)
+    eighth = round_up(-(-cap // 8), 32)
+    if batch == 1:
+        return min(cap, max(160, min(eighth, max(320, round_up(-(-cap // 16), 32)))))
+    return min(cap, max(256, eighth))
 
 
 class DeviceModel:

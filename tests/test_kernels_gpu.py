@@ -480,6 +480,8 @@ def attn_oracle(c, B, T):
     (3, 1, [5, 64, 129], 192, 128, 8),
     (2, 8, [0, 170], 256, 64, 8),
     (8, 2, [1000, 1017, 31, 64, 0, 511, 512, 700], 1056, 512, 8),
+    (2, 1, [4000, 3100], 4384, 576, 4),
+    (1, 3, [2200], 2336, 320, 4),
 ])
 def test_attention_vs_oracle(lib, B, T, lens, cap, chunk, waves):
     c = attn_case(lib, B, T, lens, cap, chunk, seed=B * 100 + T * 10 + lens[0], waves=waves)
