@@ -340,6 +340,94 @@ int scratch_on_current_device(hipStream_t s, unsigned char **out) {
 
 }  // namespace
 
+// ------------------------------------------------- one layer per launch
+// Everything a qdec_layer call launches, from its arguments: each stage's
+// plan (the same validation as its own call), checked against the stage
+// plans layer_kernel is compiled for; the launch's workgroups and LDS.
+namespace {
+
+constexpr size_t kLayerLdsMax = 80u << 10;  // two workgroups per CU
+static_assert(sizeof(LayerParams) <= QDEC_LAYER_PLAN_BYTES, "plan fits its buffer");
+static_assert(sizeof(LayerCtl) == QDEC_LAYER_CTL_BYTES, "ctl layout");
+
+uint64_t fnv1a(const void *p, size_t n) {
+  const unsigned char *b = static_cast<const unsigned char *>(p);
+  uint64_t h = 1469598103934665603ull;
+  for (size_t i = 0; i < n; ++i) h = (h ^ b[i]) * 1099511628211ull;
+  return h;
+}
+
+int plan_layer(const qdec_layer_args *a, LayerParams *L, int *workgroups, size_t *lds) {
+  if (!a || !a->qkv || !a->attn || !a->o || !a->gate_up || !a->down)
+    return set_error(QDEC_EINVAL, "qdec_layer: null argument");
+  if (!a->plan || !aligned16(a->plan)) return set_error(QDEC_EALIGN, "qdec_layer: plan must be 16-byte aligned");
+  if (!a->ctl || (reinterpret_cast<uintptr_t>(a->ctl) & 7u)) return set_error(QDEC_EALIGN, "qdec_layer: ctl must be 8-byte aligned");
+  const qdec_attn_args &at = *a->attn;
+  if (at.t_rows != 1 || at.waves != 4 || at.out_partials != 1 || at.batch < 1 || at.batch > kLayerMaxRows)
+    return set_error(QDEC_EUNSUPPORTED,
+                     "qdec_layer: attention t_rows %d waves %d out_partials %d batch %d (1, 4, 1, at most %d)",
+                     at.t_rows, at.waves, at.out_partials, at.batch, kLayerMaxRows);
+  if (a->o->x_attn != a->attn) return set_error(QDEC_EUNSUPPORTED, "qdec_layer: o must merge the attention (x_attn == attn)");
+  memset(L, 0, sizeof *L);  // the key hashes the bytes, padding included
+  const qdec_gemm_args *ga[4] = {a->qkv, a->o, a->gate_up, a->down};
+  static const char *const names[4] = {"qkv", "o", "gate_up", "down"};
+  static const uint32_t flags[4] = {QDEC_NORM_IN, QDEC_RES_OUT, QDEC_NORM_IN | QDEC_GLU, QDEC_RES_OUT};
+  static const int rings[4] = {20, 16, 10, 20};
+  for (int i = 0; i < 4; ++i) {
+    const int rc = plan_gemm(ga[i], &L->g[i], true);
+    if (rc != QDEC_OK) return rc;
+    const GemmParams &p = L->g[i];
+    const bool direct = i == 3;
+    if (ga[i]->flags != flags[i] || p.rows != at.batch || p.waves != 4 || p.ksplit != 1 || p.rw != rings[i] ||
+        (p.xd != 0) != direct || (!direct && !p.xfast) || p.xt || p.xpre || p.tw != 1 || p.ofrag || p.xparts ||
+        p.parts_out || (p.amerge != 0) != (i == 1))
+      return set_error(QDEC_EUNSUPPORTED,
+                       "qdec_layer: %s plan (flags 0x%x rows %d waves %d ksplit %d ring %d direct %d) is not the "
+                       "layer kernel's",
+                       names[i], ga[i]->flags, p.rows, p.waves, p.ksplit, p.rw, p.xd);
+    L->nblk[i] = (p.n / 16 / p.tiles_per_wg) * p.ksplit;
+  }
+  const int rc = plan_attn(a->attn, &L->a, true);
+  if (rc != QDEC_OK) return rc;
+  size_t need = layer_attn_lds_bytes();
+  for (int i = 0; i < 4; ++i) need = std::max(need, L->g[i].lds_bytes);
+  if (need > kLayerLdsMax) return set_error(QDEC_EUNSUPPORTED, "qdec_layer: %zu B of LDS per workgroup", need);
+  // Workgroups that fit at once, queried once per device (the first call,
+  // qdec_layer_prepare, runs outside stream capture).
+  static std::mutex mu;
+  static int wgs[kMaxDevices];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return set_error(QDEC_ENODEV, "qdec_layer: no current HIP device (or id >= %d)", kMaxDevices);
+  }
+  int maxw = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (!wgs[dev]) {
+      const hipError_t e = layer_workgroups(kLayerLdsMax, &wgs[dev]);
+      if (e != hipSuccess) {
+        wgs[dev] = 0;
+        return set_error(QDEC_ELAUNCH, "qdec_layer: occupancy query: %s", hipGetErrorString(e));
+      }
+    }
+    maxw = wgs[dev];
+  }
+  const int w = a->workgroups ? a->workgroups : maxw;
+  if (w < 1 || w > maxw)
+    return set_error(QDEC_EINVAL, "qdec_layer: workgroups %d not in [1, %d] (all resident at once)", a->workgroups, maxw);
+  int blocks = L->a.nchunks * L->a.nkv * L->a.batch;
+  for (int i = 0; i < 4; ++i) blocks = std::max(blocks, L->nblk[i]);
+  if (blocks > w)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_layer: a stage has %d blocks for %d workgroups", blocks, w);
+  L->key = fnv1a(L, sizeof *L) | 1ull;  // never 0, the value of zeroed memory
+  *workgroups = w;
+  *lds = need;
+  return QDEC_OK;
+}
+
+}  // namespace
+
 }  // namespace qdec
 
 using namespace qdec;
@@ -451,6 +539,28 @@ int qdec_attn_noalloc(const qdec_attn_args *a, qdec_stream_t stream) {
   b.counters = reinterpret_cast<uint32_t *>(base);
   b.partial = reinterpret_cast<float *>(base + QDEC_NOALLOC_COUNTER_BYTES);
   return qdec_attn(&b, stream);
+}
+
+int qdec_layer_prepare(const qdec_layer_args *a) {
+  LayerParams L;
+  int w = 0;
+  size_t lds = 0;
+  const int rc = plan_layer(a, &L, &w, &lds);
+  if (rc != QDEC_OK) return rc;
+  const hipError_t e = hipMemcpy(a->plan, &L, sizeof L, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return set_error(QDEC_ELAUNCH, "qdec_layer_prepare: copy of the plan: %s", hipGetErrorString(e));
+  return QDEC_OK;
+}
+
+int qdec_layer(const qdec_layer_args *a, qdec_stream_t stream) {
+  LayerParams L;
+  int w = 0;
+  size_t lds = 0;
+  const int rc = plan_layer(a, &L, &w, &lds);
+  if (rc != QDEC_OK) return rc;
+  return launch_status(launch_layer(static_cast<const LayerParams *>(a->plan), L.key, static_cast<LayerCtl *>(a->ctl),
+                                    a->spin_limit ? a->spin_limit : (1u << 22), w, lds, (hipStream_t)stream),
+                       "qdec_layer");
 }
 
 int qdec_ngram_draft(const qdec_draft_args *a, qdec_stream_t stream) {

@@ -93,6 +93,34 @@ struct AttnParams {
 };
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 
+// ---- one decode layer per launch (layer.hip)
+// Barrier state of the layer kernel: a ticket that only grows (every
+// workgroup adds 1 per barrier) and an error word (1: a barrier wait ran out
+// of polls).
+struct LayerCtl {
+  uint64_t ticket;
+  uint32_t err;
+  uint32_t pad;
+};
+// Stages in order: g[0] QKV, a attention, g[1] O, g[2] gate/up, g[3] down;
+// nblk[i] = workgroups of g[i]'s own launch.  A launch reads it from device
+// memory (a plan qdec_layer_prepare wrote), each stage when it starts: as
+// kernel arguments all of it would be loaded at entry and held across the
+// layer.  key: a hash of the rest, which the launch passes too.
+struct LayerParams {
+  uint64_t key;
+  GemmParams g[4];
+  AttnParams a;
+  int nblk[4];
+};
+constexpr int kLayerThreads = 256;  // 4 waves: the plans of every stage
+constexpr int kLayerMaxRows = 4;    // the GEMM stages stage their rows from registers
+// Workgroups of one launch on the current device (all resident at once).
+hipError_t layer_workgroups(size_t lds_bytes, int *out);
+hipError_t launch_layer(const LayerParams *plan, uint64_t key, LayerCtl *ctl, uint32_t spin_limit, int workgroups,
+                        size_t lds_bytes, hipStream_t s);
+size_t layer_attn_lds_bytes();
+
 
 // ---- prefill (prefill.hip)
 // Product tiles of a workgroup (activation rows x weight rows): 256 x 128,

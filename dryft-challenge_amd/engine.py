@@ -45,6 +45,15 @@ from qdec.runtime import DecodeState, DeviceModel, max_rows_per_seq  # noqa: E40
 # Decode steps queued ahead of the one being handed to the caller (as the
 # reference, engine/engine.py:66); one before the first token.
 LOOKAHEAD = 3
+# One launch per layer (qdec_layer) instead of five, as the reference's
+# MEGA_ENABLED / MEGA_FORCE / MARGIN (engine/engine.py:81-91, 123): when
+# enabled, a shape of plain decode that qdec_layer takes is checked against
+# the per-operation step and raced against it, and kept only if it is faster
+# by the margin.  Off by default: on MI355X a layer's four grid barriers cost
+# more than the four launch boundaries they replace.
+MEGA_ENABLED = False
+MEGA_FORCE = False
+MEGA_MARGIN = 0.97
 # n-gram drafter settings of speculative decoding (notes/v10/spec.py:13-16).
 SPEC_PRIMARY = 3
 SPEC_BACKOFF = 2
@@ -85,26 +94,27 @@ class _Shape:
 
 
 class Engine:
-    def __init__(self, model_path: str, speculate: bool = False) -> None:
-        """Load the checkpoint at ``model_path`` (HF layout, local files only)."""
+    def __init__(self, model_path: str, speculate: bool = False, mega=None) -> None:
+        """Load the checkpoint at ``model_path`` (HF layout, local files only).
+        ``mega``: try one launch per layer for plain decode (None: MEGA_ENABLED)."""
         start = time.perf_counter()
         if not torch.cuda.is_available():
             raise RuntimeError("Engine needs a HIP device (torch.cuda.is_available() is False)")
         cfg = load_config(model_path)
         tensors = load_tensors(model_path)
-        self._setup(cfg, tensors, speculate)
+        self._setup(cfg, tensors, speculate, mega=mega)
         del tensors
         _log(f"engine ready in {time.perf_counter() - start:.1f}s "
              f"({self.model.weight_bytes() / 1e9:.2f} GB of packed weights)")
 
     @classmethod
-    def from_tensors(cls, cfg, tensors, speculate=False, use_graphs=True):
+    def from_tensors(cls, cfg, tensors, speculate=False, use_graphs=True, mega=None):
         """Build around in-memory HF-named tensors (tests)."""
         self = cls.__new__(cls)
-        self._setup(cfg, tensors, speculate, use_graphs)
+        self._setup(cfg, tensors, speculate, use_graphs, mega=mega)
         return self
 
-    def _setup(self, cfg, tensors, speculate, use_graphs=True):
+    def _setup(self, cfg, tensors, speculate, use_graphs=True, mega=None):
         self.device = torch.device("cuda:0")
         torch.cuda.set_device(self.device)
         self.lib = capi.lib()
@@ -115,6 +125,7 @@ class Engine:
         self.speculate = bool(speculate)
         self.spec_gate = True  # speculation falls back to plain steps when drafts do not pay
         self.use_graphs = use_graphs
+        self.mega = MEGA_ENABLED if mega is None else bool(mega)
         self.shape = None
         self.stats = {}
 
@@ -129,6 +140,8 @@ class Engine:
         sh = _Shape(self, batch, prompt_len, new_tokens, self.speculate)
         if self.use_graphs:
             sh.graph = self._capture(lambda: sh.state.step(t_rows=1))
+            if self.mega and not self.speculate and sh.state.layer_supported():
+                self._try_mega(sh, prompt_len, new_tokens)
         self.shape = sh
         _log(f"shape B={batch} S={prompt_len} N={new_tokens}: capacity {sh.state.cap}, "
              f"attention chunk {sh.state.chunk}, graph={'yes' if sh.graph else 'no'}, "
@@ -149,6 +162,83 @@ class Engine:
         torch.cuda.synchronize()
         return graph
 
+    # ------------------------------------------------ one launch per layer
+    def _check_mega(self, st, prompt_len, n_check=3):
+        """Logits of the one-launch-per-layer step against the per-operation
+        step on the same prompt and the same forced tokens, over a few
+        consecutive positions (engine/engine.py:691-734): the layer kernel
+        sums O and down over 4 waves, the per-operation plans over 8, so the
+        two agree to rounding, not bit for bit."""
+        B, dev = st.batch, self.device
+        g = torch.Generator().manual_seed(4321)
+        prompt = torch.randint(100, self.model.cfg.vocab, (B, prompt_len), generator=g)
+        toks = torch.randint(100, self.model.cfg.vocab, (n_check, B), generator=g).to(dev)
+        st.logits = torch.empty((st.max_rows, self.model.cfg.vocab), dtype=torch.bfloat16, device=dev)
+        try:
+            st.prefill(prompt.to(dev))
+            out = {}
+            for layer_launch in (False, True):
+                st.layer_launch = layer_launch
+                rows = []
+                for t in range(n_check):
+                    st.lens.fill_(prompt_len + t)
+                    st.ids[:B].copy_(toks[t])
+                    st.run_step(t_rows=1, advance=False)
+                    rows.append(st.logits[:B].float().clone())
+                out[layer_launch] = torch.stack(rows)
+            torch.cuda.synchronize(dev)
+        finally:
+            st.logits = None
+        err = st.layer_error()
+        ref, got = out[False], out[True]
+        if err or not torch.isfinite(got).all():
+            return False, f"error word {err}, finite {bool(torch.isfinite(got).all())}"
+        diff = (got - ref).abs()
+        max_d, mean_d = diff.max().item(), diff.mean().item()
+        agree = int((got.argmax(-1) == ref.argmax(-1)).sum())
+        # the reference's gate (engine/engine.py:733): max over the vocabulary
+        # and the mean over bf16 logits, read as a pair
+        ok = max_d <= 1.5 and mean_d <= 0.1
+        return ok, f"max|dlogit|={max_d:.3f} mean={mean_d:.4f} argmax {agree}/{n_check * B}"
+
+    def _time_graph(self, st, graph, start_len, reps):
+        st.lens.fill_(start_len)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            graph.replay()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / reps
+
+    def _try_mega(self, sh, prompt_len, new_tokens):
+        """Build the one-launch-per-layer step, check it against the
+        per-operation step and race the two; keep it only if it is faster by
+        MEGA_MARGIN, or MEGA_FORCE (engine/engine.py:856-884)."""
+        start = time.perf_counter()
+        st = sh.state
+        st.enable_layer_launch()
+        ok, detail = self._check_mega(st, prompt_len)
+        info = {"check": detail, "ok": ok, "used": False}
+        if ok:
+            graph = self._capture(lambda: st.step(t_rows=1))
+            reps = max(1, min(16, new_tokens))
+            t_cur, t_mega = [], []
+            for _ in range(2):
+                st.disable_layer_launch()
+                t_cur.append(self._time_graph(st, sh.graph, prompt_len, reps))
+                st.layer_launch = True
+                t_mega.append(self._time_graph(st, graph, prompt_len, reps))
+            t_cur, t_mega = min(t_cur), min(t_mega)
+            err = st.layer_error()
+            use = err == 0 and (MEGA_FORCE or t_mega < t_cur * MEGA_MARGIN)
+            info.update(per_op_ms=round(t_cur, 4), layer_ms=round(t_mega, 4), error_word=err, used=use)
+            if use:
+                sh.graph = graph
+        st.layer_launch = info["used"]
+        info["setup_s"] = round(time.perf_counter() - start, 2)
+        self.stats["mega"] = info
+        _log(f"layer-launch step: {info}")
+
     # ---------------------------------------------------------- generation
     def _launch(self, sh, step):
         if sh.graph is not None:
@@ -161,8 +251,13 @@ class Engine:
         sh.host[step].copy_(sh.state.ids[:sh.batch], non_blocking=True)
         sh.events[step].record()
 
-    def _fetch(self, sh, step):
+    def _fetch(self, sh, step, last=False):
         sh.events[step].synchronize()
+        if last and sh.state.layer_launch and sh.state.layer_error():
+            # read once, after the last step (a read per step would wait for
+            # the steps queued behind it)
+            raise capi.QdecError("generate", -1, f"layer kernel error word {sh.state.layer_error()} (a grid "
+                                 "barrier wait ran out of polls, or a stale plan)")
         return self._checked(sh.host[step].tolist())
 
     def _checked(self, toks):
@@ -208,7 +303,7 @@ class Engine:
             while launched < target:
                 self._launch(sh, launched)
                 launched += 1
-            yield self._fetch(sh, step)
+            yield self._fetch(sh, step, last=step == steps - 1)
 
     # --------------------------------------------------------- speculation
     def _generate_spec(self, ids, steps):

@@ -21,6 +21,9 @@ NAN_ID = 2147483647
 # Library-owned scratch of qdec_attn_noalloc (QDEC_NOALLOC_*_BYTES).
 NOALLOC_PARTIAL_BYTES = 8 << 20
 NOALLOC_COUNTER_BYTES = 64 << 10
+# Device memory of a qdec_layer call (QDEC_LAYER_PLAN_BYTES, QDEC_LAYER_CTL_BYTES).
+LAYER_PLAN_BYTES = 4096
+LAYER_CTL_BYTES = 16
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32
@@ -53,6 +56,13 @@ class AttnArgs(ctypes.Structure):
                 ("counters", P), ("eps", F32), ("sm_scale", F32), ("batch", I32), ("t_rows", I32),
                 ("nq", I32), ("nkv", I32), ("head_dim", I32), ("cap", I32), ("chunk", I32),
                 ("waves", I32), ("out_partials", I32), ("out_frag", I32)]
+
+
+class LayerArgs(ctypes.Structure):
+    _fields_ = [("qkv", ctypes.POINTER(GemmArgs)), ("attn", ctypes.POINTER(AttnArgs)),
+                ("o", ctypes.POINTER(GemmArgs)), ("gate_up", ctypes.POINTER(GemmArgs)),
+                ("down", ctypes.POINTER(GemmArgs)), ("plan", P), ("ctl", P),
+                ("spin_limit", ctypes.c_uint32), ("workgroups", I32)]
 
 
 class DraftArgs(ctypes.Structure):
@@ -122,6 +132,10 @@ class Lib:
             fn = getattr(so, name)
             fn.argtypes = [ctypes.POINTER(st), P]
             fn.restype = ctypes.c_int
+        so.qdec_layer_prepare.argtypes = [ctypes.POINTER(LayerArgs)]
+        so.qdec_layer_prepare.restype = ctypes.c_int
+        so.qdec_layer.argtypes = [ctypes.POINTER(LayerArgs), P]
+        so.qdec_layer.restype = ctypes.c_int
         for name, st in (("qdec_gemm_workspace", GemmArgs), ("qdec_attn_workspace", AttnArgs)):
             fn = getattr(so, name)
             fn.argtypes = [ctypes.POINTER(st), ctypes.POINTER(ctypes.c_size_t),
@@ -161,6 +175,12 @@ class Lib:
 
     def attn_noalloc(self, args, stream):
         self._check("qdec_attn_noalloc", self.so.qdec_attn_noalloc(ctypes.byref(args), stream))
+
+    def layer_prepare(self, args):
+        self._check("qdec_layer_prepare", self.so.qdec_layer_prepare(ctypes.byref(args)))
+
+    def layer(self, args, stream):
+        self._check("qdec_layer", self.so.qdec_layer(ctypes.byref(args), stream))
 
     def ngram_draft(self, args, stream):
         self._check("qdec_ngram_draft", self.so.qdec_ngram_draft(ctypes.byref(args), stream))

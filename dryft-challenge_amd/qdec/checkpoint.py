@@ -86,7 +86,7 @@ def param_shapes(cfg):
             (p + "mlp.down_proj.weight", (H, I), "normal"),
         ]
     out.append(("model.norm.weight", (H,), "norm"))
-    if not cfg.get("tie_word_embeddings", True):
+    if not cfg.get("tie_word_embeddings", False):  # untied unless stated, as the runtime reads it
         out.append(("lm_head.weight", (cfg["vocab_size"], H), "normal"))
     return out
 

@@ -51,6 +51,9 @@ PREFILL_ROW_TILE = 256
 LM_TILES_BATCHED = 8
 # Plain decode up to this batch merges attention chunks in the O projection.
 MERGE_IN_O_MAX_BATCH = 4
+# qdec_layer (one launch per layer) takes plain decode up to this batch: its
+# GEMM stages stage their rows from registers (kLayerMaxRows).
+LAYER_MAX_BATCH = 4
 # From this many rows per call the attention output and the SwiGLU output
 # are written in MFMA fragment order and read that way by the O and down
 # projections: one contiguous KiB per fragment load and no re-layout
@@ -378,6 +381,7 @@ class DecodeState:
         self.attn_counters = torch.zeros((max(ac, 4) // 4 + 4,), dtype=torch.int32, device=dev)
         self._gemm_cache = {}
         self._attn_cache = {}
+        self.layer_launch = False  # plain steps as one qdec_layer launch per layer
 
     # ----------------------------------------------------------- arguments
     def _merge_in_o(self, t_rows):
@@ -498,7 +502,11 @@ class DecodeState:
         e.rows, e.hidden, e.vocab = rows, c.hidden, c.vocab
         lib.embed(e, s)
         pm = self._merge_in_o(t_rows)
+        by_layer = self.layer_launch and t_rows == 1
         for i in range(c.n_layers):
+            if by_layer:
+                lib.layer(self._layer_args[i], s)
+                continue
             lib.gemm(self._cached_gemm("qkv", i, rows), s)
             lib.attn(self._cached_attn(i, t_rows, pm), s)
             lib.gemm(self._cached_gemm("o", i, rows, self._cached_attn(i, t_rows, pm) if pm else None), s)
@@ -528,6 +536,62 @@ class DecodeState:
     def step(self, t_rows=1, lm_head=True, ids_out=None, advance=True, stream=None):
         """One forward (``run_step``); the name every caller captures."""
         self.run_step(t_rows=t_rows, lm_head=lm_head, ids_out=ids_out, advance=advance, stream=stream)
+
+    # ------------------------------------------------ one layer per launch
+    def layer_supported(self):
+        """Whether qdec_layer takes this state's plain decode steps: up to
+        LAYER_MAX_BATCH sequences, attention partials merged in O."""
+        return self.batch <= LAYER_MAX_BATCH and self._merge_in_o(1)
+
+    def layer_gemm_args(self, role, layer, x_attn=None):
+        """A GEMM stage of qdec_layer: the role's arguments under the layer
+        kernel's plan (4 waves, no k split; gate/up two tiles per workgroup
+        so every stage has at most one block per workgroup)."""
+        a = self._gemm_args(role, layer, self.batch, x_attn=x_attn)
+        a.ksplit, a.waves = 1, 4
+        a.tiles_per_wg = 2 if role == "gate_up" else 1
+        return a
+
+    def enable_layer_launch(self, spin_limit=0, workgroups=0):
+        """Run plain decode steps (t_rows 1) as one qdec_layer launch per
+        layer: writes every layer's plan to device memory now (synchronous,
+        so not under graph capture).  Verify passes (t_rows > 1) keep the
+        per-operation launches; the layer kernel's 4-wave O and down sum in
+        another order than this state's plans, so its rows are not
+        bit-identical to theirs (within the logit tolerance instead)."""
+        if not self.layer_supported():
+            raise ValueError(f"qdec_layer takes at most {LAYER_MAX_BATCH} sequences (batch {self.batch})")
+        c, dev = self.model.cfg, self.model.device
+        if getattr(self, "layer_plan", None) is None:
+            self.layer_plan = torch.zeros((c.n_layers, capi.LAYER_PLAN_BYTES), dtype=torch.uint8, device=dev)
+            self.layer_ctl = torch.zeros((capi.LAYER_CTL_BYTES // 4,), dtype=torch.int32, device=dev)
+        self._layer_args = []
+        for i in range(c.n_layers):
+            at = self._attn_args(i, 1, partials=True)
+            g = [self.layer_gemm_args("qkv", i), self.layer_gemm_args("o", i, x_attn=at),
+                 self.layer_gemm_args("gate_up", i), self.layer_gemm_args("down", i)]
+            la = capi.LayerArgs()
+            la.qkv, la.o, la.gate_up, la.down = (ctypes.pointer(x) for x in g)
+            la.attn = ctypes.pointer(at)
+            la._keep = (at, g)  # the structs the pointers refer to
+            la.plan, la.ctl = self.layer_plan[i].data_ptr(), self.layer_ctl.data_ptr()
+            la.spin_limit, la.workgroups = spin_limit, workgroups
+            self.lib.layer_prepare(la)
+            self._layer_args.append(la)
+        torch.cuda.synchronize(dev)
+        self.layer_launch = True
+
+    def disable_layer_launch(self):
+        self.layer_launch = False
+
+    def layer_error(self):
+        """The layer kernel's error word: 0, 1 (a barrier wait ran out of
+        polls) or 2 (a launch whose plan was written for other arguments)."""
+        return int(self.layer_ctl[2].item()) if getattr(self, "layer_ctl", None) is not None else 0
+
+    def reset_layer_ctl(self):
+        """Zero the barrier state (after an error, before the next launch)."""
+        self.layer_ctl.zero_()
 
     # ------------------------------------------------------------- prefill
     def prefill(self, prompt, stream=None):

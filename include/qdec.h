@@ -266,6 +266,50 @@ int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,
 #define QDEC_NOALLOC_COUNTER_BYTES (64u << 10)
 int qdec_attn_noalloc(const qdec_attn_args *a, qdec_stream_t stream);
 
+/* -------------------------------------------- one decode layer per launch */
+
+/* A whole decoder layer of plain decode in one launch: the qkv, attn, o,
+ * gate_up and down calls above as the stages of one kernel whose workgroups
+ * all stay resident and meet at a grid barrier between stages.  Each stage
+ * runs the per-block code of its own launch under a 4-wave plan, so the
+ * layer computes what those five calls would (the engine's own plans use 8
+ * waves for O and down at batch 1, which sums their k ranges in another
+ * order).  Accepted plans: batch <= 4 rows, t_rows 1; every GEMM waves 4,
+ * ksplit 1, no fragment order, no split residual; qkv NORM_IN, o RES_OUT
+ * with x_attn == attn, gate_up NORM_IN | GLU with tiles_per_wg 2, down
+ * RES_OUT; attn waves 4, out_partials 1; at most `workgroups` blocks per
+ * stage.  Anything else fails with QDEC_EUNSUPPORTED.
+ *
+ * plan: device memory for the launch parameters, written by
+ *   qdec_layer_prepare (synchronous; not under stream capture) and read by
+ *   every qdec_layer call with the same arguments (a call whose arguments
+ *   differ from the prepared ones runs nothing and sets the error word to 2).
+ * ctl: barrier state, zeroed before the first call, then left to the
+ *   library (a ticket that only grows, at ctl, and an error word, uint32 at
+ *   ctl + 8).  A workgroup that waits longer than spin_limit polls sets the
+ *   word to 1 and every later wait gives up, so a launch whose workgroups
+ *   cannot all be resident ends with wrong numbers and the flag, never with
+ *   a hang; zero ctl again before reusing it.  Calls sharing ctl must use one
+ *   workgroup count and must not overlap in time.
+ * Replaces the reference's one-launch layer (engine/kernels/layer.py:46-285:
+ * _arrive_and_wait with SPIN_LIMIT, _layer_kernel) and its engine hook
+ * (engine/engine.py:834-884; MEGA_ENABLED = False there, :81). */
+#define QDEC_LAYER_PLAN_BYTES 4096u
+#define QDEC_LAYER_CTL_BYTES 16u
+typedef struct {
+  const qdec_gemm_args *qkv;
+  const qdec_attn_args *attn;
+  const qdec_gemm_args *o;
+  const qdec_gemm_args *gate_up;
+  const qdec_gemm_args *down;
+  void *plan;          /* QDEC_LAYER_PLAN_BYTES, 16-byte aligned */
+  void *ctl;           /* QDEC_LAYER_CTL_BYTES, 8-byte aligned */
+  uint32_t spin_limit; /* polls before a barrier wait gives up; 0 = 1 << 22 */
+  int32_t workgroups;  /* 0: as many as fit the GPU at once (the most allowed) */
+} qdec_layer_args;
+int qdec_layer_prepare(const qdec_layer_args *a);
+int qdec_layer(const qdec_layer_args *a, qdec_stream_t stream);
+
 /* ------------------------------------------------ n-gram speculation */
 
 /* Suffix-match drafter over each sequence's own history hist[b, 0..lens[b]]

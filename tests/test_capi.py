@@ -27,7 +27,7 @@ def test_structs_match_header_fields():
                       ("qdec_attn_args", capi.AttnArgs), ("qdec_draft_args", capi.DraftArgs),
                       ("qdec_accept_args", capi.AcceptArgs), ("qdec_rownorm_args", capi.RownormArgs),
                       ("qdec_pgemm_args", capi.PgemmArgs), ("qdec_prefill_qk_args", capi.PrefillQkArgs),
-                      ("qdec_prefill_attn_args", capi.PrefillAttnArgs)):
+                      ("qdec_prefill_attn_args", capi.PrefillAttnArgs), ("qdec_layer_args", capi.LayerArgs)):
         body = re.search(r"typedef struct (?:\w+ )?\{([^{}]*)\}\s*" + cname + ";", text).group(1)
         fields = re.findall(r"\*?\s*(\w+)\s*;", body)
         assert fields == [f[0] for f in st._fields_], cname
@@ -124,6 +124,58 @@ def test_attn_workspace(qlib):
     assert pb == 4 * 2 * 8 * 4 * 12 * 130 and cb == 2 * 8 * 4
     pb, cb = qlib.attn_workspace(_attn(cap=64, chunk=64))
     assert pb == 0 and cb == 0
+
+
+def _layer(**kw):
+    """qdec_layer arguments of a batch-1 Qwen3-4B layer under the layer
+    kernel's plans (pointer values are placeholders: these calls are
+    refused before anything touches a GPU)."""
+    at = _attn(batch=1, out_partials=1, cap=800, chunk=96)
+    g = dict(qkv=_gemm(flags=capi.NORM_IN, n=6144, k=2560),
+             o=_gemm(flags=capi.RES_OUT, n=2560, k=4096),
+             gate_up=_gemm(flags=capi.NORM_IN | capi.GLU, n=19456, k=2560, tiles_per_wg=2),
+             down=_gemm(flags=capi.RES_OUT, n=2560, k=9728))
+    g["o"].x_attn = ctypes.addressof(at)
+    la = capi.LayerArgs(plan=4096, ctl=64)
+    la.attn = ctypes.pointer(at)
+    for name, a in g.items():
+        setattr(la, name, ctypes.pointer(a))
+    la._keep = (at, g)
+    for k, v in kw.items():
+        if callable(v):
+            v(la, at, g)
+        else:
+            setattr(la, k, v)
+    return la
+
+
+def _set(obj, **kw):
+    def f(la, at, g):
+        target = at if obj == "attn" else g[obj]
+        for k, v in kw.items():
+            setattr(target, k, v)
+    return f
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(plan=8), -2, "plan"),
+    (dict(ctl=12), -2, "ctl"),
+    (dict(fix=_set("attn", t_rows=2)), -3, "t_rows"),
+    (dict(fix=_set("attn", batch=5)), -3, "batch"),
+    (dict(fix=_set("attn", out_partials=0)), -3, "out_partials"),
+    (dict(fix=_set("o", x_attn=None)), -3, "x_attn"),
+    (dict(fix=_set("qkv", waves=8)), -3, "qkv plan"),
+    (dict(fix=_set("down", ksplit=4)), -3, "down plan"),
+    (dict(fix=_set("gate_up", flags=capi.NORM_IN)), -3, "gate_up plan"),
+    (dict(fix=_set("qkv", rows=2)), -3, "qkv plan"),
+])
+def test_layer_validation(qlib, kw, code, needle):
+    fix = kw.pop("fix", None)
+    la = _layer(**kw) if fix is None else _layer(fix=fix)
+    assert qlib.so.qdec_layer(ctypes.byref(la), None) == code
+    assert needle in qlib.last_error()
+    assert qlib.so.qdec_layer_prepare(ctypes.byref(la)) == code
+    assert qlib.so.qdec_layer(None, None) == -1
 
 
 def test_other_validation(qlib):

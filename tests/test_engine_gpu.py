@@ -197,6 +197,165 @@ def test_speculative_equals_plain_greedy(ckpt, engine):
 
 
 
+# ------------------------------------------------- one layer per launch
+def _layer_state(engine, B, S, seed, **kw):
+    from qdec.runtime import DecodeState
+    st = DecodeState(engine.model, B, S + 30, max_t=1, keep_logits=True)
+    st.prefill(prompts(B, S, seed).to(engine.device))
+    st.enable_layer_launch(**kw)
+    torch.cuda.synchronize()
+    return st
+
+
+def _snapshot(st):
+    return [t.clone() for t in (st.hbuf, st.k_cache, st.v_cache, st.qkv, st.act, st.attn_partial, st.ids, st.lens)]
+
+
+def _restore(st, snap):
+    for t, v in zip((st.hbuf, st.k_cache, st.v_cache, st.qkv, st.act, st.attn_partial, st.ids, st.lens), snap):
+        t.copy_(v)
+
+
+def _stage_launches(st):
+    """The layers of a plain step as the five per-operation calls under the
+    layer kernel's plans (what each qdec_layer launch runs as its stages)."""
+    from qdec import capi
+    lib, c = st.lib, st.model.cfg
+    s = torch.cuda.current_stream().cuda_stream
+    e = capi.EmbedArgs()
+    e.ids, e.emb, e.h = st.ids.data_ptr(), st.model.emb.data_ptr(), st.h.data_ptr()
+    e.rows, e.hidden, e.vocab = st.batch, c.hidden, c.vocab
+    lib.embed(e, s)
+    for i in range(c.n_layers):
+        at = st._attn_args(i, 1, partials=True)
+        lib.gemm(st.layer_gemm_args("qkv", i), s)
+        lib.attn(at, s)
+        lib.gemm(st.layer_gemm_args("o", i, x_attn=at), s)
+        lib.gemm(st.layer_gemm_args("gate_up", i), s)
+        lib.gemm(st.layer_gemm_args("down", i), s)
+
+
+def _same(a, b):
+    """Bit-identical (NaN payloads included)."""
+    return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
+
+
+def _ticket(st):
+    lo, hi = st.layer_ctl[:2].cpu().tolist()
+    return (lo & 0xFFFFFFFF) | ((hi & 0xFFFFFFFF) << 32)
+
+
+@pytest.mark.parametrize("B,S,seed", [(1, 150, 41), (3, 333, 42), (4, 90, 43)])
+def test_layer_launch_equals_its_stage_launches(engine, B, S, seed):
+    """qdec_layer runs the per-block code of each stage's own launch: the
+    residual, the new cache slots, the SwiGLU activations and the attention
+    partials come out bit for bit as from the five calls with the same
+    plans."""
+    st = _layer_state(engine, B, S, seed)
+    snap = _snapshot(st)
+    _stage_launches(st)
+    torch.cuda.synchronize()
+    want = _snapshot(st)
+    _restore(st, snap)
+    t0 = _ticket(st)
+    st.run_step(t_rows=1, lm_head=False, advance=False)
+    torch.cuda.synchronize()
+    got = _snapshot(st)
+    names = ("hbuf", "k_cache", "v_cache", "qkv", "act", "attn_partial", "ids", "lens")
+    for name, g, w in zip(names, got, want):
+        assert _same(g, w), name
+    assert st.layer_error() == 0
+    # every workgroup passed 4 barriers per layer
+    n = _ticket(st) - t0
+    per = 4 * engine.model.cfg.n_layers
+    assert n % per == 0 and n // per >= 304, n  # at least gate/up's 304 blocks
+    assert not torch.equal(snap[0], got[0])  # the step did something
+
+
+@pytest.mark.parametrize("B,S,n,seed", [(1, 60, 8, 51), (4, 45, 6, 52)])
+def test_layer_launch_vs_oracle(engine, oracle, B, S, n, seed):
+    """Plain decode with one launch per layer, teacher-forced against the
+    oracle: the same logit tolerance and near-tie rule as the per-operation
+    step."""
+    from qdec.runtime import DecodeState
+    prompt = prompts(B, S, seed)
+    st = DecodeState(engine.model, B, S + n + 30, max_t=1, keep_logits=True)
+    st.prefill(prompt.to(engine.device))
+    st.enable_layer_launch()
+    toks, logits = [st.ids[:B].cpu()], [st.logits[:B].float().cpu()]
+    for _ in range(n - 1):
+        st.run_step(t_rows=1)
+        toks.append(st.ids[:B].cpu())
+        logits.append(st.logits[:B].float().cpu())
+    torch.cuda.synchronize()
+    assert st.layer_error() == 0
+    toks, logits = torch.stack(toks, 1), torch.stack(logits, 1)
+    ref = oracle.teacher_forced(prompt, toks)
+    err = normalized_max_err(logits, ref)
+    print(f"layer launch B={B}: normalised max err {err.max().item():.4g}")
+    assert err.max().item() <= TOL
+    mism = ref.argmax(-1) != toks
+    near = top2_gap(ref) < TOL * ref.abs().amax(-1)
+    assert bool((~mism | near).all()), mism.nonzero().tolist()
+
+
+def test_layer_wait_limit_and_stale_plan(engine):
+    """The bounded barrier wait, forced from the host: with a limit of one
+    poll a wait runs out, the error word says 1 and every workgroup still
+    finishes.  A call whose arguments differ from the prepared plan runs
+    nothing and says 2.  After a reset the same state steps correctly."""
+    st = _layer_state(engine, 1, 64, 61, spin_limit=1)
+    snap = _snapshot(st)
+    st.run_step(t_rows=1, lm_head=False, advance=False)
+    torch.cuda.synchronize()
+    assert st.layer_error() == 1
+    _restore(st, snap)  # the stages ran unsynchronised: whatever they left
+    st.reset_layer_ctl()
+    st.enable_layer_launch()
+    la = st._layer_args[0]
+    la.qkv.contents.eps = 1e-3  # no longer the prepared plan
+    st.lib.layer(la, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert st.layer_error() == 2
+    assert all(_same(g, w) for g, w in zip(_snapshot(st), snap))
+    la.qkv.contents.eps = engine.model.cfg.eps
+    st.reset_layer_ctl()
+    _stage_launches(st)
+    want = _snapshot(st)
+    _restore(st, snap)
+    st.run_step(t_rows=1, lm_head=False, advance=False)
+    torch.cuda.synchronize()
+    assert st.layer_error() == 0
+    assert all(_same(g, w) for g, w in zip(_snapshot(st), want))
+
+
+def test_engine_mega_check_race_and_force(ckpt, engine, oracle):
+    """Engine(mega=True): the layer step is checked against the
+    per-operation step and raced; with MEGA_FORCE it is used, and its
+    tokens are the oracle's greedy picks up to near-ties."""
+    import engine as engine_mod
+    from engine import Engine
+    mega = Engine.from_tensors(engine.model.cfg.raw, load_tensors(ckpt[0]), mega=True)
+    prompt = prompts(1, 48, 71)
+    out = list(mega.generate(prompt.tolist(), 6))
+    info = mega.stats["mega"]
+    print(f"mega race: {info}")
+    assert info["ok"] and info["error_word"] == 0 and info["layer_ms"] > 0 and info["per_op_ms"] > 0
+    assert len(out) == 6
+    engine_mod.MEGA_FORCE = True
+    try:
+        mega.shape = None
+        out = list(mega.generate(prompt.tolist(), 6))
+    finally:
+        engine_mod.MEGA_FORCE = False
+    assert mega.stats["mega"]["used"] and mega.shape.state.layer_launch
+    toks = torch.tensor(out).T  # [B, n]
+    ref = oracle.teacher_forced(prompt, toks)
+    mism = ref.argmax(-1) != toks
+    near = top2_gap(ref) < TOL * ref.abs().amax(-1)
+    assert bool((~mism | near).all()), mism.nonzero().tolist()
+
+
 def test_invalid_inputs_raise(engine):
     """Out-of-range prompt ids are refused on the host; an out-of-range id
     that reaches the device makes the step emit capi.NAN_ID, which the engine
