@@ -23,6 +23,10 @@ Printed JSON fields beyond the driver contract:
   prefill       prompt processing of the headline prompt (time to first
                 token: the prompt through the 36 layers on the matrix cores,
                 lm_head + argmax of the last position), tok/s and TFLOP/s;
+  layer_launch  the same decode step with each layer as one qdec_layer launch
+                (38 launches instead of 182): its logit check against the
+                per-operation step and both graphs timed over the same
+                positions (skip with --no-layer);
   batched       decode tok/s of configs[2] (batch 8, 1024 prompt tokens) and
                 configs[3] (batch 32, 4096), each after a real (timed)
                 prefill of its random prompts (skip with --no-batched);
@@ -287,6 +291,29 @@ def spec_ceiling(eng, prompts, plain_steps, new_tokens, plain_tps):
             "token_identical": toks == plain_steps}
 
 
+def layer_launch_bench(eng, sh, prompt, new_tokens, steps):
+    """The one-launch-per-layer step (qdec_layer) on the headline shape: its
+    logit check against the per-operation step (the engine's own gate), then
+    both graphs replayed over the same positions, best of 3 rounds."""
+    st = sh.state
+    B, S = prompt.shape
+    st.enable_layer_launch()
+    ok, detail = eng._check_mega(st, S)
+    st.prefill(prompt)
+    layer_graph = eng._capture(lambda: st.step(t_rows=1))
+    reps = max(1, min(steps, new_tokens - 2))
+    per_op, layer = [], []
+    for _ in range(3):
+        per_op.append(eng._time_graph(st, sh.graph, S, reps))
+        layer.append(eng._time_graph(st, layer_graph, S, reps))
+    err = st.layer_error()
+    st.disable_layer_launch()
+    n = eng.model.cfg.n_layers
+    return {"check": detail, "ok": ok, "error_word": err, "steps": reps,
+            "per_op_ms_per_step": round(min(per_op), 4), "layer_ms_per_step": round(min(layer), 4),
+            "launches_per_step": {"per_op": 5 * n + 2, "layer": n + 2}}
+
+
 def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):
     """Decode throughput of a batched configuration: its prompts (uniform
     random tokens from ``seed``) are prefilled for real (timed), every
@@ -397,6 +424,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-spec", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--no-layer", action="store_true",
+                    help="skip timing the one-launch-per-layer step (qdec_layer) beside the per-op step")
     ap.add_argument("--pmc-role", choices=ROLES + ("all",),
                     help="only launch this role's kernel over every layer (6 rounds, rows = the "
                          "config's batch; 'all' = every role in turn), then a 512 MiB device copy "
@@ -499,6 +528,11 @@ def main():
         roles[role] = round(time_gemm_role(eng, st, role) * 1e6, 2)
     log(f"other roles us/launch: {roles}")
 
+    layer = None
+    if not args.no_layer and st.layer_supported():
+        layer = layer_launch_bench(eng, sh, prompt.to(eng.device), N, args.steps)
+        log(f"one launch per layer: {layer}")
+
     batched = {}
     if not args.no_batched:
         del sh, st, graph
@@ -558,6 +592,7 @@ def main():
         "role_us_per_launch": roles,
         "prefill": prefill,
         "batched": batched or None,
+        "layer_launch": layer,
         "speculation": spec,
         "cpu_baseline": cpu,
     }

@@ -413,9 +413,10 @@ int plan_layer(const qdec_layer_args *a, LayerParams *L, int *workgroups, size_t
     }
     maxw = wgs[dev];
   }
-  const int w = a->workgroups ? a->workgroups : maxw;
-  if (w < 1 || w > maxw)
-    return set_error(QDEC_EINVAL, "qdec_layer: workgroups %d not in [1, %d] (all resident at once)", a->workgroups, maxw);
+  const int w = a->workgroups ? a->workgroups : maxw - maxw % kLayerGroups;
+  if (w < kLayerGroups || w > maxw || w % kLayerGroups)
+    return set_error(QDEC_EINVAL, "qdec_layer: workgroups %d not a multiple of %d in [%d, %d] (all resident at once)",
+                     a->workgroups, kLayerGroups, kLayerGroups, maxw);
   int blocks = L->a.nchunks * L->a.nkv * L->a.batch;
   for (int i = 0; i < 4; ++i) blocks = std::max(blocks, L->nblk[i]);
   if (blocks > w)

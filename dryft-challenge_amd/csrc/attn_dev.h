@@ -57,7 +57,9 @@ struct AttnLds {
   static_assert(64 * kAttnRowStride * 2 <= NW * 8 * 64 * 16, "query rows fit the partials area");
 };
 
-template <int D, int G, int MTQ, int NW>
+// COH: the projection rows are read and the chunk partials written at device
+// scope, for a body that shares its launch with their producer and consumer.
+template <int D, int G, int MTQ, int NW, bool COH = false>
 __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, const int kvh, const int b,
                                            unsigned char *smem) {
   static_assert(D == 128 && G == 4, "head_dim 128, 4 query heads per kv head");
@@ -130,13 +132,13 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   for (int i = 0; i < QPW; ++i) {
     const int r = min(wave + NW * i, R - 1);
     const int t = r / G, hq = r % G;
-    qraw[i] = *reinterpret_cast<const uint32_t *>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + 2 * lane);
+    qraw[i] = ldv4<COH>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + 2 * lane);
   }
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     const uint16_t *row = qkv + (size_t)(b * T + min(wave + NW * i, T - 1)) * width;
-    kraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + kvh) * D + 2 * lane);
-    vraw[i] = *reinterpret_cast<const uint32_t *>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
+    kraw[i] = ldv4<COH>(row + (size_t)(nq + kvh) * D + 2 * lane);
+    vraw[i] = ldv4<COH>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
   }
   const uint32_t qw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + 2 * lane);
   const uint32_t kw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + 2 * lane);
@@ -381,7 +383,7 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
           *reinterpret_cast<uint2 *>(out_at(b * T + t, (kvh * G + hq) * D + dt * 16 + grp * 4)) = o;
         } else {
           float *dst = part + (size_t)r * D + dt * 16 + grp * 4;
-          if (p.out_partials)  // read by the next launch only
+          if (p.out_partials && !COH)  // read by the next launch only
             *reinterpret_cast<f32x4_t *>(dst) = tot;
           else
             store_coherent4(dst, tot);
@@ -389,7 +391,7 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
       }
     }
     if (!direct && wave == 0 && grp == 0 && r < R) {
-      if (p.out_partials) {
+      if (p.out_partials && !COH) {
         part[(size_t)R * D + r] = M;
         part[(size_t)R * D + R + r] = Lrow;
       } else {

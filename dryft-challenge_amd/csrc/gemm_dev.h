@@ -87,6 +87,7 @@ __device__ __forceinline__ void block_row_sums(float (&ss)[8], float *s_red, int
 // max [R], sum [R], R = t_rows * 4).  The same operations in the same order
 // as the attention's own chunk merge, so the bf16 result is bit-identical
 // to the output that call would have written.
+template <bool COH>
 __device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk) {
   constexpr int D = 128, G = 4, CB = 8;
   const int T = p.a_t_rows, R = T * G;
@@ -109,10 +110,10 @@ __device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk)
 #pragma unroll
     for (int j = 0; j < CB; ++j) {
       const float *pr = part_b + (size_t)min(cc + j, n_active - 1) * cstride;
-      mc[j] = pr[(size_t)R * D + r];
-      lc[j] = pr[(size_t)R * D + R + r];
-      a0[j] = *reinterpret_cast<const f32x4_t *>(pr + (size_t)r * D + d0);
-      a1[j] = *reinterpret_cast<const f32x4_t *>(pr + (size_t)r * D + d0 + 4);
+      mc[j] = ldf<COH>(pr + (size_t)R * D + r);
+      lc[j] = ldf<COH>(pr + (size_t)R * D + R + r);
+      a0[j] = ldf4<COH>(pr + (size_t)r * D + d0);
+      a1[j] = ldf4<COH>(pr + (size_t)r * D + d0 + 4);
     }
   };
   load_group(0);
@@ -123,7 +124,7 @@ __device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk)
   for (int cc = CB; cc < n_active; cc += CB) {
     float mg[CB];
 #pragma unroll
-    for (int j = 0; j < CB; ++j) mg[j] = part_b[(size_t)min(cc + j, n_active - 1) * cstride + (size_t)R * D + r];
+    for (int j = 0; j < CB; ++j) mg[j] = ldf<COH>(part_b + (size_t)min(cc + j, n_active - 1) * cstride + (size_t)R * D + r);
 #pragma unroll
     for (int j = 0; j < CB; ++j)
       if (cc + j < n_active) mmax = fmaxf(mmax, mg[j]);
@@ -180,7 +181,9 @@ constexpr int kMergeParts = 4;
 // wave loads then feeds TW tiles' MFMAs, so from two M tiles the activation
 // reads per weight byte halve at TW = 2 and the ring's registers go to
 // weights instead (a tile's sums are the same whatever TW is).
-template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows, bool XP = false, int TW = 1>
+// COH: activations and outputs at device scope (ldv16 and friends), for a
+// body that shares its launch with the workgroups that produce or consume them.
+template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows, bool XP = false, int TW = 1, bool COH = false>
 __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, const int nblk,
                                           unsigned char *__restrict__ smem) {
   constexpr bool NORM = (FLAGS & QDEC_NORM_IN) != 0;
@@ -231,7 +234,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = mt * 16 + col;
-        res_v[mt] = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p.res) +
+        res_v[mt] = ldv8<COH>(reinterpret_cast<const uint16_t *>(p.res) +
                                                      (size_t)(m < rows ? m : 0) * p.n + tile0 * 16 + grp * 4);
       }
     }
@@ -282,7 +285,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
         if constexpr (XD) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
-            xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + (size_t)min(r, p.ksw - 1) * xkstep);
+            xb[mt][r] = ldv16<COH>(xg[mt] + (size_t)min(r, p.ksw - 1) * xkstep);
         }
       }
     } else {
@@ -324,9 +327,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
         const bool ok = m < rows && vr < per_row;
         const int mm = ok ? m : 0, vv = ok ? vr : 0;
         if (merge) {
-          xr[m][j] = ok ? attn_merge8(p, mm, ks_wg * 32 + 8 * vv) : zero4();
+          xr[m][j] = ok ? attn_merge8<COH>(p, mm, ks_wg * 32 + 8 * vv) : zero4();
         } else {
-          const uint4 v = *reinterpret_cast<const uint4 *>(X + (size_t)mm * p.k + ks_wg * 32 + 8 * vv);
+          const uint4 v = ldv16<COH>(X + (size_t)mm * p.k + ks_wg * 32 + 8 * vv);
           xr[m][j] = ok ? v : zero4();
         }
       }
@@ -423,7 +426,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
             const uint16_t *xrow = X + (size_t)m * p.k;
             for (int v = tid; v < nvec; v += nthr) {
               float f[8];
-              unpack8(*reinterpret_cast<const uint4 *>(xrow + 8 * v), f);
+              unpack8(ldv16<COH>(xrow + 8 * v), f);
 #pragma unroll
               for (int e = 0; e < 8; ++e) ss[j] += f[e] * f[e];
             }
@@ -440,7 +443,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
         const int m = v / per_row;
         const int vr = v - m * per_row;
         const int kg = ks_wg * 32 + 8 * vr;
-        uint4 xv = *reinterpret_cast<const uint4 *>(X + (size_t)m * p.k + kg);
+        uint4 xv = ldv16<COH>(X + (size_t)m * p.k + kg);
         if constexpr (NORM)
           xv = norm8(xv, *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p.norm_w) + kg), s_rstd[m]);
         *reinterpret_cast<uint4 *>(s_x + (size_t)m * xstride + 8 * vr) = xv;
@@ -523,7 +526,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
                 }
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
-                  xb[mt][r] = *reinterpret_cast<const uint4 *>(xg[mt] + (size_t)((i + RW) % p.ksw) * xkstep);
+                  xb[mt][r] = ldv16<COH>(xg[mt] + (size_t)((i + RW) % p.ksw) * xkstep);
               }
             }
           }
@@ -547,7 +550,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
             const int i = r >> 2;
             const int q = r & 3;
             const int kg = (ks_wg + w2 * p.ksw + kbeg + i) * 32 + q * 8;
-            uint4 xv = *reinterpret_cast<const uint4 *>(X + (size_t)m * p.k + kg);
+            uint4 xv = ldv16<COH>(X + (size_t)m * p.k + kg);
             if constexpr (NORM)
               xv = norm8(xv, *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint16_t *>(p.norm_w) + kg),
                          s_rstd[m]);
@@ -684,11 +687,11 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
               }
           } else if constexpr (RES) {
             uint16_t *rp = reinterpret_cast<uint16_t *>(p.res) + (size_t)m * p.n + n0;
-            const uint2 r = res_early ? res_v[mt] : *reinterpret_cast<const uint2 *>(rp);
+            const uint2 r = res_early ? res_v[mt] : ldv8<COH>(rp);
             uint2 o;
             o.x = pack2(lo16(r.x) + rbf(g4[0]), hi16(r.x) + rbf(g4[1]));
             o.y = pack2(lo16(r.y) + rbf(g4[2]), hi16(r.y) + rbf(g4[3]));
-            *reinterpret_cast<uint2 *>(rp) = o;
+            stv8<COH>(rp, o);
           } else if constexpr (GLU) {
             const f32x4_t u4 = acc[tw * NACC + 1][mt];
             float o4[4];
@@ -702,12 +705,12 @@ __device__ __forceinline__ void gemm_body(const GemmParams p, const int blk, con
             uint2 o;
             o.x = pack2(o4[0], o4[1]);
             o.y = pack2(o4[2], o4[3]);
-            *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
+            stv8<COH>(out_at(m, n0), o);
           } else {
             uint2 o;
             o.x = pack2(g4[0], g4[1]);
             o.y = pack2(g4[2], g4[3]);
-            *reinterpret_cast<uint2 *>(out_at(m, n0)) = o;
+            stv8<COH>(out_at(m, n0), o);
           }
         }
       }

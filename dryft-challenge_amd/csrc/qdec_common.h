@@ -117,6 +117,57 @@ __device__ __forceinline__ void store_coherent4(float *p, f32x4_t v) {
   st64_dev(p, (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32));
   st64_dev(p + 2, (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32));
 }
+template <bool COH>
+__device__ __forceinline__ f32x4_t ldf4(const float *p) {
+  if constexpr (COH)
+    return load_coherent4(p);
+  else
+    return *reinterpret_cast<const f32x4_t *>(p);
+}
+template <bool COH>
+__device__ __forceinline__ float ldf(const float *p) {
+  if constexpr (COH)
+    return load_coherent(p);
+  else
+    return *p;
+}
+// Activation accesses of a kernel body, plain or (COH) at device scope: COH
+// is for a body that runs inside a launch whose other workgroups wrote the
+// data or will read it (the one-launch-per-layer kernel); per-operation
+// launches hand their data over at the launch boundary and use plain ones.
+template <bool COH>
+__device__ __forceinline__ uint4 ldv16(const void *p) {
+  if constexpr (COH) {
+    const uint64_t a = ld64_dev(p), b = ld64_dev(static_cast<const char *>(p) + 8);
+    return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+  } else {
+    return *reinterpret_cast<const uint4 *>(p);
+  }
+}
+template <bool COH>
+__device__ __forceinline__ uint2 ldv8(const void *p) {
+  if constexpr (COH) {
+    const uint64_t a = ld64_dev(p);
+    return make_uint2((uint32_t)a, (uint32_t)(a >> 32));
+  } else {
+    return *reinterpret_cast<const uint2 *>(p);
+  }
+}
+template <bool COH>
+__device__ __forceinline__ void stv8(void *p, uint2 v) {
+  if constexpr (COH)
+    st64_dev(p, (uint64_t)v.x | ((uint64_t)v.y << 32));
+  else
+    *reinterpret_cast<uint2 *>(p) = v;
+}
+template <bool COH>
+__device__ __forceinline__ uint32_t ldv4(const void *p) {
+  if constexpr (COH)
+    return __hip_atomic_load(reinterpret_cast<const uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    return *reinterpret_cast<const uint32_t *>(p);
+}
+
 __device__ __forceinline__ int load_coherent_i(const int *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -94,13 +94,20 @@ struct AttnParams {
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 
 // ---- one decode layer per launch (layer.hip)
-// Barrier state of the layer kernel: a ticket that only grows (every
-// workgroup adds 1 per barrier) and an error word (1: a barrier wait ran out
-// of polls).
+// Barrier state of the layer kernel: tickets that only grow, in two levels
+// (workgroup w arrives at group w % kLayerGroups, the last of a group at the
+// top), each counter on its own 128-byte line; and an error word (1: a
+// barrier wait ran out of polls, 2: a stale plan).
+constexpr int kLayerGroups = 8;
 struct LayerCtl {
-  uint64_t ticket;
+  uint64_t ticket;  // top level: one arrival per group and barrier
   uint32_t err;
-  uint32_t pad;
+  uint32_t pad0[29];
+  struct Group {
+    uint64_t arrive;   // one per workgroup and barrier
+    uint64_t release;  // barriers this group has been released from
+    uint64_t pad[14];
+  } group[kLayerGroups];
 };
 // Stages in order: g[0] QKV, a attention, g[1] O, g[2] gate/up, g[3] down;
 // nblk[i] = workgroups of g[i]'s own launch.  A launch reads it from device

@@ -23,7 +23,7 @@ NOALLOC_PARTIAL_BYTES = 8 << 20
 NOALLOC_COUNTER_BYTES = 64 << 10
 # Device memory of a qdec_layer call (QDEC_LAYER_PLAN_BYTES, QDEC_LAYER_CTL_BYTES).
 LAYER_PLAN_BYTES = 4096
-LAYER_CTL_BYTES = 16
+LAYER_CTL_BYTES = 1152
 
 P = ctypes.c_void_p
 I32 = ctypes.c_int32

@@ -285,8 +285,7 @@ int qdec_attn_noalloc(const qdec_attn_args *a, qdec_stream_t stream);
  *   every qdec_layer call with the same arguments (a call whose arguments
  *   differ from the prepared ones runs nothing and sets the error word to 2).
  * ctl: barrier state, zeroed before the first call, then left to the
- *   library (a ticket that only grows, at ctl, and an error word, uint32 at
- *   ctl + 8).  A workgroup that waits longer than spin_limit polls sets the
+ *   library (tickets that only grow, and an error word, uint32 at ctl + 8).  A workgroup that waits longer than spin_limit polls sets the
  *   word to 1 and every later wait gives up, so a launch whose workgroups
  *   cannot all be resident ends with wrong numbers and the flag, never with
  *   a hang; zero ctl again before reusing it.  Calls sharing ctl must use one
@@ -295,7 +294,7 @@ int qdec_attn_noalloc(const qdec_attn_args *a, qdec_stream_t stream);
  * _arrive_and_wait with SPIN_LIMIT, _layer_kernel) and its engine hook
  * (engine/engine.py:834-884; MEGA_ENABLED = False there, :81). */
 #define QDEC_LAYER_PLAN_BYTES 4096u
-#define QDEC_LAYER_CTL_BYTES 16u
+#define QDEC_LAYER_CTL_BYTES 1152u
 typedef struct {
   const qdec_gemm_args *qkv;
   const qdec_attn_args *attn;
@@ -305,7 +304,8 @@ typedef struct {
   void *plan;          /* QDEC_LAYER_PLAN_BYTES, 16-byte aligned */
   void *ctl;           /* QDEC_LAYER_CTL_BYTES, 8-byte aligned */
   uint32_t spin_limit; /* polls before a barrier wait gives up; 0 = 1 << 22 */
-  int32_t workgroups;  /* 0: as many as fit the GPU at once (the most allowed) */
+  int32_t workgroups;  /* a multiple of 8; 0: as many as fit the GPU at once
+                          (the most allowed) */
 } qdec_layer_args;
 int qdec_layer_prepare(const qdec_layer_args *a);
 int qdec_layer(const qdec_layer_args *a, qdec_stream_t stream);

@@ -240,9 +240,11 @@ def _same(a, b):
     return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
 
 
-def _ticket(st):
-    lo, hi = st.layer_ctl[:2].cpu().tolist()
-    return (lo & 0xFFFFFFFF) | ((hi & 0xFFFFFFFF) << 32)
+def _tickets(st):
+    """(top ticket, arrivals summed over the 8 groups) of the layer kernel's
+    barrier state: the top at byte 0, group g's arrivals at 128 + 128 g."""
+    w = st.layer_ctl.cpu().view(torch.int64).tolist()
+    return w[0], sum(w[16 + 16 * g] for g in range(8))
 
 
 @pytest.mark.parametrize("B,S,seed", [(1, 150, 41), (3, 333, 42), (4, 90, 43)])
@@ -257,7 +259,7 @@ def test_layer_launch_equals_its_stage_launches(engine, B, S, seed):
     torch.cuda.synchronize()
     want = _snapshot(st)
     _restore(st, snap)
-    t0 = _ticket(st)
+    top0, arr0 = _tickets(st)
     st.run_step(t_rows=1, lm_head=False, advance=False)
     torch.cuda.synchronize()
     got = _snapshot(st)
@@ -265,10 +267,12 @@ def test_layer_launch_equals_its_stage_launches(engine, B, S, seed):
     for name, g, w in zip(names, got, want):
         assert _same(g, w), name
     assert st.layer_error() == 0
-    # every workgroup passed 4 barriers per layer
-    n = _ticket(st) - t0
-    per = 4 * engine.model.cfg.n_layers
-    assert n % per == 0 and n // per >= 304, n  # at least gate/up's 304 blocks
+    # every workgroup passed 4 barriers per layer; a group's last arrival
+    # went on to the top
+    top, arr = _tickets(st)
+    barriers = 4 * engine.model.cfg.n_layers
+    assert top - top0 == 8 * barriers
+    assert (arr - arr0) % barriers == 0 and (arr - arr0) // barriers >= 304  # gate/up has 304 blocks
     assert not torch.equal(snap[0], got[0])  # the step did something
 
 
