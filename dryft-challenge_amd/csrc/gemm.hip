@@ -5,11 +5,21 @@
 namespace qdec {
 namespace {
 
-// One workgroup per block of the plan (the body: gemm_dev.h).
+// One workgroup per block of the plan (the body and its design: gemm_body.inc,
+// gemm_dev.h).
 template <int MT, uint32_t FLAGS, int RW, bool XD, int FR = kFastRows, bool XP = false, int TW = 1>
 __global__ void __launch_bounds__(512) gemm_kernel(const GemmParams p) {
   extern __shared__ __align__(16) unsigned char smem[];
-  gemm_body<MT, FLAGS, RW, XD, FR, XP, TW>(p, blockIdx.x, gridDim.x, smem);
+  const int blk = blockIdx.x, nblk = gridDim.x;
+#define QDEC_LDX16(q) (*reinterpret_cast<const uint4 *>(q))
+#define QDEC_LDX8(q) (*reinterpret_cast<const uint2 *>(q))
+#define QDEC_STX8(q, v) (*reinterpret_cast<uint2 *>(q) = (v))
+#define QDEC_MERGE8(pp, m, kk) attn_merge8<false>((pp), (m), (kk))
+#include "gemm_body.inc"
+#undef QDEC_LDX16
+#undef QDEC_LDX8
+#undef QDEC_STX8
+#undef QDEC_MERGE8
 }
 
 // x' = norm_w * bf16(x * rstd) of one row per workgroup, written to xn: the

@@ -117,20 +117,6 @@ __device__ __forceinline__ void store_coherent4(float *p, f32x4_t v) {
   st64_dev(p, (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32));
   st64_dev(p + 2, (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32));
 }
-template <bool COH>
-__device__ __forceinline__ f32x4_t ldf4(const float *p) {
-  if constexpr (COH)
-    return load_coherent4(p);
-  else
-    return *reinterpret_cast<const f32x4_t *>(p);
-}
-template <bool COH>
-__device__ __forceinline__ float ldf(const float *p) {
-  if constexpr (COH)
-    return load_coherent(p);
-  else
-    return *p;
-}
 // Activation accesses of a kernel body, plain or (COH) at device scope: COH
 // is for a body that runs inside a launch whose other workgroups wrote the
 // data or will read it (the one-launch-per-layer kernel); per-operation
