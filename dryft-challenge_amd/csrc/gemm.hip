@@ -1,5 +1,5 @@
-// Launchers of the weight-streaming skinny GEMM (the kernel body and its
-// design: gemm_dev.h) and the row-normalisation pre-pass.
+// Launchers of the weight-streaming skinny GEMM (its design: gemm_dev.h; its
+// body: gemm_body.inc) and the row-normalisation pre-pass.
 #include "gemm_dev.h"
 
 namespace qdec {

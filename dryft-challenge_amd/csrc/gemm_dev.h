@@ -36,9 +36,10 @@
 // _gemv_vec_kernel, _gemv_splitk_kernel + reduce) and the lm_head + argmax of
 // engine/engine.py:492-498, 542-545.
 //
-// The body takes its workgroup index and count as arguments, so that the
-// per-operation launches (gemm.hip) and the one-layer-per-launch kernel
-// (layer.hip) run the same code.
+// The body itself is gemm_body.inc, included by the per-operation kernel
+// (gemm_kernel, gemm.hip) and by gemm_body below, which takes its workgroup
+// index and count as arguments for the one-layer-per-launch kernel
+// (layer.hip): both run the same code.
 #pragma once
 #include "qdec_common.h"
 #include "qdec_kernels.h"
