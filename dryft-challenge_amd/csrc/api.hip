@@ -618,6 +618,10 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
   if (!pair_ok)
     return set_error(QDEC_EINVAL, "qdec_prefill_gemm: tile %d x %d (0 x 0, 256 x 128, 256 x 256 or 64 x 64)",
                      trows, tcols);
+  // Buffers of fewer whole 256-row tiles than the call covers (a short
+  // prompt padded to 64 rows) take the 64 x 64 tile only.
+  const bool whole256 = a->tiles % (kPgRows / 16) == 0;
+  if (trows == 0 && !whole256) trows = 64, tcols = 64;
   if (trows == 0) {
     const int64_t row_tiles = a->tiles / 16;
     if (a->n % 256 == 0 && (a->n / 256) * row_tiles >= 600) {
@@ -631,9 +635,10 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
   if (a->rows < 1 || a->k < kPgStageK || a->k % kPgStageK || a->n < tcols || a->n % tcols)
     return set_error(QDEC_EINVAL, "qdec_prefill_gemm: rows %d n %d k %d (n a multiple of %d, k of %d)", a->rows,
                      a->n, a->k, tcols, kPgStageK);
-  if (a->tiles < 1 || a->tiles % (kPgRows / 16) || a->rows > a->tiles * 16)
-    return set_error(QDEC_EINVAL, "qdec_prefill_gemm: tiles %d must be a multiple of %d covering %d rows", a->tiles,
-                     kPgRows / 16, a->rows);
+  const int gran = (trows == 64 ? kPgRowsSmall : kPgRows) / 16;
+  if (a->tiles < 1 || a->tiles % gran || a->rows > a->tiles * 16)
+    return set_error(QDEC_EINVAL, "qdec_prefill_gemm: tiles %d must be a multiple of %d (tile %d x %d) covering %d rows",
+                     a->tiles, gran, trows, tcols, a->rows);
   if ((f & QDEC_RES_OUT) && (!a->res || a->out_frag))
     return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_gemm: RES_OUT needs res and a row-major out");
   if (a->out_frag != 0 && a->out_frag != 1) return set_error(QDEC_EINVAL, "qdec_prefill_gemm: out_frag must be 0 or 1");

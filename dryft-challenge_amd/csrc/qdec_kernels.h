@@ -132,8 +132,10 @@ size_t layer_attn_lds_bytes();
 // ---- prefill (prefill.hip)
 // Product tiles of a workgroup (activation rows x weight rows): 256 x 128,
 // 256 x 256 or 64 x 64; k a multiple of kPgStageK; the activation buffers
-// hold whole kPgRows row tiles.
+// hold whole row tiles of the tile used: kPgRows rows, or kPgRowsSmall with
+// the 64 x 64 tile (the only one a call of fewer whole kPgRows tiles takes).
 constexpr int kPgRows = 256;
+constexpr int kPgRowsSmall = 64;
 constexpr int kPgStageK = 64;
 struct PgemmParams {
   const uint16_t *x;

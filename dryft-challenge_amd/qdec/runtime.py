@@ -41,8 +41,11 @@ ATTN_MAX_T = 16
 # the 256 x 256 product tile (32 x 4096 prompts: 1.33 s at 16K rows, 1.27 s
 # at 32K, 1.29 s at 64K; the tokens are the same for any chunking).
 PREFILL_ROWS = 32768
-# Row tile of the prefill product (kPgRows of qdec_kernels.h).
+# Row tile of the prefill product (kPgRows of qdec_kernels.h); a chunk of
+# fewer rows is padded to PREFILL_ROW_TILE_SMALL instead (kPgRowsSmall, the
+# 64 x 64 tile), see prefill_tiles.
 PREFILL_ROW_TILE = 256
+PREFILL_ROW_TILE_SMALL = 64
 # lm_head output tiles per workgroup from 2 rows (the role plan's 4 stays at
 # 1 row).  Grouping changes no sum and the argmax partials are scanned
 # lowest index first, so tokens and logits do not depend on it (MI355X,
@@ -77,6 +80,15 @@ WIDE_MIN_ROWS = 17
 
 def round_up(x, m):
     return (x + m - 1) // m * m
+
+
+def prefill_tiles(rows):
+    """16-row tiles of a prefill chunk of ``rows`` rows: rows rounded up to
+    PREFILL_ROW_TILE_SMALL below PREFILL_ROW_TILE, else to PREFILL_ROW_TILE.
+    So a short prompt's products run over its rows rounded up to 64, not to
+    a whole 256-row tile."""
+    g = PREFILL_ROW_TILE_SMALL if rows < PREFILL_ROW_TILE else PREFILL_ROW_TILE
+    return round_up(rows, g) // 16
 
 
 class ModelConfig:
@@ -596,13 +608,28 @@ class DecodeState:
     # ------------------------------------------------------------- prefill
     def prefill(self, prompt, stream=None):
         """Fill cache slots ``0 .. S-1`` from ``prompt`` ``[B, S]`` (device
-        int64) with the prefill kernels (``Prefill``); returns with
-        ``ids[:B]`` = the first generated token and ``lens[:] = S``."""
+        int64) with the prefill kernels (``Prefill``), or with one decode
+        step when the prompt fits one (``prefill_steps``); returns with
+        ``ids[:B]`` = the first generated token, ``logits[:B]`` (if kept) its
+        logits and ``lens[:] = S``."""
         B, S = prompt.shape
         if B != self.batch:
             raise ValueError(f"prompt batch {B} != state batch {self.batch}")
         if S < 1 or S >= self.cap:
             raise ValueError(f"prompt length {S} must be in [1, {self.cap})")
+        if S <= max_rows_per_seq(B):
+            # A prompt one decode step holds goes through the decode kernels:
+            # with few rows the prefill products have too few workgroups
+            # (MI355X, time to the first token, 16 tokens: 3.08 ms against
+            # 5.35 at batch 1, 4.51 against 5.50 at batch 4; 8 tokens at
+            # batch 8: 4.30 against 5.50).  The rule depends on (batch,
+            # length) only, and the decode kernels give the same bits in any
+            # number of steps, so plain and speculative states agree.
+            self.prefill_steps(prompt, stream=stream)
+            t = (S - 1) % self.max_t + 1
+            if self.logits is not None and t > 1:  # logits[:B]: each sequence's last position
+                self.logits[:B].copy_(self.logits[:B * t].view(B, t, -1)[:, t - 1].clone())
+            return
         pf = getattr(self, "_prefill", None)
         if pf is None or pf.chunk < min(S, pf.max_chunk):
             pf = self._prefill = Prefill(self, S)
@@ -650,7 +677,7 @@ class Prefill:
         self.state = state
         self.max_chunk = max(1, rows // B)
         self.chunk = min(prompt_len, self.max_chunk)
-        rows = round_up(B * self.chunk, PREFILL_ROW_TILE)
+        rows = prefill_tiles(B * self.chunk) * 16
         dev, bf = state.model.device, torch.bfloat16
         self.h = torch.zeros((rows, c.hidden), dtype=bf, device=dev)
         self.xn = torch.zeros((rows * c.hidden,), dtype=bf, device=dev)
@@ -676,7 +703,7 @@ class Prefill:
         for c0 in range(0, S, self.chunk):
             T = min(self.chunk, S - c0)
             R = B * T
-            tiles = round_up(R, PREFILL_ROW_TILE) // 16
+            tiles = prefill_tiles(R)
             self.ids[:R].view(B, T).copy_(prompt[:, c0:c0 + T])
             e = capi.EmbedArgs()
             e.ids, e.emb, e.h = self.ids.data_ptr(), m.emb.data_ptr(), self.h.data_ptr()

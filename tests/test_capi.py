@@ -236,7 +236,8 @@ def _pgemm(**kw):
     (dict(tile_rows=256, tile_cols=64), -1, "tile 256 x 64"),
     (dict(tile_cols=128), -1, "tile 0 x 128"),
     (dict(k=96), -1, "k of 64"),
-    (dict(tiles=24), -1, "tiles"),
+    (dict(tiles=24, tile_rows=256, tile_cols=128), -1, "multiple of 16"),  # 256-row tiles: whole ones
+    (dict(tiles=22), -1, "multiple of 4"),  # 64-row granularity otherwise
     (dict(rows=513), -1, "tiles"),
     (dict(flags=capi.RES_OUT), -3, "RES_OUT"),
     (dict(flags=capi.RES_OUT, res=16, out_frag=1), -3, "RES_OUT"),

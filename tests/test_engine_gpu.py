@@ -105,12 +105,13 @@ def v_rows(v):
     return v.reshape(*lead, cap // 8, d, 8).transpose(-1, -2).reshape(*lead, cap, d)
 
 
-@pytest.mark.parametrize("B,S,seed", [(1, 100, 11), (3, 70, 12)])
+@pytest.mark.parametrize("B,S,seed", [(1, 100, 11), (3, 70, 12), (2, 12, 13), (1, 16, 14)])
 def test_prefill_vs_oracle_and_chunking(engine, oracle, B, S, seed):
-    """The matrix-core prefill against the oracle's forward over the whole
-    prompt (first-token logits and the filled K/V slots), against the
-    decode-kernel route, and bit for bit against itself in 16-position
-    chunks."""
+    """The prefill against the oracle's forward over the whole prompt
+    (first-token logits and the filled K/V slots), against the decode-kernel
+    route, and bit for bit against itself in 16-position chunks.  Prompts
+    one decode step holds (12 and 16 tokens here) take the decode-kernel
+    route themselves."""
     from qdec.runtime import DecodeState, Prefill
     prompt = prompts(B, S, seed)
     dprompt = prompt.to(engine.device)
@@ -135,11 +136,15 @@ def test_prefill_vs_oracle_and_chunking(engine, oracle, B, S, seed):
     t_last = (S - 1) % st2.max_t + 1
     steps_logits = st2.logits[:B * t_last].view(B, t_last, -1)[:, t_last - 1].float().cpu()
     assert normalized_max_err(steps_logits, ref).max().item() <= TOL
+    from qdec.runtime import max_rows_per_seq
+    if S <= max_rows_per_seq(B):  # prefill took this very route
+        assert torch.equal(st2.k_cache, kc) and torch.equal(st2.v_cache, vc)
+        assert torch.equal(steps_logits, logits) and torch.equal(st2.ids[:B].cpu(), ids)
     # chunking does not change a bit
     st3 = DecodeState(engine.model, B, S + 18, max_t=16, keep_logits=True)
     st3._prefill = Prefill(st3, S, rows=16 * B)
     st3.prefill(dprompt)
-    assert st3._prefill.chunk == 16
+    assert st3._prefill.chunk == min(16, S)
     assert torch.equal(st3.k_cache, kc) and torch.equal(st3.v_cache, vc)
     assert torch.equal(st3.ids[:B].cpu(), ids)
 

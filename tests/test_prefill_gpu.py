@@ -141,6 +141,24 @@ def test_prefill_gemm_exact_small_ints(lib, rows, n, k, tile):
     assert torch.equal(frag_to_rows(fr, rows, n, tiles).float(), ref)
 
 
+@pytest.mark.parametrize("tile", [(64, 64), (0, 0)])
+@pytest.mark.parametrize("rows,n,k", [(1, 256, 64), (37, 384, 192), (64, 128, 256), (130, 512, 512)])
+def test_prefill_gemm_64_row_padding(lib, rows, n, k, tile):
+    """Buffers padded to 64 rows (a short prompt): the 64 x 64 tile, picked
+    automatically, gives the exact products; 256-row tiles are refused."""
+    from qdec import capi
+    x, w = small_ints(rows, k, seed=rows + 7), small_ints(n, k, seed=n + k + 7)
+    tiles = round_up(rows, 64) // 16
+    xf, wp = to_frag(lib, x, tiles), pack(lib, w)
+    ref = x.float() @ w.float().T
+    assert torch.equal(pgemm(lib, xf, wp, rows, n, k, tiles, tile=tile).float(), ref)
+    fr = pgemm(lib, xf, wp, rows, n, k, tiles, out_frag=1, tile=tile)
+    assert torch.equal(frag_to_rows(fr, rows, n, tiles).float(), ref)
+    if tiles % 16:
+        with pytest.raises(capi.QdecError):
+            pgemm(lib, xf, wp, rows, n, k, tiles, tile=(256, 128))
+
+
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("rows,n,k", [(5, 256, 128), (300, 512, 2560), (512, 1024, 640)])
 def test_prefill_gemm_glu(lib, rows, n, k, tile):
