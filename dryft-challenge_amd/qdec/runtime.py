@@ -46,6 +46,10 @@ PREFILL_ROWS = 32768
 # 64 x 64 tile), see prefill_tiles.
 PREFILL_ROW_TILE = 256
 PREFILL_ROW_TILE_SMALL = 64
+# A prompt of at most this many rows in all (batch x length) runs its layer
+# products through the decode GEMMs (qdec_gemm) instead of the matrix-core
+# prefill products, which make too few workgroups at so few rows.
+PREFILL_SKINNY_ROWS = GEMM_MAX_ROWS
 # lm_head output tiles per workgroup from 2 rows (the role plan's 4 stays at
 # 1 row).  Grouping changes no sum and the argmax partials are scanned
 # lowest index first, so tokens and logits do not depend on it (MI355X,
@@ -665,8 +669,11 @@ class Prefill:
     rownorm -> QKV product -> head norm / RoPE / cache fill -> causal
     attention over the cache -> O product + residual -> rownorm -> gate/up
     product with SwiGLU -> down product + residual, the products on the
-    matrix cores (qdec_prefill_gemm).  After the last chunk the final row of
-    each sequence goes through the decode lm_head + argmax.
+    matrix cores (qdec_prefill_gemm).  A prompt of at most
+    PREFILL_SKINNY_ROWS rows runs its products as the decode GEMMs instead
+    (qdec_gemm over all its rows, each weight read once; MI355X, one
+    sequence: see DecodeState.prefill).  After the last chunk the final row
+    of each sequence goes through the decode lm_head + argmax.
 
     Replaces engine/engine.py:448-490 (``_layers_forward`` over the whole
     prompt, ``_attend_prefill``, ``_prefill``)."""
@@ -677,6 +684,9 @@ class Prefill:
         self.state = state
         self.max_chunk = max(1, rows // B)
         self.chunk = min(prompt_len, self.max_chunk)
+        # The whole prompt in one chunk of at most PREFILL_SKINNY_ROWS rows:
+        # the decode GEMMs (see _skinny_args).
+        self.skinny = B * prompt_len <= min(PREFILL_SKINNY_ROWS, B * self.max_chunk)
         rows = prefill_tiles(B * self.chunk) * 16
         dev, bf = state.model.device, torch.bfloat16
         self.h = torch.zeros((rows, c.hidden), dtype=bf, device=dev)
@@ -685,6 +695,53 @@ class Prefill:
         self.att = torch.zeros((rows * c.nq * c.head_dim,), dtype=bf, device=dev)
         self.act = torch.zeros((rows * c.inter,), dtype=bf, device=dev)
         self.ids = torch.zeros((rows,), dtype=torch.int64, device=dev)
+        self.partial = self.counters = None
+
+    def _skinny_args(self, role, layer, R):
+        """qdec_gemm arguments of one layer product over all R prompt rows
+        (row b*S + t): x of QKV and gate/up is the residual h (row-major,
+        NORM_IN), the attention output comes in fragment order, and gate/up
+        hands its SwiGLU rows to down in fragment order from FRAG_ROWS rows,
+        as the decode step does.  Plans as the decode step's for R rows
+        (two tiles per wave at 17-32 rows), without a k split."""
+        st, m, c = self.state, self.state.model, self.state.model.cfg
+        ksplit, waves, _ = m.plans[role]
+        if role == "qkv" and R >= WIDE_MIN_ROWS:
+            waves = 8
+        a = capi.GemmArgs()
+        a.eps, a.rows, a.ksplit, a.waves, a.tiles_per_wg = c.eps, R, 1, waves, 1
+        frag = 1 if R >= FRAG_ROWS else 0
+        if role == "qkv":
+            a.x, a.w, a.out, a.norm_w = self.h.data_ptr(), m.w_qkv[layer].data_ptr(), self.qkv.data_ptr(), \
+                m.in_w[layer].data_ptr()
+            a.n, a.k, a.flags = c.n_qkv, c.hidden, capi.NORM_IN
+        elif role == "o":
+            a.x, a.w, a.res = self.att.data_ptr(), m.w_o[layer].data_ptr(), self.h.data_ptr()
+            a.n, a.k, a.flags, a.x_frag = c.hidden, c.nq * c.head_dim, capi.RES_OUT, 1
+        elif role == "gate_up":
+            a.x, a.w, a.out, a.norm_w = self.h.data_ptr(), m.w_gu[layer].data_ptr(), self.act.data_ptr(), \
+                m.post_w[layer].data_ptr()
+            a.n, a.k, a.flags, a.out_frag = c.inter, c.hidden, capi.NORM_IN | capi.GLU, frag
+        else:
+            a.x, a.w, a.res = self.act.data_ptr(), m.w_down[layer].data_ptr(), self.h.data_ptr()
+            a.n, a.k, a.flags, a.x_frag = c.hidden, c.inter, capi.RES_OUT, frag
+        if role in ("qkv", "down") and WIDE_MIN_ROWS <= R <= 32 and (a.n // 16) % WIDE_TILES == 0:
+            a.tiles_per_wg = WIDE_TILES
+        if self.partial is not None:
+            a.partial, a.counters = self.partial.data_ptr(), self.counters.data_ptr()
+        return a
+
+    def _skinny_workspace(self, R):
+        """Scratch of the decode GEMMs over R rows (the plan, and so its
+        scratch, depends on the row count); grown, never shrunk."""
+        pb = cb = 16
+        for role in ("qkv", "o", "gate_up", "down"):
+            p_, c_ = self.state.lib.gemm_workspace(self._skinny_args(role, 0, R))
+            pb, cb = max(pb, p_), max(cb, c_)
+        if self.partial is None or self.partial.numel() * 4 < pb or self.counters.numel() * 4 < cb:
+            dev = self.state.model.device
+            self.partial = torch.zeros((pb // 4 + 4,), dtype=torch.float32, device=dev)
+            self.counters = torch.zeros((cb // 4 + 4,), dtype=torch.int32, device=dev)
 
     def _gemm(self, x, w, out, n, k, rows, tiles, flags=0, res=None, out_frag=0):
         a = capi.PgemmArgs()
@@ -720,6 +777,19 @@ class Prefill:
             at.qkv, at.out, at.sm_scale = self.qkv.data_ptr(), self.att.data_ptr(), D ** -0.5
             at.batch, at.t_rows, at.pos0, at.nq, at.nkv = B, T, c0, c.nq, c.nkv
             at.head_dim, at.cap, at.tiles = D, st.cap, tiles
+            if self.skinny:
+                self._skinny_workspace(R)
+                at.tiles = -(-R // 16)  # the fragment order of the decode GEMMs
+                for i in range(c.n_layers):
+                    lib.gemm(self._skinny_args("qkv", i, R), s)
+                    qk.q_norm_w, qk.k_norm_w = m.q_norm[i].data_ptr(), m.k_norm[i].data_ptr()
+                    qk.k_cache, qk.v_cache = st.k_cache[i].data_ptr(), st.v_cache[i].data_ptr()
+                    lib.prefill_qk(qk, s)
+                    at.k_cache, at.v_cache = qk.k_cache, qk.v_cache
+                    lib.prefill_attn(at, s)
+                    for role in ("o", "gate_up", "down"):
+                        lib.gemm(self._skinny_args(role, i, R), s)
+                continue
             g_qkv = self._gemm(self.xn, m.w_qkv[0], self.qkv, c.n_qkv, H, R, tiles)
             g_o = self._gemm(self.att, m.w_o[0], self.h, H, c.nq * D, R, tiles, capi.RES_OUT, res=self.h)
             g_gu = self._gemm(self.xn, m.w_gu[0], self.act, 2 * c.inter, H, R, tiles, capi.GLU, out_frag=1)

@@ -105,13 +105,14 @@ def v_rows(v):
     return v.reshape(*lead, cap // 8, d, 8).transpose(-1, -2).reshape(*lead, cap, d)
 
 
-@pytest.mark.parametrize("B,S,seed", [(1, 100, 11), (3, 70, 12), (2, 12, 13), (1, 16, 14)])
+@pytest.mark.parametrize("B,S,seed", [(1, 100, 11), (3, 70, 12), (2, 12, 13), (1, 16, 14), (1, 40, 15), (3, 21, 16)])
 def test_prefill_vs_oracle_and_chunking(engine, oracle, B, S, seed):
     """The prefill against the oracle's forward over the whole prompt
     (first-token logits and the filled K/V slots), against the decode-kernel
     route, and bit for bit against itself in 16-position chunks.  Prompts
     one decode step holds (12 and 16 tokens here) take the decode-kernel
-    route themselves."""
+    route themselves; prompts of at most PREFILL_SKINNY_ROWS rows (40 and
+    3 x 21 here) run their products as the decode GEMMs."""
     from qdec.runtime import DecodeState, Prefill
     prompt = prompts(B, S, seed)
     dprompt = prompt.to(engine.device)
@@ -140,13 +141,21 @@ def test_prefill_vs_oracle_and_chunking(engine, oracle, B, S, seed):
     if S <= max_rows_per_seq(B):  # prefill took this very route
         assert torch.equal(st2.k_cache, kc) and torch.equal(st2.v_cache, vc)
         assert torch.equal(steps_logits, logits) and torch.equal(st2.ids[:B].cpu(), ids)
-    # chunking does not change a bit
+    # chunking does not change a bit of the matrix-core route (the other
+    # routes are checked against the oracle instead)
+    from qdec.runtime import PREFILL_SKINNY_ROWS
     st3 = DecodeState(engine.model, B, S + 18, max_t=16, keep_logits=True)
     st3._prefill = Prefill(st3, S, rows=16 * B)
     st3.prefill(dprompt)
     assert st3._prefill.chunk == min(16, S)
-    assert torch.equal(st3.k_cache, kc) and torch.equal(st3.v_cache, vc)
-    assert torch.equal(st3.ids[:B].cpu(), ids)
+    if S > max_rows_per_seq(B) and B * S > PREFILL_SKINNY_ROWS:
+        assert torch.equal(st3.k_cache, kc) and torch.equal(st3.v_cache, vc)
+        assert torch.equal(st3.ids[:B].cpu(), ids)
+    elif S > max_rows_per_seq(B):
+        assert not st3._prefill.skinny  # 16-position chunks: the products
+        for got, want in ((st3.k_cache[:, :, :, :S].float().cpu(), okc[:, :, :, :S]),
+                          (v_rows(st3.v_cache.float().cpu())[:, :, :, :S], ovc[:, :, :, :S])):
+            assert (got - want).abs().max().item() <= TOL * want.abs().max().item()
 
 
 def test_generate_matches_eager_steps(engine):
