@@ -56,8 +56,14 @@ PREFILL_SKINNY_ROWS = GEMM_MAX_ROWS
 # ms/step at 4 vs 8 tiles: batch 8 3.055 -> 3.031, batch 32 3.78 -> 3.72;
 # batch 1 2.160 vs 2.170).
 LM_TILES_BATCHED = 8
-# Plain decode up to this batch merges attention chunks in the O projection.
-MERGE_IN_O_MAX_BATCH = 4
+# Plain decode up to this batch merges attention chunks in the O projection;
+# above it the attention's last-arriving chunk merges them.  Same-box A/B,
+# ms per step (merge in O / in the attention): batch 1 2.129 / 2.203 (512
+# prompt), 2.228 / 2.320 (2048); batch 2 2.282 / 2.347 (512), 2.294 / 2.353
+# (1024), 2.507 / 2.551 (4096); batch 3 2.427 / 2.413 (1024), 2.403 / 2.385
+# (256); batch 4 2.538 / 2.474 (512), 2.569 / 2.483 (1024), 2.866 / 2.767
+# (4096).  Both give the same bits.
+MERGE_IN_O_MAX_BATCH = 2
 # qdec_layer (one launch per layer) takes plain decode up to this batch: its
 # GEMM stages stage their rows from registers (kLayerMaxRows).
 LAYER_MAX_BATCH = 4
@@ -401,9 +407,10 @@ class DecodeState:
 
     # ----------------------------------------------------------- arguments
     def _merge_in_o(self, t_rows):
-        """Plain decode of up to 4 sequences: the attention leaves its chunk
-        partials and the O projection merges them while staging its
-        activations (no arrival pass); bit-identical to the merged output."""
+        """Plain decode of up to MERGE_IN_O_MAX_BATCH sequences: the
+        attention leaves its chunk partials and the O projection merges them
+        while staging its activations (no arrival pass); bit-identical to
+        the merged output."""
         return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH
 
     def _hb(self, layer):
@@ -556,8 +563,9 @@ class DecodeState:
     # ------------------------------------------------ one layer per launch
     def layer_supported(self):
         """Whether qdec_layer takes this state's plain decode steps: up to
-        LAYER_MAX_BATCH sequences, attention partials merged in O."""
-        return self.batch <= LAYER_MAX_BATCH and self._merge_in_o(1)
+        LAYER_MAX_BATCH sequences (its O stage always merges the attention
+        partials, whatever MERGE_IN_O_MAX_BATCH says for five launches)."""
+        return self.batch <= LAYER_MAX_BATCH
 
     def layer_gemm_args(self, role, layer, x_attn=None):
         """A GEMM stage of qdec_layer: the role's arguments under the layer
