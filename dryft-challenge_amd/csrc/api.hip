@@ -611,7 +611,7 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
   // gate/up ~+10%, down +6%, O even with 640 workgroups; at 8K rows O and
   // down, 320 workgroups, are 10% faster on 256 x 128), 256 x 128 from 512,
   // else 64 x 64 (a 512-token prompt: O and down would have 40 workgroups
-  // of 256 x 128).
+  // of 256 x 128) -- unless one round of large tiles fills 128-256 CUs.
   int trows = a->tile_rows, tcols = a->tile_cols;
   const bool pair_ok = (trows == 0 && tcols == 0) || (trows == 256 && (tcols == 128 || tcols == 256)) ||
                        (trows == 64 && tcols == 64);
@@ -623,10 +623,18 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
   const bool whole256 = a->tiles % (kPgRows / 16) == 0;
   if (trows == 0 && !whole256) trows = 64, tcols = 64;
   if (trows == 0) {
+    // Workgroups of each large tile; from 600 (256 x 256) or 512 (256 x 128)
+    // they run in several rounds.  Below that a large tile still pays when
+    // one round of them covers half to all of the 256 CUs: the prefill of
+    // one sequence on MI355X, ms (64 x 64 / chosen), gate/up 256 x 256 at
+    // 512 rows 9.46 / 8.67 and at 768 rows 12.41 / 10.49, gate/up 256 x 128
+    // at 256 rows 7.11 / 6.85, QKV 256 x 128 at 1024 rows 14.62 / 14.11.
     const int64_t row_tiles = a->tiles / 16;
-    if (a->n % 256 == 0 && (a->n / 256) * row_tiles >= 600) {
+    const int64_t w256 = a->n % 256 == 0 ? (a->n / 256) * row_tiles : 0;
+    const int64_t w128 = a->n % 128 == 0 ? (a->n / 128) * row_tiles : 0;
+    if (w256 >= 600 || (w256 >= 128 && w256 <= 256)) {
       trows = 256, tcols = 256;
-    } else if (a->n % 128 == 0 && (a->n / 128) * row_tiles >= 512) {
+    } else if (w128 >= 512 || (w128 >= 128 && w128 <= 256)) {
       trows = 256, tcols = 128;
     } else {
       trows = 64, tcols = 64;
