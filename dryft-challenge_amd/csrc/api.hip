@@ -674,9 +674,9 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream) {
 int qdec_prefill_qk(const qdec_prefill_qk_args *a, qdec_stream_t stream) {
   if (!a || !a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->k_cache || !a->v_cache)
     return set_error(QDEC_EINVAL, "qdec_prefill_qk: null pointer");
-  if (a->head_dim != 128 || a->nq < 1 || a->nkv < 1)
-    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_qk: head_dim %d nq %d nkv %d (head_dim 128)", a->head_dim, a->nq,
-                     a->nkv);
+  if (a->head_dim != 128 || a->nq < 1 || a->nkv < 1 || a->nq + a->nkv > kPqMaxHeads)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_qk: head_dim %d nq %d nkv %d (head_dim 128, nq + nkv <= %d)",
+                     a->head_dim, a->nq, a->nkv, kPqMaxHeads);
   if (a->batch < 1 || a->t_rows < 1 || a->pos0 < 0 || a->cap < 32 || a->cap % 32 || a->pos0 + a->t_rows > a->cap)
     return set_error(QDEC_EINVAL, "qdec_prefill_qk: batch %d t_rows %d pos0 %d cap %d", a->batch, a->t_rows, a->pos0,
                      a->cap);

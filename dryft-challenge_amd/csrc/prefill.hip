@@ -302,8 +302,14 @@ __global__ void __launch_bounds__(128 * NWM, 1) pgemm_kernel(const PgemmParams p
 }
 
 // ------------------------------------------------------- head norm + RoPE
+constexpr int kPqHeadsPerWave = kPqMaxHeads / 4;  // per wave of the per-row kernel
+
 // Few rows: one workgroup per row, wave w normalising and rotating heads w,
-// w+4, ...; the values go to the V cache element by element.
+// w+4, ...  The values move in groups of 8 slots, the channel-major V
+// cache's 16-byte cells: the row that starts a group (its slot a multiple of
+// 8, or the call's first row) writes every row of the group that the call
+// holds, one vector per (kv head, channel) when all 8 are there, element by
+// element at the call's ragged ends.
 __global__ void __launch_bounds__(256) pqk_row_kernel(const PqkParams p) {
   constexpr int D = 128;
   const int m = blockIdx.x;
@@ -316,18 +322,40 @@ __global__ void __launch_bounds__(256) pqk_row_kernel(const PqkParams p) {
   const uint32_t sw = *reinterpret_cast<const uint32_t *>(p.sin_tab + (size_t)pos * D + 2 * lane);
   const uint32_t qw = *reinterpret_cast<const uint32_t *>(p.q_norm_w + 2 * lane);
   const uint32_t kw = *reinterpret_cast<const uint32_t *>(p.k_norm_w + 2 * lane);
-  for (int h = wave; h < p.nq + p.nkv; h += 4) {
-    uint32_t *cell = reinterpret_cast<uint32_t *>(row + (size_t)h * D + 2 * lane);
-    const uint32_t o = head_norm_rope2(*cell, h < p.nq ? qw : kw, cw, sw, p.eps);
+  // Every head of this wave loaded before the first is reduced, so their
+  // latencies overlap (the host admits at most 4 * kPqHeadsPerWave heads).
+  const int nh = p.nq + p.nkv;
+  uint32_t raw[kPqHeadsPerWave];
+#pragma unroll
+  for (int j = 0; j < kPqHeadsPerWave; ++j) {
+    const int h = wave + 4 * j;
+    raw[j] = h < nh ? *reinterpret_cast<const uint32_t *>(row + (size_t)h * D + 2 * lane) : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kPqHeadsPerWave; ++j) {
+    const int h = wave + 4 * j;
+    if (h >= nh) break;
+    const uint32_t o = head_norm_rope2(raw[j], h < p.nq ? qw : kw, cw, sw, p.eps);
     if (h < p.nq)
-      *cell = o;
+      *reinterpret_cast<uint32_t *>(row + (size_t)h * D + 2 * lane) = o;
     else
       *reinterpret_cast<uint32_t *>(p.k_cache + (((size_t)b * p.nkv + (h - p.nq)) * p.cap + pos) * D + 2 * lane) = o;
   }
+  if ((pos & 7) != 0 && t != 0) return;  // another row writes this group
+  const int n = min(8 - (pos & 7), p.t_rows - t);  // rows of the group in this call
   for (int i = threadIdx.x; i < p.nkv * D; i += blockDim.x) {
     const int kvh = i >> 7, ch = i & 127;
-    p.v_cache[((size_t)b * p.nkv + kvh) * p.cap * D + ((size_t)(pos >> 3) * D + ch) * 8 + (pos & 7)] =
-        row[(size_t)(p.nq + p.nkv + kvh) * D + ch];
+    const uint16_t *src = row + (size_t)(p.nq + p.nkv + kvh) * D + ch;
+    uint16_t *vb = p.v_cache + ((size_t)b * p.nkv + kvh) * p.cap * D + ((size_t)(pos >> 3) * D + ch) * 8;
+    if (n == 8) {
+      uint16_t v[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) v[r] = src[(size_t)r * width];
+      *reinterpret_cast<uint4 *>(vb) = make_uint4(v[0] | ((uint32_t)v[1] << 16), v[2] | ((uint32_t)v[3] << 16),
+                                                  v[4] | ((uint32_t)v[5] << 16), v[6] | ((uint32_t)v[7] << 16));
+    } else {
+      for (int r = 0; r < n; ++r) vb[(pos & 7) + r] = src[(size_t)r * width];
+    }
   }
 }
 
