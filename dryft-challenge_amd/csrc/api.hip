@@ -51,6 +51,7 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
     pb = sizeof(float) * (size_t)a->ksplit * a->rows * a->n * ((a->flags & QDEC_GLU) ? 2 : 1);
     cb = sizeof(uint32_t) * (size_t)ntiles;
   }
+  if (a->next_norm_w) cb = std::max(cb, (size_t)8);  // hand-over arrival / departure words
   size_t off = 0;
   if (p.xd && p.xpre) {
     off = (pb + 255) & ~(size_t)255;
@@ -87,6 +88,8 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: out_frag with RES_OUT or ARGMAX");
   if (a->x_frag && ((f & QDEC_NORM_IN) || a->x_attn))
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_frag needs no NORM_IN and no x_attn");
+  if ((f == QDEC_GLU || f == QDEC_ARGMAX) && !a->x_frag)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: GLU or ARGMAX without NORM_IN needs x_frag = 1");
   if (a->parts_out && (f != QDEC_RES_OUT || a->ksplit < 2))
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: parts_out needs RES_OUT alone and ksplit > 1");
   if (a->x_parts) {
@@ -247,6 +250,42 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   if (p->lds_bytes > (size_t)kGemmLdsX)
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: rows %d x waves %d needs %zu B of LDS", a->rows, a->waves,
                      p->lds_bytes);
+  // Norm hand-over to the next NORM_IN call (gemm_dev.h hand_over_row).
+  p->hnorm_w = nullptr;
+  p->hxn = nullptr;
+  p->hmerged = nullptr;
+  p->hthreads = 0;
+  p->hxt = 0;
+  p->hsync = nullptr;
+  if (a->next_norm_w) {
+    const int nblk = (ntiles / a->tiles_per_wg) * a->ksplit;
+    const int nr = mt * 16;
+    if (f != QDEC_RES_OUT || !p->xd || (a->ksplit > 1 && !a->parts_out))
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: next_norm_w needs RES_OUT alone on the direct path "
+                       "(x_frag = 1 or 17+ rows), ksplit 1 or parts_out");
+    if (a->parts_out && a->ksplit > kHandMaxParts)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: next_norm_w with parts_out merges at most %d splits", kHandMaxParts);
+    // Two 16-byte vectors of the row per thread of this call (hand_over_row).
+    const int vec_cap = a->next_threads > 64 * a->waves ? a->next_threads : 2 * a->next_threads;
+    if (a->next_threads < 64 || a->next_threads % 64 || a->next_threads > 2 * 64 * a->waves || a->n / 8 > vec_cap)
+      return set_error(QDEC_EUNSUPPORTED,
+                       "qdec_gemm: next_threads %d (a multiple of 64, at most twice this call's %d threads; n / 8 = %d "
+                       "vectors at most twice it, or at most it when it exceeds %d)",
+                       a->next_threads, 64 * a->waves, a->n / 8, 64 * a->waves);
+    if (nblk < nr)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: next_norm_w needs %d workgroups, the plan has %d", nr, nblk);
+    if (need_scratch && (!a->next_xn || !a->counters || (a->parts_out && !a->next_merged)))
+      return set_error(QDEC_EINVAL, "qdec_gemm: next_norm_w needs next_xn, counters and (with parts_out) next_merged");
+    if (!aligned16(a->next_norm_w) || (a->next_xn && !aligned16(a->next_xn)) ||
+        (a->next_merged && !aligned16(a->next_merged)))
+      return set_error(QDEC_EALIGN, "qdec_gemm: next_norm_w, next_xn and next_merged must be 16-byte aligned");
+    p->hnorm_w = reinterpret_cast<const uint16_t *>(a->next_norm_w);
+    p->hxn = reinterpret_cast<uint16_t *>(a->next_xn);
+    p->hmerged = reinterpret_cast<uint16_t *>(a->next_merged);
+    p->hthreads = a->next_threads;
+    p->hxt = mt;
+    p->hsync = a->counters;
+  }
   return QDEC_OK;
 }
 
@@ -380,7 +419,7 @@ int plan_layer(const qdec_layer_args *a, LayerParams *L, int *workgroups, size_t
     const bool direct = i == 3;
     if (ga[i]->flags != flags[i] || p.rows != at.batch || p.waves != 4 || p.ksplit != 1 || p.rw != rings[i] ||
         (p.xd != 0) != direct || (!direct && !p.xfast) || p.xt || p.xpre || p.tw != 1 || p.ofrag || p.xparts ||
-        p.parts_out || (p.amerge != 0) != (i == 1))
+        p.parts_out || p.hxn || (p.amerge != 0) != (i == 1))
       return set_error(QDEC_EUNSUPPORTED,
                        "qdec_layer: %s plan (flags 0x%x rows %d waves %d ksplit %d ring %d direct %d) is not the "
                        "layer kernel's",
@@ -491,6 +530,14 @@ int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes, size_t *
   if (partial_bytes) *partial_bytes = pb;
   if (counter_bytes) *counter_bytes = cb;
   return QDEC_OK;
+}
+
+int qdec_gemm_prepass(const qdec_gemm_args *a, int32_t *threads) {
+  GemmParams p;
+  const int rc = plan_gemm(a, &p, false);
+  if (rc != QDEC_OK) return rc;
+  if (threads) *threads = 64 * a->waves;
+  return (p.xd && p.xpre) ? 1 : 0;
 }
 
 int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream) {

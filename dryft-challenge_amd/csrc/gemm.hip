@@ -170,8 +170,10 @@ hipError_t launch_pass(const GemmParams &p, uint32_t flags, dim3 grid, dim3 bloc
 }  // namespace
 
 bool gemm_flags_supported(uint32_t flags) {
+  // GLU and ARGMAX alone: the direct path only (x_frag, the input a norm
+  // hand-over leaves), checked by the planner.
   return flags == 0u || flags == QDEC_NORM_IN || flags == (QDEC_NORM_IN | QDEC_GLU) || flags == QDEC_RES_OUT ||
-         flags == (QDEC_NORM_IN | QDEC_ARGMAX);
+         flags == (QDEC_NORM_IN | QDEC_ARGMAX) || flags == QDEC_GLU || flags == QDEC_ARGMAX;
 }
 
 bool gemm_fast_path(const GemmParams &p, uint32_t flags) {
@@ -201,6 +203,10 @@ hipError_t launch_direct(const GemmParams &p, uint32_t flags, dim3 grid, dim3 bl
     case 0u: hipLaunchKernelGGL((gemm_kernel<MT, 0u, RW, true, kFastRows, false, TW>), grid, block, lds, s, p); break;
     case QDEC_RES_OUT:
       hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT, RW, true, kFastRows, false, TW>), grid, block, lds, s, p);
+      break;
+    case QDEC_RES_OUT | kGemmHandOver:
+      hipLaunchKernelGGL((gemm_kernel<MT, QDEC_RES_OUT | kGemmHandOver, RW, true, kFastRows, false, TW>), grid, block,
+                         lds, s, p);
       break;
     case QDEC_ARGMAX:
       hipLaunchKernelGGL((gemm_kernel<MT, QDEC_ARGMAX, RW, true, kFastRows, false, TW>), grid, block, lds, s, p);
@@ -289,6 +295,7 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   const size_t lds = p.lds_bytes;
   if (p.xd) {
     GemmParams q = p;
+    if (p.hxn) flags |= kGemmHandOver;
     if (p.xpre) {
       const hipError_t e = launch_rownorm(p, block, (flags & QDEC_NORM_IN) != 0, s);
       if (e != hipSuccess) return e;

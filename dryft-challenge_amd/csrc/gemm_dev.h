@@ -188,6 +188,164 @@ __device__ __forceinline__ uint4 merge_res8(const float *__restrict__ parts, int
 // Pending split residual updates merged from registers (one row): at most
 // this many partials (the down projection leaves four).
 constexpr int kMergeParts = 4;
+static_assert(kHandMaxParts == kMergeParts, "a hand-over merges what the pre-pass keeps in registers");
+
+// Norm hand-over, the last step of a RES_OUT call that feeds a NORM_IN call
+// (template flag kGemmHandOver): that call's normalisation needs every output
+// tile of this one, so it is done here, after the last tile, instead of by a
+// pre-pass launch of the consumer.  Every workgroup, once its outputs are
+// stored (at device scope: a row is read back by a workgroup on another
+// XCD), takes an arrival ticket (hsync[0]); the last NR = hxt*16 to arrive
+// each take one row, wait until all nblk have arrived, and write that row
+// as the consumer's pre-pass (rownorm_kernel) would: the merged residual
+// with split partials, then bf16(norm_w * bf16(r * rstd)) in fragment
+// order.  The statistic follows a workgroup of hthreads threads -- virtual
+// thread t sums vectors t and t + hthreads, lanes in wave_sum's tree, then
+// virtual waves in order -- which this workgroup emulates when it is half
+// or twice that size (a zero contribution leaves an fp32 sum unchanged), so
+// the row is bit-identical to the pre-pass's.  Rows past `rows` are zeros.
+// The row that leaves last (hsync[1]) resets both words.  A wait past
+// kHandSpin polls (a workgroup that never arrives) writes a NaN row instead
+// of hanging.
+//
+// Its parameters are read from the kernel's argument segment (GemmParams is
+// gemm_kernel's only argument, at offset 0) through a pointer the compiler
+// cannot see through, so none of those loads is hoisted into the GEMM's loop,
+// where the scalar registers holding them would cost the loop a wave per
+// SIMD.  (Through the address of the parameter the whole block would be
+// copied to scratch.)
+typedef const __attribute__((address_space(4))) GemmParams *KernargParams;
+__device__ __forceinline__ uint4 nan8() { return make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u); }
+// The thread index comes from the lane count (mbcnt) and the wave index in
+// a scalar register (wave_s), so no vector register has to keep threadIdx
+// across the loop for it.
+__device__ __forceinline__ void hand_over_row(const int nblk, const int wave_s, float *s_red, uint32_t *s_flag) {
+  KernargParams pp = (KernargParams)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(pp));
+  const auto &p = *pp;
+  const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int wave = wave_s, tid = wave * 64 + lane;
+  const int R = blockDim.x, V = p.hthreads, NR = p.hxt * 16;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(p.hsync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int row = (int)old - (nblk - NR);
+    uint32_t ok = 1u;
+    if (row >= NR) row = -1;
+    if (row >= 0) {
+      uint32_t polls = 0;
+      while (__hip_atomic_load(p.hsync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (uint32_t)nblk) {
+        if (++polls >= kHandSpin) {
+          ok = 0u;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      const uint32_t d = __hip_atomic_fetch_add(p.hsync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == (uint32_t)NR - 1u) {
+        __hip_atomic_store(p.hsync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(p.hsync + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    s_flag[0] = (uint32_t)row;
+    s_flag[1] = ok;
+  }
+  __syncthreads();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const int m = (int)s_flag[0];
+  if (m < 0) return;
+  const bool ok = s_flag[1] != 0u;
+  const int k = p.n, nvec = k >> 3;
+  auto dst = [&](int v) {
+    return p.hxn + (((size_t)(v >> 2) * p.hxt + (m >> 4)) * 64 + (m & 15) + 16 * (v & 3)) * 8;
+  };
+  if (m >= p.rows) {
+    for (int v = tid; v < nvec; v += R) *reinterpret_cast<uint4 *>(dst(v)) = zero4();
+    return;
+  }
+  const uint16_t *xrow = reinterpret_cast<const uint16_t *>(p.res) + (size_t)m * k;
+  const bool parts = p.parts_out != nullptr;
+  // Two vector slots per thread.  Same size (nsl = 1): virtual thread tid,
+  // its vectors tid and tid + V.  Half the consumer's size (nsl = 2, where
+  // the plan ensures a row of at most V vectors): virtual threads tid and
+  // tid + R, one vector each.
+  const int nsl = V > R ? 2 : 1;
+  uint4 xv[2];
+  float ss[2] = {0.f, 0.f};
+  int vs[2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    const int t = nsl == 2 ? tid + sl * R : tid;
+    const int v = nsl == 2 ? t : t + sl * V;
+    vs[sl] = (t < V && v < nvec) ? v : -1;
+  }
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    const int v = vs[sl];
+    const int vv = v >= 0 ? v : 0;
+    if (parts) {
+      // bf16(x + bf16(((p0 + p1) + p2) + p3)): merge_res8's order and rounding
+      const uint4 x = *reinterpret_cast<const uint4 *>(xrow + 8 * vv);
+      const float *q = p.parts_out + (size_t)m * k + 8 * vv;
+      const size_t stride = (size_t)p.rows * k;
+      f32x4_t pa[kMergeParts][2];
+#pragma unroll
+      for (int part = 0; part < kMergeParts; ++part) {
+        const float *qp = q + (part < p.ksplit ? part : 0) * stride;
+        pa[part][0] = load_coherent4(qp);
+        pa[part][1] = load_coherent4(qp + 4);
+      }
+      f32x4_t s0 = pa[0][0], s1 = pa[0][1];
+#pragma unroll
+      for (int part = 1; part < kMergeParts; ++part)
+        if (part < p.ksplit) {
+          s0 += pa[part][0];
+          s1 += pa[part][1];
+        }
+      uint4 o;
+      o.x = pack2(lo16(x.x) + rbf(s0[0]), hi16(x.x) + rbf(s0[1]));
+      o.y = pack2(lo16(x.y) + rbf(s0[2]), hi16(x.y) + rbf(s0[3]));
+      o.z = pack2(lo16(x.z) + rbf(s1[0]), hi16(x.z) + rbf(s1[1]));
+      o.w = pack2(lo16(x.w) + rbf(s1[2]), hi16(x.w) + rbf(s1[3]));
+      xv[sl] = o;
+      if (v >= 0) *reinterpret_cast<uint4 *>(p.hmerged + (size_t)m * k + 8 * v) = ok ? o : nan8();
+    } else {
+      xv[sl] = ldv16<true>(xrow + 8 * vv);
+    }
+    if (v >= 0) {
+      float f[8];
+      unpack8(xv[sl], f);
+      float &acc = ss[nsl == 2 ? sl : 0];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += f[e] * f[e];
+    }
+  }
+  // The norm weights only now: their latency overlaps the reduction.
+  uint4 wv[2];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) wv[sl] = *reinterpret_cast<const uint4 *>(p.hnorm_w + 8 * (vs[sl] >= 0 ? vs[sl] : 0));
+  // s_red[w'] = sum of virtual wave w' (real wave w' mod R/64, slice w' / (R/64))
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl) {
+    if (sl >= nsl) break;
+    const float s = wave_sum(ss[sl]);
+    if (lane == 0) s_red[wave + sl * (R >> 6)] = s;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w2 = 0; w2 < (V >> 6); ++w2) t += s_red[w2];
+    s_red[16] = 1.0f / sqrtf(t / (float)k + p.eps);
+  }
+  __syncthreads();
+  const float rs = s_red[16];
+#pragma unroll
+  for (int sl = 0; sl < 2; ++sl)
+    if (vs[sl] >= 0) *reinterpret_cast<uint4 *>(dst(vs[sl])) = ok ? norm8(xv[sl], wv[sl], rs) : nan8();
+}
 
 // XP: the instantiation that merges a pending split residual update into its
 // one register-staged row (FR = 1); 0 elsewhere.

@@ -64,8 +64,24 @@ struct GemmParams {
   const float *xparts;
   int xnparts;
   uint16_t *xmerged;
+  // Norm hand-over (RES_OUT, direct path; gemm_dev.h hand_over_row): the
+  // next NORM_IN call's rows, normalised in fragment order with hxt M tiles
+  // (hxn), the merged residual with parts_out (hmerged), the consumer's
+  // workgroup size (hthreads), and the arrival / departure words (hsync).
+  const uint16_t *hnorm_w;
+  uint16_t *hxn;
+  uint16_t *hmerged;
+  int hthreads, hxt;
+  uint32_t *hsync;
   size_t lds_bytes;
 };
+// Template flag of the hand-over instantiations (beside the QDEC_* flags).
+constexpr uint32_t kGemmHandOver = 1u << 8;
+// Polls a hand-over row waits for the last arrival before it writes NaN.
+constexpr uint32_t kHandSpin = 1u << 22;
+// Split partials a hand-over merges (the pre-pass it replaces keeps them in
+// registers up to this many).
+constexpr int kHandMaxParts = 4;
 bool gemm_flags_supported(uint32_t flags);
 bool gemm_fast_path(const GemmParams &p, uint32_t flags);
 int gemm_ring(int ksw, uint32_t flags);

@@ -47,7 +47,8 @@ class GemmArgs(ctypes.Structure):
                 ("counters", P), ("ids_out", P), ("lens_inc", P), ("eps", F32), ("rows", I32),
                 ("n", I32), ("k", I32), ("flags", ctypes.c_uint32), ("ksplit", I32), ("waves", I32),
                 ("tiles_per_wg", I32), ("x_attn", P), ("x_frag", I32), ("out_frag", I32),
-                ("parts_out", P), ("x_parts", P), ("x_nparts", I32), ("x_merged", P)]
+                ("parts_out", P), ("x_parts", P), ("x_nparts", I32), ("x_merged", P),
+                ("next_norm_w", P), ("next_xn", P), ("next_merged", P), ("next_threads", I32)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -141,6 +142,8 @@ class Lib:
             fn.argtypes = [ctypes.POINTER(st), ctypes.POINTER(ctypes.c_size_t),
                            ctypes.POINTER(ctypes.c_size_t)]
             fn.restype = ctypes.c_int
+        so.qdec_gemm_prepass.argtypes = [ctypes.POINTER(GemmArgs), ctypes.POINTER(I32)]
+        so.qdec_gemm_prepass.restype = ctypes.c_int
 
     def _check(self, fn, rc):
         if rc != 0:
@@ -205,6 +208,15 @@ class Lib:
         self._check("qdec_gemm_workspace",
                     self.so.qdec_gemm_workspace(ctypes.byref(args), ctypes.byref(pb), ctypes.byref(cb)))
         return pb.value, cb.value
+
+    def gemm_prepass(self, args):
+        """(runs a normalisation pre-pass of its own, its workgroup size) of a
+        qdec_gemm call with these arguments."""
+        t = I32()
+        rc = self.so.qdec_gemm_prepass(ctypes.byref(args), ctypes.byref(t))
+        if rc < 0:
+            self._check("qdec_gemm_prepass", rc)
+        return rc == 1, t.value
 
     def attn_workspace(self, args):
         pb, cb = ctypes.c_size_t(), ctypes.c_size_t()

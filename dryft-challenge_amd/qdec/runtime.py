@@ -74,6 +74,17 @@ LAYER_MAX_BATCH = 4
 # with fragment order from 17 rows, 3.11 from 9; batch 12 3.18 / 3.15;
 # batch 8 (8-row plain steps) 2.96 / 2.95; batch 32 3.86 vs 4.09 row-major.
 FRAG_ROWS = 9
+# Norm hand-over: a RES_OUT call (O, or down) that feeds a NORM_IN call which
+# would normalise its rows in a pre-pass launch of its own (gate/up from 8
+# rows; the next QKV or the lm_head from 9) writes those rows itself, as its
+# last workgroups finish (qdec_gemm's next_norm_w), and the consumer runs as
+# a plain fragment-order call: one launch fewer, the same bits.  Off: on
+# MI355X the in-launch hand-off (device-scope output stores, the arrival
+# ticket, the wait, device-scope row loads) costs more than the launch it
+# saves.  Same-box A/B, ms per step with / without: batch 8 3.002 / 2.966,
+# batch 12 3.202 / 3.157, batch 20 4.138 / 4.011, batch 32 5.839 / 5.687
+# (tokens identical).
+HAND_OVER = False
 # Loss-free speculation needs identical arithmetic in the plain and verify
 # steps, so attention chunking depends on (batch, capacity) only.
 # k splits of the down projection from this batch size (see role_plan).
@@ -387,12 +398,16 @@ class DecodeState:
         self.lens = torch.zeros((batch,), dtype=torch.int32, device=dev)
         cos, sin = rope_tables(self.cap, D, c.theta)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
+        # Norm hand-over target: the consumer's rows in fragment order.
+        self.hand_over = HAND_OVER
+        self._hand_cache = {}
+        self.xn_hand = torch.zeros((round_up(R, 16) * H,), dtype=bf, device=dev)
         # scratch: sized for the largest call of every kernel.
         gw = 0
         gc = 1
         for role in ("qkv", "o", "gate_up", "down", "lm"):
             for t in range(1, self.max_t + 1):  # the plan (and its workspace) depends on the row count
-                a = self._gemm_args(role, 0, batch * t)
+                a = self._gemm_args(role, 0, batch * t, hand=self.hand_over)
                 pb, cb = self.lib.gemm_workspace(a)
                 gw, gc = max(gw, pb), max(gc, cb)
         self.gemm_partial = torch.zeros((max(gw, 16) // 4 + 4,), dtype=torch.float32, device=dev)
@@ -433,7 +448,42 @@ class DecodeState:
         else:
             a.x = self._hb(layer).data_ptr()
 
-    def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None, x_attn=None, pending=True):
+    def _hand_threads(self, prod_role, rows, last=False):
+        """Workgroup size of the NORM_IN call that reads what ``prod_role``
+        writes (O: gate/up; down: the next QKV, or the lm_head after the last
+        layer) when that call would run a normalisation pre-pass of its own
+        and ``prod_role`` can hand it its rows instead (qdec_gemm_prepass,
+        and the producer's plan accepting next_norm_w); else None.  Both
+        calls have ``rows`` rows, and the answer depends on nothing else."""
+        key = (prod_role, rows, last)
+        if key not in self._hand_cache:
+            c = self.model.cfg
+            cons = "gate_up" if prod_role == "o" else ("lm" if last else "qkv")
+            pre, threads = self.lib.gemm_prepass(self._gemm_args(cons, c.n_layers if last else 1, rows))
+            t = None
+            if pre:
+                pa = self._gemm_args(prod_role, 0, rows)
+                pa.next_norm_w, pa.next_threads = self.model.norm_w.data_ptr(), threads
+                try:
+                    self.lib.gemm_workspace(pa)
+                    t = threads
+                except capi.QdecError:
+                    t = None
+            self._hand_cache[key] = t
+        return self._hand_cache[key]
+
+    def _take_hand(self, a):
+        """A NORM_IN call whose producer handed it its normalised rows: a
+        plain fragment-order call on them."""
+        a.flags &= ~capi.NORM_IN
+        a.x, a.x_frag, a.norm_w = self.xn_hand.data_ptr(), 1, None
+        a.x_parts, a.x_nparts, a.x_merged = None, 0, None
+
+    def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None, x_attn=None, pending=True, hand=False):
+        """qdec_gemm arguments of ``role`` in ``layer`` over ``rows`` rows.
+        ``hand``: the arguments of the step's own sequence of calls, where O
+        and down hand the next NORM_IN call its rows when that pays
+        (_hand_threads) and that call takes them."""
         m, c = self.model, self.model.cfg
         ksplit, waves, tiles = self.plans[role]
         a = capi.GemmArgs()
@@ -485,6 +535,22 @@ class DecodeState:
         if hasattr(self, "gemm_partial"):
             a.partial = self.gemm_partial.data_ptr()
             a.counters = self.gemm_counters.data_ptr()
+        if hand:
+            L = c.n_layers
+            if role in ("o", "down"):
+                last = role == "down" and layer == L - 1
+                t = self._hand_threads(role, rows, last)
+                if t:
+                    nw = m.post_w[layer] if role == "o" else (m.norm_w if last else m.in_w[layer + 1])
+                    a.next_norm_w, a.next_xn, a.next_threads = nw.data_ptr(), self.xn_hand.data_ptr(), t
+                    if role == "down" and self.down_parts is not None:
+                        a.next_merged = self._hb(layer + 1).data_ptr()  # the consumer's x_merged
+            elif role == "gate_up" and self._hand_threads("o", rows):
+                self._take_hand(a)
+            elif role == "qkv" and layer > 0 and pending and self._hand_threads("down", rows):
+                self._take_hand(a)
+            elif role == "lm" and pending and self._hand_threads("down", rows, last=True):
+                self._take_hand(a)
         return a
 
     def _attn_args(self, layer, t_rows, partials=False):
@@ -537,14 +603,14 @@ class DecodeState:
             lib.gemm(self._cached_gemm("down", i, rows), s)
         if lm_head:
             a = self._gemm_args("lm", 0, rows, ids_out=ids_out,
-                                lens_inc=self.lens if (advance and t_rows == 1) else None)
+                                lens_inc=self.lens if (advance and t_rows == 1) else None, hand=self.hand_over)
             lib.gemm(a, s)
 
     def _cached_gemm(self, role, layer, rows, x_attn=None):
-        key = (role, layer, rows, x_attn is not None)
+        key = (role, layer, rows, x_attn is not None, self.hand_over)
         a = self._gemm_cache.get(key)
         if a is None:
-            a = self._gemm_args(role, layer, rows, x_attn=x_attn)
+            a = self._gemm_args(role, layer, rows, x_attn=x_attn, hand=self.hand_over)
             self._gemm_cache[key] = a
         return a
 

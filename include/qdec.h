@@ -130,6 +130,8 @@ struct qdec_attn_args;  /* below: the attention call a GEMM may take its x from 
  *             when every logit of the row is NaN);
  *             out (optional, may be NULL) receives the bf16 logits;
  *             lens_inc (optional) gets lens_inc[m] += 1 after the pick.
+ * flags: 0, NORM_IN, NORM_IN|GLU, RES_OUT, NORM_IN|ARGMAX; GLU and ARGMAX
+ * also without NORM_IN when x_frag = 1 (the input of a norm hand-over).
  * The summation order of every output element depends only on k, ksplit and
  * waves -- never on rows -- so a row's result is bit-identical whether it is
  * computed alone or inside a larger batch.
@@ -190,11 +192,43 @@ typedef struct {
   const float *x_parts;
   int32_t x_nparts;
   void *x_merged;
+  /* Norm hand-over (RES_OUT on the direct path, i.e. x_frag = 1 or 17+
+   * rows): this call also produces the input of the NORM_IN call that
+   * follows it, so that call runs as a plain x_frag = 1 call on next_xn
+   * (same flags without QDEC_NORM_IN, no x_parts) and launches no
+   * normalisation pre-pass.  Let r be the updated residual row: res after
+   * this call's update, or -- with parts_out -- bf16(res + bf16(((p0 + p1)
+   * + p2) + ...)), which is then also written to next_merged ([rows, n]
+   * bf16; res is still not touched).  Row m of next_xn (fragment order,
+   * ceil(rows / 16) M tiles, n columns; rows past `rows` zero) is
+   * bf16(next_norm_w * bf16(r * rsqrt(mean(r^2) + eps))), its statistic
+   * summed in the order a pre-pass of the consumer would use: pass
+   * next_threads = that call's workgroup size (qdec_gemm_prepass).  The
+   * result is bit-identical to the consumer's own pre-pass.  The last
+   * ceil(rows / 16) * 16 workgroups of this call to finish each take one
+   * row, after every workgroup has arrived (two words of the counters
+   * workspace; a wait longer than about 2^22 polls writes NaN rows).
+   * Needs next_threads a multiple of 64 and at most twice this call's
+   * workgroup size, n / 8 at most 2 * next_threads (at most next_threads
+   * when that exceeds this call's workgroup size), and at least
+   * ceil(rows / 16) * 16 workgroups (QDEC_EUNSUPPORTED otherwise).
+   * next_norm_w = NULL: off.
+   * No counterpart in the reference, whose fused.gemv epilogue leaves the
+   * statistic to the consumer's own pass (engine/kernels/fused.py:33-338). */
+  const void *next_norm_w; /* [n] bf16 */
+  void *next_xn;
+  void *next_merged;
+  int32_t next_threads;
 } qdec_gemm_args;
 int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream);
 /* Scratch sizes (bytes) a qdec_gemm call with these arguments needs. */
 int qdec_gemm_workspace(const qdec_gemm_args *a, size_t *partial_bytes,
                         size_t *counter_bytes);
+/* Whether a qdec_gemm call with these arguments normalises its rows in a
+ * pre-pass of its own (1) or not (0); *threads receives its workgroup size
+ * (the statistic order a norm hand-over to it must follow).  Negative: the
+ * arguments are invalid (the error of qdec_gemm). */
+int qdec_gemm_prepass(const qdec_gemm_args *a, int32_t *threads);
 
 /* --------------------------------------------------- GQA decode attention */
 

@@ -68,7 +68,8 @@ def _gemm(**kw):
     (dict(k=100), -1, "multiple of 32"),
     (dict(waves=9), -1, "waves"),
     (dict(ksplit=3), -1, "ksplit"),
-    (dict(flags=capi.GLU), -3, "not supported"),
+    (dict(flags=capi.GLU | capi.RES_OUT), -3, "not supported"),
+    (dict(flags=capi.GLU), -3, "x_frag = 1"),
     (dict(flags=capi.ARGMAX | capi.NORM_IN, ksplit=2), -3, "ksplit 1"),
     (dict(tiles_per_wg=3), -1, "tiles_per_wg"),
     (dict(x_frag=2), -1, "x_frag"),
@@ -96,6 +97,61 @@ def test_gemm_workspace_sizes(qlib):
     assert pb == 8 * (9496 // 4) and cb == 8 + 8 * 16  # one row: a 64-bit key per workgroup
     pb, cb = qlib.gemm_workspace(_gemm(flags=capi.NORM_IN, n=6144, k=2560))
     assert pb == 0 and cb == 0
+
+
+def test_gemm_prepass_query(qlib):
+    """Which NORM_IN calls normalise in a pre-pass launch of their own (the
+    consumers a norm hand-over serves), and with how many threads."""
+    gu = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4)
+    assert qlib.gemm_prepass(_gemm(rows=4, **gu)) == (False, 256)  # rows staged from registers
+    assert qlib.gemm_prepass(_gemm(rows=8, **gu)) == (True, 256)
+    assert qlib.gemm_prepass(_gemm(rows=8, flags=capi.NORM_IN, n=6144, k=2560)) == (False, 256)
+    assert qlib.gemm_prepass(_gemm(rows=20, flags=capi.NORM_IN, n=6144, k=2560, waves=8, tiles_per_wg=2)) == (True, 512)
+    assert qlib.gemm_prepass(_gemm(rows=20, flags=capi.RES_OUT, n=2560, k=4096, x_frag=1)) == (False, 256)
+    assert qlib.so.qdec_gemm_prepass(ctypes.byref(_gemm(rows=0)), None) == -1
+
+
+def test_gemm_glu_argmax_alone_need_fragment_order(qlib):
+    for f in (capi.GLU, capi.ARGMAX):
+        assert qlib.so.qdec_gemm(ctypes.byref(_gemm(flags=f, rows=20, n=9728 if f == capi.GLU else 151936,
+                                                    k=2560)), None) == -3
+        assert "x_frag" in qlib.last_error()
+    qlib.gemm_workspace(_gemm(flags=capi.GLU, rows=20, n=9728, k=2560, x_frag=1, out_frag=1))
+    qlib.gemm_workspace(_gemm(flags=capi.ARGMAX, rows=20, n=151936, k=2560, x_frag=1, tiles_per_wg=8))
+
+
+def _hand(**kw):
+    """An O-shaped RES_OUT call on the direct path handing over to gate/up."""
+    base = dict(flags=capi.RES_OUT, n=2560, k=4096, rows=20, waves=8, x_frag=1, next_norm_w=16, next_xn=16,
+                next_threads=256)
+    return _gemm(**{**base, **kw})
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(flags=0), -3, "RES_OUT alone"),
+    (dict(rows=4, x_frag=0, waves=8), -3, "direct path"),
+    (dict(ksplit=2), -3, "parts_out"),
+    (dict(ksplit=8, waves=4, parts_out=16), -3, "at most 4 splits"),
+    (dict(next_threads=96), -3, "next_threads"),
+    (dict(next_threads=1536), -3, "next_threads"),
+    (dict(next_threads=128), -3, "next_threads"),       # a 2560-wide row is 320 vectors: 2 per thread at most
+    (dict(waves=1, next_threads=128, k=256), -3, "next_threads"),  # 128 threads from 64: one vector each
+    (dict(n=256, k=4096, next_threads=64), -3, "workgroups"),  # 16 workgroups for 32 hand-over rows
+    (dict(next_xn=None), -1, "next_xn"),
+    (dict(counters=None), -1, "counters"),
+    (dict(ksplit=4, waves=4, parts_out=16, next_merged=None), -1, "next_merged"),
+    (dict(next_xn=24), -2, "16-byte"),
+])
+def test_gemm_hand_over_validation(qlib, kw, code, needle):
+    rc = qlib.so.qdec_gemm(ctypes.byref(_hand(**kw)), None)
+    assert rc == code, qlib.last_error()
+    assert needle in qlib.last_error()
+
+
+def test_gemm_hand_over_workspace(qlib):
+    # two counter words (arrival, departure) beyond what the call needs otherwise
+    assert qlib.gemm_workspace(_hand()) == (0, 8)
+    assert qlib.gemm_workspace(_hand(ksplit=4, waves=4, parts_out=16, next_merged=16, next_threads=512)) == (0, 8)
 
 
 def _attn(**kw):

@@ -254,6 +254,38 @@ def _same(a, b):
     return torch.equal(a.contiguous().view(torch.uint8), b.contiguous().view(torch.uint8))
 
 
+# The norm hand-over (O / down writing the next NORM_IN call's normalised
+# rows as their last workgroups finish) against the pre-pass launches it
+# replaces: plain steps at 8 rows (gate/up only), 12 (down without a k split
+# hands to 4-wave QKV and lm_head), 20 and 32 (down's four split partials
+# merged and handed to 8-wave QKV: a 4-wave producer emulating an 8-wave
+# statistic), and verify steps of 16 and 18 rows.  Logits, tokens and both
+# residual buffers bit for bit.
+@pytest.mark.parametrize("B,S,t_rows,seed", [(8, 40, 1, 61), (12, 33, 1, 62), (20, 50, 1, 63), (32, 70, 1, 64),
+                                             (4, 30, 4, 65), (2, 25, 9, 66)])
+def test_norm_hand_over_equals_the_pre_pass(engine, B, S, t_rows, seed):
+    from qdec.runtime import DecodeState
+    rows = B * t_rows
+    outs = []
+    for hand in (True, False):
+        st = DecodeState(engine.model, B, S + 40, max_t=16, keep_logits=True)
+        st.hand_over = hand
+        if hand:
+            assert st._hand_threads("o", rows) == 256
+            assert st._hand_threads("down", rows) == (None if rows < 9 else 64 * st.plans["qkv"][1])
+        st.prefill(prompts(B, S, seed).to(engine.device))
+        for _ in range(3):
+            st.run_step(t_rows=1)
+        if t_rows > 1:
+            st.run_step(t_rows=t_rows, advance=False)
+        torch.cuda.synchronize()
+        outs.append((st.logits[:rows].clone(), st.ids[:rows].clone(), st.hbuf[:, :rows].clone(), st.lens.clone()))
+        assert not torch.isnan(st.logits[:rows].float()).any()
+        del st
+    for a, b in zip(*outs):
+        assert _same(a, b)
+
+
 def _tickets(st):
     """(top ticket, arrivals summed over the 8 groups) of the layer kernel's
     barrier state: the top at byte 0, group g's arrivals at 128 + 128 g."""
