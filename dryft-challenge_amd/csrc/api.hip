@@ -207,6 +207,10 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
       p->xpre = 1;
     }
   }
+  // Register staging of 5..8 rows has a window-path instantiation only; on
+  // the pass path (a wave's k range that no ring divides, e.g. the lm_head's
+  // 8 k steps at hidden 1024) the rows are staged through LDS instead.
+  if (p->xfast && a->rows > kFastRowsMax && p->rw == 0) p->xfast = 0;
   // A pending split residual update is merged by the register-staged
   // prologue at one row, else by the normalisation pre-pass (once per row;
   // per workgroup it would re-read every partial for every row).
@@ -292,10 +296,14 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
 static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) {
   if (!a) return set_error(QDEC_EINVAL, "qdec_attn: null args");
   if (a->head_dim != 128) return set_error(QDEC_EUNSUPPORTED, "qdec_attn: head_dim %d (only 128)", a->head_dim);
-  if (a->nkv < 1 || a->nq != 4 * a->nkv)
-    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: nq %d / nkv %d (only 4 query heads per kv head)", a->nq, a->nkv);
+  if (a->nkv < 1 || a->nq < a->nkv || a->nq % a->nkv)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: nq %d / nkv %d (a whole number of query heads per kv head)", a->nq,
+                     a->nkv);
   if (a->batch < 1 || a->batch > 65535) return set_error(QDEC_EINVAL, "qdec_attn: batch %d", a->batch);
   if (a->t_rows < 1 || a->t_rows > 16) return set_error(QDEC_EINVAL, "qdec_attn: t_rows %d not in [1, 16]", a->t_rows);
+  if (a->t_rows * (a->nq / a->nkv) > (a->waves == 8 ? 32 : 64))
+    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: %d query rows per kv head (t_rows x nq / nkv; at most 64, 32 with 8 waves)",
+                     a->t_rows * (a->nq / a->nkv));
   if (a->cap < 32 || a->cap % 32) return set_error(QDEC_EINVAL, "qdec_attn: cap %d not a positive multiple of 32", a->cap);
   if (a->chunk < 32 || a->chunk % 32) return set_error(QDEC_EINVAL, "qdec_attn: chunk %d not a positive multiple of 32", a->chunk);
   if (a->waves != 4 && a->waves != 8)
@@ -749,8 +757,9 @@ int qdec_prefill_qk(const qdec_prefill_qk_args *a, qdec_stream_t stream) {
 
 int qdec_prefill_attn(const qdec_prefill_attn_args *a, qdec_stream_t stream) {
   if (!a || !a->qkv || !a->k_cache || !a->v_cache || !a->out) return set_error(QDEC_EINVAL, "qdec_prefill_attn: null pointer");
-  if (a->head_dim != 128 || a->nkv < 1 || a->nq != 4 * a->nkv)
-    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_attn: head_dim %d nq %d nkv %d (head_dim 128, 4 query heads per kv head)",
+  if (a->head_dim != 128 || a->nkv < 1 || a->nq % a->nkv ||
+      (a->nq / a->nkv != 2 && a->nq / a->nkv != 4 && a->nq / a->nkv != 8))
+    return set_error(QDEC_EUNSUPPORTED, "qdec_prefill_attn: head_dim %d nq %d nkv %d (head_dim 128; 2, 4 or 8 query heads per kv head)",
                      a->head_dim, a->nq, a->nkv);
   if (a->batch < 1 || a->t_rows < 1 || a->pos0 < 0 || a->cap < 32 || a->cap % 32 || a->pos0 + a->t_rows > a->cap)
     return set_error(QDEC_EINVAL, "qdec_prefill_attn: batch %d t_rows %d pos0 %d cap %d", a->batch, a->t_rows,

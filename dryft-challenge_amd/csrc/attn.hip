@@ -35,35 +35,41 @@ namespace {
 
 // Up to 32 query rows per kv head the body fits 256 registers without
 // spills: two 4-wave workgroups per CU, or one of 8 waves.
-template <int D, int G, int MTQ, int NW>
+template <int D, int GQ, int MTQ, int NW>
 __global__ void __launch_bounds__(64 * NW, NW == 4 && MTQ <= 2 ? 2 : 1) attn_kernel(const AttnParams p) {
   __shared__ __align__(16) unsigned char smem[AttnLds<NW>::bytes];
-  attn_block<D, G, MTQ, NW>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+  attn_block<D, GQ, MTQ, NW>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }
 
 }  // namespace
+
+template <int GQ>
+hipError_t launch_attn_g(const AttnParams &p, int mtq, dim3 grid, dim3 block, hipStream_t s) {
+  if (p.waves == 8) {
+    switch (mtq) {
+      case 1: hipLaunchKernelGGL((attn_kernel<128, GQ, 1, 8>), grid, block, 0, s, p); break;
+      case 2: hipLaunchKernelGGL((attn_kernel<128, GQ, 2, 8>), grid, block, 0, s, p); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipSuccess;
+  }
+  switch (mtq) {
+    case 1: hipLaunchKernelGGL((attn_kernel<128, GQ, 1, 4>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((attn_kernel<128, GQ, 2, 4>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((attn_kernel<128, GQ, 3, 4>), grid, block, 0, s, p); break;
+    case 4: hipLaunchKernelGGL((attn_kernel<128, GQ, 4, 4>), grid, block, 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipSuccess;
+}
 
 hipError_t launch_attn(const AttnParams &p, hipStream_t s) {
   const int R = p.t_rows * (p.nq / p.nkv);
   const int mtq = (R + 15) / 16;
   dim3 grid(p.nchunks, p.nkv, p.batch);
   dim3 block(64 * p.waves);
-  if (p.waves == 8) {
-    switch (mtq) {
-      case 1: hipLaunchKernelGGL((attn_kernel<128, 4, 1, 8>), grid, block, 0, s, p); break;
-      case 2: hipLaunchKernelGGL((attn_kernel<128, 4, 2, 8>), grid, block, 0, s, p); break;
-      default: return hipErrorInvalidValue;
-    }
-    return hipSuccess;
-  }
-  switch (mtq) {
-    case 1: hipLaunchKernelGGL((attn_kernel<128, 4, 1, 4>), grid, block, 0, s, p); break;
-    case 2: hipLaunchKernelGGL((attn_kernel<128, 4, 2, 4>), grid, block, 0, s, p); break;
-    case 3: hipLaunchKernelGGL((attn_kernel<128, 4, 3, 4>), grid, block, 0, s, p); break;
-    case 4: hipLaunchKernelGGL((attn_kernel<128, 4, 4, 4>), grid, block, 0, s, p); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipSuccess;
+  // 4 query heads per kv head as a constant; other group sizes read it from p
+  return p.nq == 4 * p.nkv ? launch_attn_g<4>(p, mtq, grid, block, s) : launch_attn_g<0>(p, mtq, grid, block, s);
 }
 
 }  // namespace qdec

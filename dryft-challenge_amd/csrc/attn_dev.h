@@ -59,10 +59,14 @@ struct AttnLds {
 
 // COH: the projection rows are read and the chunk partials written at device
 // scope, for a body that shares its launch with their producer and consumer.
-template <int D, int G, int MTQ, int NW, bool COH = false>
+// GQ: query heads per kv head, 4 (Qwen3-4B and -8B) or 0 for the group
+// size of the call (nq / nkv: 2 for Qwen3-0.6B and -1.7B, 5 for -14B, 8 for
+// -32B), with at most 16 * MTQ query rows per kv head.
+template <int D, int GQ, int MTQ, int NW, bool COH = false>
 __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, const int kvh, const int b,
                                            unsigned char *smem) {
-  static_assert(D == 128 && G == 4, "head_dim 128, 4 query heads per kv head");
+  static_assert(D == 128 && (GQ == 4 || GQ == 0), "head_dim 128; 4 query heads per kv head, or the call's count");
+  const int G = GQ > 0 ? GQ : p.nq / p.nkv;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   using LY = AttnLds<NW>;
   constexpr int DS = D / 32;              // MFMA k steps over the head dimension

@@ -352,6 +352,7 @@ hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
       default: return hipErrorInvalidValue;
     }
   }
+  if (p.xfast && p.rows > kFastRows) return hipErrorInvalidValue;  // the pass kernels stage kFastRows from registers
   switch (mt) {
     case 1: return launch_pass<1>(p, flags, grid, block, lds, s);
     case 2: return launch_pass<2>(p, flags, grid, block, lds, s);

@@ -62,6 +62,7 @@ static_assert(kGemmKpMax == kWbuf && 2 * kGemmKpMaxGlu == kWbuf, "pass register 
 constexpr int kFastRows = 4;
 constexpr int kFastRowsNorm = 8;
 constexpr int kFastVec = 2;
+static_assert(kFastRows == kFastRowsMax, "the planner's bound on register-staged rows of the pass path");
 
 // Sum one fp32 value per thread of the workgroup for up to 8 rows in a fixed
 // order (lane tree, then waves in order); thread m < nrows gets row m's total.

@@ -475,12 +475,14 @@ __global__ void __launch_bounds__(256) pnorm_kernel(const uint16_t *__restrict__
 }
 
 // ---------------------------------------------------------------- attention
-// A workgroup takes kPaRows positions of the 4 query heads of one kv head of
-// one sequence; wave w takes head 4*kvh + w, its positions as 4 M tiles of
-// 16 rows.  Blocks of 32 cache slots go from global memory straight into
-// LDS (global_load_lds_dwordx4 with per-lane gather addresses, so every
-// fragment lands in MFMA operand order), three blocks in a ring, two ahead
-// of the compute, shared by the 4 waves:
+// A workgroup takes kPaRows positions of the G query heads of one kv head of
+// one sequence; wave w takes head G*kvh + w % G and its share of the
+// positions, 2 or 4 M tiles of 16 rows (G = 2 and 4: two waves per head, 4
+// and 8 waves; G = 8: one wave per head, 8 waves).  Blocks of 32 cache slots
+// go from global memory straight into LDS (global_load_lds_dwordx4 with
+// per-lane gather addresses, so every fragment lands in MFMA operand
+// order), three blocks in a ring, two ahead of the compute, shared by the
+// waves:
 //   K fragment (s, h): lane (c, g) holds slot 8*(c >> 2) + (c & 3) + 4h,
 //     channels 32s + 8g .. +8: the slot order that makes the score registers
 //     of S^T = K . Q^T exactly the B operand of O^T += V^T . P^T (each lane
@@ -498,25 +500,29 @@ __global__ void __launch_bounds__(256) pnorm_kernel(const uint16_t *__restrict__
 constexpr int kPaKFrags = 8, kPaVFrags = 8;
 constexpr int kPaBlockVec = (kPaKFrags + kPaVFrags) * 64;  // uint4 per staged block
 constexpr int kPaRing = 3;
-constexpr int kPaWph = 2;  // waves per query head
+// Waves per query head for G query heads per kv head (so that every wave
+// takes 2 or 4 M tiles and the workgroup at most 8 waves).
+constexpr int pa_wph(int G) { return G == 8 ? 1 : 2; }
 
-template <int WPH>  // waves per query head: 1 (4 M tiles each) or 2 (2 M tiles each)
-__global__ void __launch_bounds__(256 * WPH, 1) pattn_kernel(const PattnParams p) {
+template <int G>
+__global__ void __launch_bounds__(64 * G * pa_wph(G), 1) pattn_kernel(const PattnParams p) {
   constexpr int D = 128;
+  constexpr int WPH = pa_wph(G);
   constexpr int MT = 4 / WPH;                  // M tiles of 16 positions per wave
-  constexpr int NWV = 4 * WPH;                 // waves
+  constexpr int NWV = G * WPH;                 // waves
+  static_assert(MT % 2 == 0 && (G == 2 || G == 4 || G == 8), "tiles taken in pairs; 2, 4 or 8 heads");
   constexpr int FPW = (kPaKFrags + kPaVFrags) / NWV;  // fragments each wave loads per block
   __shared__ uint4 lds[kPaRing * kPaBlockVec];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  const int head = wave & 3, half = wave >> 2;  // query head of the group, which 16*MT positions
+  const int head = wave % G, half = wave / G;  // query head of the group, which 16*MT positions
   const int T = p.t_rows;
   const int nqb = (T + kPaRows - 1) / kPaRows;
   const int cells = p.batch * p.nkv;
   const int qb = nqb - 1 - (int)(blockIdx.x / cells);  // longest rows first
   const int cell = (int)(blockIdx.x % cells);
   const int b = cell / p.nkv, kvh = cell - b * p.nkv;
-  const int hq = kvh * 4 + head;
+  const int hq = kvh * G + head;
   const int width = (p.nq + 2 * p.nkv) * D;
   const int t0 = qb * kPaRows;
   const int tw = t0 + half * 16 * MT;  // this wave's first position
@@ -748,7 +754,13 @@ hipError_t launch_pnorm(const void *x, const void *norm_w, void *out, float eps,
 
 hipError_t launch_prefill_attn(const PattnParams &p, hipStream_t s) {
   const int nqb = (p.t_rows + kPaRows - 1) / kPaRows;
-  hipLaunchKernelGGL(pattn_kernel<kPaWph>, dim3(nqb * p.batch * p.nkv), dim3(256 * kPaWph), 0, s, p);
+  const dim3 grid(nqb * p.batch * p.nkv);
+  switch (p.nq / p.nkv) {
+    case 2: hipLaunchKernelGGL(pattn_kernel<2>, grid, dim3(64 * 2 * pa_wph(2)), 0, s, p); break;
+    case 4: hipLaunchKernelGGL(pattn_kernel<4>, grid, dim3(64 * 4 * pa_wph(4)), 0, s, p); break;
+    case 8: hipLaunchKernelGGL(pattn_kernel<8>, grid, dim3(64 * 8 * pa_wph(8)), 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipSuccess;
 }
 

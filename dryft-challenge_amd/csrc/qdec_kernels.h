@@ -19,6 +19,8 @@ constexpr int kGemmRetileRows = 17;
 // whose staged path stops at 4 register rows, from 8).
 constexpr int kGemmDirectNormRows = 9;
 constexpr int kGemmDirectGluRows = 8;
+// Rows the pass path stages from registers (kFastRows of gemm_dev.h).
+constexpr int kFastRowsMax = 4;
 // 64-bit argmax keys per row (ARGMAX), each workgroup folding into one.
 constexpr int kArgSlots = 16;
 

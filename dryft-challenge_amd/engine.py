@@ -60,13 +60,13 @@ SPEC_BACKOFF = 2
 SPEC_K_MAX = 8
 
 
-def spec_k(batch):
+def spec_k(batch, group=4):
     """Drafts per sequence per verify iteration: up to SPEC_K_MAX, and few
     enough that the batch's verify rows fit one 16-row MFMA tile (the GEMMs'
     fast path), so a verify iteration costs about a plain step.  0 = no
     speculation at this batch size.  The verify pass's k + 1 rows per
     sequence also stay within what the state's attention takes."""
-    return max(0, min(SPEC_K_MAX, 16 // batch - 1, max_rows_per_seq(batch) - 1))
+    return max(0, min(SPEC_K_MAX, 16 // batch - 1, max_rows_per_seq(batch, group=group) - 1))
 
 
 def _log(message):
@@ -82,7 +82,7 @@ class _Shape:
         # The verify slack is reserved in both modes: attention chunking is a
         # function of (batch, capacity), and plain and speculative runs of one
         # shape must chunk alike to produce the same bits.
-        self.spec_k = spec_k(batch)
+        self.spec_k = spec_k(batch, engine.model.cfg.group)
         slack = 2 * (self.spec_k + 1)
         self.capacity = prompt_len + new_tokens + slack
         max_t = (self.spec_k + 1) if (speculate and self.spec_k) else 16

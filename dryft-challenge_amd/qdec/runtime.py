@@ -131,13 +131,24 @@ class ModelConfig:
         # unless the config says otherwise.
         self.tied = bool(cfg.get("tie_word_embeddings", False))
         self.n_qkv = (self.nq + 2 * self.nkv) * self.head_dim
+        # query heads per kv head (2 for Qwen3-0.6B / 1.7B, 4 for 4B / 8B, 5
+        # for 14B, 8 for 32B)
+        self.group = self.nq // self.nkv if self.nkv and self.nq % self.nkv == 0 else 0
+
+    @property
+    def prefill_kernels(self):
+        """Whether the prefill attention and head-norm kernels take this
+        shape (2, 4 or 8 query heads per kv head, at most 64 heads of q and
+        k); otherwise prompts go through the decode kernels
+        (DecodeState.prefill_steps)."""
+        return self.group in (2, 4, 8) and self.nq + self.nkv <= 64
 
     def check_supported(self):
         problems = []
         if self.head_dim != 128:
             problems.append(f"head_dim {self.head_dim} (kernels implement 128)")
-        if self.nq != 4 * self.nkv:
-            problems.append(f"{self.nq} q heads / {self.nkv} kv heads (kernels implement 4 per kv head)")
+        if not 1 <= self.group <= 16:
+            problems.append(f"{self.nq} q heads / {self.nkv} kv heads (kernels take 1..16 query heads per kv head)")
         for name, v, m in (("hidden", self.hidden, 32), ("intermediate", self.inter, 32),
                            ("vocab", self.vocab, 16)):
             if v % m:
@@ -222,11 +233,14 @@ def attn_waves(batch):
     return 8 if batch >= ATTN8_MIN_BATCH else 4
 
 
-def max_rows_per_seq(batch, requested=ATTN_MAX_T):
+def max_rows_per_seq(batch, requested=ATTN_MAX_T, group=4):
     """Rows per sequence a state of ``batch`` runs per call (verify passes,
     prefill through the decode kernels): at most ``requested``, ATTN_MAX_T,
-    GEMM_MAX_ROWS in all, and ATTN8_MAX_T when the attention runs 8 waves."""
-    cap = ATTN8_MAX_T if attn_waves(batch) == 8 else ATTN_MAX_T
+    GEMM_MAX_ROWS in all, and ATTN8_MAX_T when the attention runs 8 waves;
+    with ``group`` query heads per kv head, at most 64 query rows per kv
+    head (32 with 8 waves) -- the same bound at Qwen3-4B's 4."""
+    eight = attn_waves(batch) == 8
+    cap = min(ATTN8_MAX_T if eight else ATTN_MAX_T, (32 if eight else 64) // group)
     return max(1, min(requested, cap, GEMM_MAX_ROWS // batch))
 
 
@@ -361,7 +375,7 @@ class DecodeState:
         self.model, self.lib = model, model.lib
         self.batch = batch
         self.cap = round_up(capacity, 32)
-        self.max_t = max_rows_per_seq(batch, max_t)
+        self.max_t = max_rows_per_seq(batch, max_t, c.group)
         if batch > GEMM_MAX_ROWS:
             raise ValueError(f"batch {batch} > {GEMM_MAX_ROWS} rows per step")
         self.max_rows = batch * self.max_t
@@ -425,8 +439,9 @@ class DecodeState:
         """Plain decode of up to MERGE_IN_O_MAX_BATCH sequences: the
         attention leaves its chunk partials and the O projection merges them
         while staging its activations (no arrival pass); bit-identical to
-        the merged output."""
-        return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH
+        the merged output.  The O-side merge takes 4 query heads per kv
+        head; other shapes merge in the attention."""
+        return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH and self.model.cfg.group == 4
 
     def _hb(self, layer):
         """Residual buffer of ``layer`` (hbuf[0] throughout when down does not
@@ -631,7 +646,7 @@ class DecodeState:
         """Whether qdec_layer takes this state's plain decode steps: up to
         LAYER_MAX_BATCH sequences (its O stage always merges the attention
         partials, whatever MERGE_IN_O_MAX_BATCH says for five launches)."""
-        return self.batch <= LAYER_MAX_BATCH
+        return self.batch <= LAYER_MAX_BATCH and self.model.cfg.group == 4
 
     def layer_gemm_args(self, role, layer, x_attn=None):
         """A GEMM stage of qdec_layer: the role's arguments under the layer
@@ -695,7 +710,7 @@ class DecodeState:
             raise ValueError(f"prompt batch {B} != state batch {self.batch}")
         if S < 1 or S >= self.cap:
             raise ValueError(f"prompt length {S} must be in [1, {self.cap})")
-        if S <= max_rows_per_seq(B):
+        if S <= max_rows_per_seq(B, group=self.model.cfg.group) or not self.model.cfg.prefill_kernels:
             # A prompt one decode step holds goes through the decode kernels:
             # with few rows the prefill products have too few workgroups
             # (MI355X, time to the first token, 16 tokens: 3.08 ms against

@@ -267,8 +267,8 @@ typedef struct qdec_attn_args {
   float sm_scale;       /* 1/sqrt(head_dim) */
   int32_t batch;
   int32_t t_rows;       /* query rows per sequence (1 = plain decode) */
-  int32_t nq;
-  int32_t nkv;
+  int32_t nq;           /* a multiple of nkv (G = nq / nkv query heads per */
+  int32_t nkv;          /* kv head); t_rows * G <= 64, <= 32 with 8 waves  */
   int32_t head_dim;     /* 128 */
   int32_t cap;          /* slots per sequence, multiple of 32 */
   int32_t chunk;        /* slots per workgroup, multiple of 32 */
@@ -468,7 +468,8 @@ int qdec_prefill_qk(const qdec_prefill_qk_args *a, qdec_stream_t stream);
 /* Causal GQA attention of the rows at positions pos0 .. pos0 + t_rows - 1
  * (queries as qdec_prefill_qk leaves them) over cache slots 0 .. position,
  * written in fragment order (`tiles` M tiles) for the O projection.  A
- * workgroup takes 64 positions of the 4 query heads of one kv head; same
+ * workgroup takes 64 positions of the G = nq / nkv query heads of one kv
+ * head (G = 2, 4 or 8; QDEC_EUNSUPPORTED otherwise); same
  * arithmetic as qdec_attn (base-2 online softmax in fp32, probabilities
  * rounded to bf16 before P.V, fp32 accumulation, one rounding).
  * Replaces Engine._attend_prefill (engine/engine.py:464-478: SDPA flash

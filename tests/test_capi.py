@@ -167,7 +167,10 @@ def _attn(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(head_dim=64), -3), (dict(nq=16), -3), (dict(t_rows=17), -1), (dict(cap=100), -1),
+    (dict(head_dim=64), -3), (dict(nq=20), -3), (dict(nq=4), -3), (dict(t_rows=17), -1), (dict(cap=100), -1),
+    (dict(nq=64, t_rows=9), -3),  # 8 query heads per kv head: 72 query rows > 64
+    (dict(nq=64, t_rows=5, waves=8), -3),  # 40 > 32 with 8 waves
+    (dict(nq=40, t_rows=13), -3),  # 5 per kv head: 65 > 64
     (dict(chunk=48), -1), (dict(waves=5), -1), (dict(waves=2), -1), (dict(out=None), -1), (dict(partial=None), -1), (dict(qkv=8), -2),
     (dict(waves=8, t_rows=9), -3),
 ])
@@ -319,7 +322,8 @@ def test_prefill_validation(qlib):
     assert qlib.so.qdec_prefill_qk(ctypes.byref(capi.PrefillQkArgs(**{**q, "cap": 120})), None) == -1
     at = dict(qkv=16, k_cache=16, v_cache=16, out=16, sm_scale=0.088, batch=2, t_rows=100, pos0=0, nq=32,
               nkv=8, head_dim=128, cap=128, tiles=13)
-    assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "nq": 16})), None) == -3
+    assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "nq": 40})), None) == -3  # 5 per kv head
+    assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "nq": 20})), None) == -3
     assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "tiles": 12})), None) == -1
     assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "t_rows": 129})), None) == -1
     assert qlib.so.qdec_prefill_attn(ctypes.byref(capi.PrefillAttnArgs(**{**at, "out": 8})), None) == -2
