@@ -152,7 +152,7 @@ size_t layer_attn_lds_bytes();
 // 256 x 256 or 64 x 64; k a multiple of kPgStageK; the activation buffers
 // hold whole row tiles of the tile used: kPgRows rows, or kPgRowsSmall with
 // the 64 x 64 tile (the only one a call of fewer whole kPgRows tiles takes).
-constexpr int kPqMaxHeads = 64;  // query + key heads per row of qdec_prefill_qk
+constexpr int kPqMaxHeads = 80;  // query + key heads per row of qdec_prefill_qk (Qwen3-32B: 72)
 constexpr int kPgRows = 256;
 constexpr int kPgRowsSmall = 64;
 constexpr int kPgStageK = 64;

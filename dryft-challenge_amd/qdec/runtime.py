@@ -138,10 +138,10 @@ class ModelConfig:
     @property
     def prefill_kernels(self):
         """Whether the prefill attention and head-norm kernels take this
-        shape (2, 4 or 8 query heads per kv head, at most 64 heads of q and
+        shape (2, 4 or 8 query heads per kv head, at most 80 heads of q and
         k); otherwise prompts go through the decode kernels
         (DecodeState.prefill_steps)."""
-        return self.group in (2, 4, 8) and self.nq + self.nkv <= 64
+        return self.group in (2, 4, 8) and self.nq + self.nkv <= 80
 
     def check_supported(self):
         problems = []

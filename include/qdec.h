@@ -444,7 +444,7 @@ int qdec_prefill_gemm(const qdec_pgemm_args *a, qdec_stream_t stream);
 /* Per-head RMSNorm (q_norm / k_norm) and RoPE of every row's query and key
  * heads, with the arithmetic of qdec_attn; the rotated keys and the raw
  * values go to cache slot pos0 + t of sequence b, the rotated queries back
- * over the query columns of qkv.  head_dim 128, nq + nkv <= 64.
+ * over the query columns of qkv.  head_dim 128, nq + nkv <= 80.
  * Replaces ops.qkv_post_rows (engine/kernels/ops.py:149-205). */
 typedef struct {
   void *qkv;            /* [batch*t_rows, (nq + 2*nkv)*head_dim] bf16; queries rewritten */

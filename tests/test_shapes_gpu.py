@@ -4,8 +4,8 @@ Qwen3-4B has 4 query heads per kv head; the rest of the family has 2
 (0.6B, 1.7B), 5 (14B) or 8 (32B), all at head_dim 128.  Each case is a
 2-layer random checkpoint with that layout (norm weights jittered
 N(1, 0.05)), prompts through whichever prefill route the shape takes (the
-prefill kernels for 2 query heads per kv head, the decode kernels for 5, and
-for 8 with 72 heads of q and k), then decode steps with logits, judged
+prefill kernels for 2 and 8 query heads per kv head, the decode kernels for
+5), then decode steps with logits, judged
 teacher-forced as tests/test_engine_gpu.py judges Qwen3-4B: logits within
 2e-2 of the row's max |logit|, every token the oracle's argmax or a
 documented near-tie.  Batch 8 runs the 8-wave attention.
