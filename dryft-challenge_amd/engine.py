@@ -12,8 +12,9 @@ Public surface (the reference's engine/engine.py:215-241, 1024-1063):
   its C ABI: embedding gather; per layer the QKV projection with the input
   RMSNorm folded in, GQA attention with head norm + RoPE + KV write folded in,
   the O projection with the residual add, gate/up with the post-attention
-  norm and SwiGLU, down with the residual add; the tied lm_head with the
-  final norm and the greedy argmax.  5 launches per layer, 182 per step.
+  norm and SwiGLU, down with the residual add; the lm_head (the embedding
+  when tied) with the final norm and the greedy argmax.  5 launches per
+  layer, 182 per step for Qwen3-4B.
 * A step reads its token ids and cache lengths from device buffers and writes
   the next ids and lengths itself, so it is captured once per shape as a
   hipGraph and replayed; up to LOOKAHEAD replays are queued ahead of the

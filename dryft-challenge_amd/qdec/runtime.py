@@ -6,8 +6,8 @@
   tiled MFMA layout of include/qdec.h -- ``qkv`` ([q; k; v] rows, 6144 x 2560
   for Qwen3-4B, as engine/engine.py:273-275 concatenates them), ``o``,
   ``gate_up`` ([gate; up] rows, engine/engine.py:277), ``down``;
-* the embedding once, tiled; the tied lm_head streams the same buffer
-  (engine/engine.py:266-269);
+* the embedding once, tiled; a tied lm_head streams the same buffer
+  (engine/engine.py:266-269), an untied one (Qwen3-8B and up) its own;
 * norm weights row-major.
 
 ``DecodeState`` holds everything one (batch, capacity) shape needs: the static
@@ -153,8 +153,6 @@ class ModelConfig:
                            ("vocab", self.vocab, 16)):
             if v % m:
                 problems.append(f"{name} {v} not a multiple of {m}")
-        if not self.tied:
-            problems.append("untied lm_head (engine streams the tied embedding)")
         if problems:
             raise ValueError("unsupported Qwen3 shape: " + "; ".join(problems))
 
@@ -314,12 +312,16 @@ class DeviceModel:
             t = tensors[name]
             return t.to(device=dev, dtype=bf).contiguous()
 
-        # A tied checkpoint may still carry lm_head.weight; the engine streams
-        # the embedding for the lm_head, so the two must be the same matrix.
-        if "lm_head.weight" in tensors and not torch.equal(tensors["lm_head.weight"],
-                                                           tensors["model.embed_tokens.weight"]):
+        # A tied checkpoint may still carry lm_head.weight; the engine then
+        # streams the embedding for the lm_head, so the two must be the same
+        # matrix.  An untied one (Qwen3-8B, -14B, -32B) must carry its own.
+        if c.tied and "lm_head.weight" in tensors and not torch.equal(tensors["lm_head.weight"],
+                                                                      tensors["model.embed_tokens.weight"]):
             raise ValueError("config ties the embeddings but lm_head.weight differs from "
                              "model.embed_tokens.weight")
+        if not c.tied and "lm_head.weight" not in tensors:
+            raise ValueError("config unties the embeddings (tie_word_embeddings false) but the checkpoint "
+                             "has no lm_head.weight")
 
         def pack(dst, src):
             n, k = src.shape
@@ -351,6 +353,11 @@ class DeviceModel:
             self.norm_w = get("model.norm.weight")
             self.emb = torch.empty((V * H,), dtype=bf, device=dev)
             pack(self.emb, get("model.embed_tokens.weight"))
+            # the lm_head's weights: the embedding itself when tied
+            self.lm_w = self.emb
+            if not c.tied:
+                self.lm_w = torch.empty((V * H,), dtype=bf, device=dev)
+                pack(self.lm_w, get("lm_head.weight"))
         stream.synchronize()
         self.plans = {
             "qkv": role_plan(c.n_qkv, H, "qkv"),
@@ -362,7 +369,7 @@ class DeviceModel:
 
     def weight_bytes(self):
         """Bytes of weights one decode step streams (norm vectors included)."""
-        ts = (self.w_qkv, self.w_o, self.w_gu, self.w_down, self.emb, self.in_w, self.post_w,
+        ts = (self.w_qkv, self.w_o, self.w_gu, self.w_down, self.lm_w, self.in_w, self.post_w,
               self.q_norm, self.k_norm, self.norm_w)
         return sum(t.numel() * t.element_size() for t in ts)
 
@@ -532,7 +539,7 @@ class DecodeState:
             a.tiles_per_wg = WIDE_TILES
         elif role == "lm":
             self._residual_in(a, c.n_layers, pending)
-            a.w = m.emb.data_ptr()
+            a.w = m.lm_w.data_ptr()
             a.norm_w = m.norm_w.data_ptr()
             a.n, a.k, a.flags = c.vocab, c.hidden, capi.NORM_IN | capi.ARGMAX
             # 8 tiles per workgroup from 2 rows; past two M tiles (33+ rows,

@@ -77,7 +77,7 @@ def run(state):
         x = one_hot(k, 1.0)
         src = {"qkv": state.h, "o": state.attn_out, "gate_up": state.h, "down": state.act, "lm": state.h}[role]
         src[:1, :k].copy_(x)
-        w = {"qkv": m.w_qkv[0], "o": m.w_o[0], "gate_up": m.w_gu[0], "down": m.w_down[0], "lm": m.emb}[role]
+        w = {"qkv": m.w_qkv[0], "o": m.w_o[0], "gate_up": m.w_gu[0], "down": m.w_down[0], "lm": m.lm_w}[role]
         if role == "down" and a.parts_out:
             # split k, partials left for the next NORM_IN call: the split
             # holding the one-hot column gives the weight column, the others 0

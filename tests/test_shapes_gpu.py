@@ -8,7 +8,8 @@ prefill kernels for 2 and 8 query heads per kv head, the decode kernels for
 5), then decode steps with logits, judged
 teacher-forced as tests/test_engine_gpu.py judges Qwen3-4B: logits within
 2e-2 of the row's max |logit|, every token the oracle's argmax or a
-documented near-tie.  Batch 8 runs the 8-wave attention.
+documented near-tie.  Batch 8 runs the 8-wave attention.  The 40/8 and 64/8
+cases have their own lm_head.weight (untied, as Qwen3-14B and -32B).
 """
 
 import pytest
@@ -24,10 +25,12 @@ TOL = 2e-2
 SHAPES = {
     # Qwen3-1.7B widths: 16 query heads / 8 kv heads
     "g2": dict(hidden_size=2048, intermediate_size=6144, num_attention_heads=16, num_key_value_heads=8),
-    # Qwen3-14B's head layout (40 / 8) at a smaller width
-    "g5": dict(hidden_size=1024, intermediate_size=3072, num_attention_heads=40, num_key_value_heads=8),
-    # Qwen3-32B's head layout (64 / 8) at a smaller width
-    "g8": dict(hidden_size=1024, intermediate_size=3072, num_attention_heads=64, num_key_value_heads=8),
+    # Qwen3-14B's head layout (40 / 8) at a smaller width, untied lm_head as 14B
+    "g5": dict(hidden_size=1024, intermediate_size=3072, num_attention_heads=40, num_key_value_heads=8,
+               tie_word_embeddings=False),
+    # Qwen3-32B's head layout (64 / 8) at a smaller width, untied lm_head as 32B
+    "g8": dict(hidden_size=1024, intermediate_size=3072, num_attention_heads=64, num_key_value_heads=8,
+               tie_word_embeddings=False),
 }
 
 
@@ -67,6 +70,7 @@ def test_head_layouts_vs_oracle(model, B, S, n, seed):
     name, cfg, eng, ora, _ = model
     c = eng.model.cfg
     assert c.group == cfg["num_attention_heads"] // cfg["num_key_value_heads"]
+    assert (eng.model.lm_w is eng.model.emb) == bool(cfg["tie_word_embeddings"])
     g = torch.Generator().manual_seed(seed)
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
     toks, logits, st = run_state(eng, prompt, n)
