@@ -71,6 +71,8 @@ def run_state(engine, prompt, n):
     return torch.stack(toks, 1), torch.stack(logits, 1)
 
 
+# B = 48 and 64 run three and four M tiles per GEMM (the lm_head one tile
+# per workgroup); 64 rows is the most a step takes.
 # B = 32 and 20 run the batched step of config 4 (>= 17 rows): attention
 # over one whole-cache chunk per (sequence, kv head) with 8 waves and its
 # output in fragment order, the O / down projections reading fragment order,
@@ -78,7 +80,7 @@ def run_state(engine, prompt, n):
 # fragment order, and the 8-tile lm_head + argmax.  B = 12 runs the 8-wave
 # attention over two 512-slot chunks merged by the last arriver.
 @pytest.mark.parametrize("B,S,n,seed", [(1, 40, 10, 1), (3, 21, 8, 2), (8, 17, 5, 4), (32, 300, 4, 31),
-                                        (20, 150, 4, 32), (12, 700, 3, 33)])
+                                        (20, 150, 4, 32), (12, 700, 3, 33), (48, 60, 3, 34), (64, 40, 3, 35)])
 def test_logits_and_tokens_vs_oracle(engine, oracle, B, S, n, seed):
     if B >= 17:
         from qdec.runtime import FRAG_ROWS, DecodeState
