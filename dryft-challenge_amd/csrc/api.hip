@@ -295,7 +295,10 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
 
 static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) {
   if (!a) return set_error(QDEC_EINVAL, "qdec_attn: null args");
-  if (a->head_dim != 128) return set_error(QDEC_EUNSUPPORTED, "qdec_attn: head_dim %d (only 128)", a->head_dim);
+  if (a->head_dim != 128 && a->head_dim != 64)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: head_dim %d (128, or 64 with 4 waves)", a->head_dim);
+  if (a->head_dim == 64 && a->waves != 4)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: head_dim 64 runs 4 waves (waves %d)", a->waves);
   if (a->nkv < 1 || a->nq < a->nkv || a->nq % a->nkv)
     return set_error(QDEC_EUNSUPPORTED, "qdec_attn: nq %d / nkv %d (a whole number of query heads per kv head)", a->nq,
                      a->nkv);
@@ -335,6 +338,7 @@ fill:
   p->cap = a->cap; p->chunk = a->chunk; p->nchunks = nchunks; p->waves = a->waves;
   p->out_partials = a->out_partials;
   p->ofrag = (a->out_frag && !a->out_partials) ? (a->batch * a->t_rows + 15) / 16 : 0;
+  p->head_dim = a->head_dim;
   return QDEC_OK;
 }
 

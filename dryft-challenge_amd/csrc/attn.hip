@@ -68,6 +68,17 @@ hipError_t launch_attn(const AttnParams &p, hipStream_t s) {
   const int mtq = (R + 15) / 16;
   dim3 grid(p.nchunks, p.nkv, p.batch);
   dim3 block(64 * p.waves);
+  if (p.head_dim == 64) {  // four waves, group size from p
+    if (p.waves != 4) return hipErrorInvalidValue;
+    switch (mtq) {
+      case 1: hipLaunchKernelGGL((attn_kernel<64, 0, 1, 4>), grid, block, 0, s, p); break;
+      case 2: hipLaunchKernelGGL((attn_kernel<64, 0, 2, 4>), grid, block, 0, s, p); break;
+      case 3: hipLaunchKernelGGL((attn_kernel<64, 0, 3, 4>), grid, block, 0, s, p); break;
+      case 4: hipLaunchKernelGGL((attn_kernel<64, 0, 4, 4>), grid, block, 0, s, p); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipSuccess;
+  }
   // 4 query heads per kv head as a constant; other group sizes read it from p
   return p.nq == 4 * p.nkv ? launch_attn_g<4>(p, mtq, grid, block, s) : launch_attn_g<0>(p, mtq, grid, block, s);
 }

@@ -65,7 +65,9 @@ struct AttnLds {
 template <int D, int GQ, int MTQ, int NW, bool COH = false>
 __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, const int kvh, const int b,
                                            unsigned char *smem) {
-  static_assert(D == 128 && (GQ == 4 || GQ == 0), "head_dim 128; 4 query heads per kv head, or the call's count");
+  static_assert((D == 128 && (GQ == 4 || GQ == 0)) || (D == 64 && GQ == 0),
+                "head_dim 128 (4 query heads per kv head, or the call's count) or 64");
+  static_assert((D / 16) % NW == 0, "every wave finishes whole 16-channel tiles");
   const int G = GQ > 0 ? GQ : p.nq / p.nkv;
   static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   using LY = AttnLds<NW>;
@@ -76,6 +78,9 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   constexpr int QPW = MTQ * 16 / NW;      // query rows per wave, at most
   constexpr int KPW = kMaxT / NW;         // new rows per wave, at most
   constexpr int RS = kAttnRowStride;
+  // A head row is 2 channels per lane on lanes 0 .. D/2 - 1; with D = 64 the
+  // other lanes load lane D/2 - 1's channels, use zeros and store nothing.
+  constexpr int LH = D / 2;
 
   uint16_t *s_kn = reinterpret_cast<uint16_t *>(smem + LY::kn);
   uint16_t *s_vp = reinterpret_cast<uint16_t *>(smem + LY::vp);
@@ -89,6 +94,8 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
   const int grp = lane >> 4;
+  const int cl = 2 * min(lane, LH - 1);  // this lane's first channel of a head row
+  const bool lv = lane < LH;
   const int T = p.t_rows;
   const int R = T * G;
   const int c0 = c * p.chunk;
@@ -136,16 +143,18 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   for (int i = 0; i < QPW; ++i) {
     const int r = min(wave + NW * i, R - 1);
     const int t = r / G, hq = r % G;
-    qraw[i] = ldv4<COH>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + 2 * lane);
+    qraw[i] = ldv4<COH>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + cl);
+    if (!lv) qraw[i] = 0u;
   }
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     const uint16_t *row = qkv + (size_t)(b * T + min(wave + NW * i, T - 1)) * width;
-    kraw[i] = ldv4<COH>(row + (size_t)(nq + kvh) * D + 2 * lane);
-    vraw[i] = ldv4<COH>(row + (size_t)(nq + nkv + kvh) * D + 2 * lane);
+    kraw[i] = ldv4<COH>(row + (size_t)(nq + kvh) * D + cl);
+    vraw[i] = ldv4<COH>(row + (size_t)(nq + nkv + kvh) * D + cl);
+    if (!lv) kraw[i] = 0u;
   }
-  const uint32_t qw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + 2 * lane);
-  const uint32_t kw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + 2 * lane);
+  const uint32_t qw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + cl);
+  const uint32_t kw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + cl);
 
   const int L = p.lens[b];
   const int last = L + T - 1;
@@ -175,26 +184,29 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
     const int t = min(wave + NW * i, R - 1) / G;
-    qcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
-    qsin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
+    qcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + cl);
+    qsin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + cl);
   }
   if (overlap) {
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       const int t = min(wave + NW * i, T - 1);
-      kcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + 2 * lane);
-      ksin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + 2 * lane);
+      kcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + cl);
+      ksin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + cl);
     }
   }
 
   // Head RMSNorm and RoPE of the two channels 2*lane, 2*lane+1 of one head row.
   auto norm_rope = [&](uint32_t raw, uint32_t w, uint32_t cw, uint32_t sw) -> uint32_t {
-    return head_norm_rope2(raw, w, cw, sw, p.eps);
+    return head_norm_rope<D>(raw, w, cw, sw, p.eps);
   };
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
     const int r = wave + NW * i;
-    if (r < R) *reinterpret_cast<uint32_t *>(s_q + r * RS + 2 * lane) = norm_rope(qraw[i], qw, qcos[i], qsin[i]);
+    if (r < R) {  // uniform per wave: the norm's wave sum runs on every lane
+      const uint32_t qo = norm_rope(qraw[i], qw, qcos[i], qsin[i]);
+      if (lv) *reinterpret_cast<uint32_t *>(s_q + r * RS + cl) = qo;
+    }
   }
   if (overlap) {
     const int g0 = L >> 3;
@@ -206,14 +218,16 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
         const uint32_t vr = vraw[i];
         const int slot = L + t;
         const int gi = (slot >> 3) - g0, e = slot & 7;
-        *reinterpret_cast<uint32_t *>(s_kn + t * RS + 2 * lane) = kout;
-        s_vp[(gi * D + 2 * lane) * 8 + e] = (uint16_t)(vr & 0xffffu);
-        s_vp[(gi * D + 2 * lane + 1) * 8 + e] = (uint16_t)(vr >> 16);
-        if (slot >= c0 && slot < c1) {  // this chunk owns the slot
-          *reinterpret_cast<uint32_t *>(kc + (size_t)slot * D + 2 * lane) = kout;
-          uint16_t *vb = vc + ((size_t)(slot >> 3) * D) * 8 + e;
-          vb[(size_t)(2 * lane) * 8] = (uint16_t)(vr & 0xffffu);
-          vb[(size_t)(2 * lane + 1) * 8] = (uint16_t)(vr >> 16);
+        if (lv) {
+          *reinterpret_cast<uint32_t *>(s_kn + t * RS + cl) = kout;
+          s_vp[(gi * D + cl) * 8 + e] = (uint16_t)(vr & 0xffffu);
+          s_vp[(gi * D + cl + 1) * 8 + e] = (uint16_t)(vr >> 16);
+          if (slot >= c0 && slot < c1) {  // this chunk owns the slot
+            *reinterpret_cast<uint32_t *>(kc + (size_t)slot * D + cl) = kout;
+            uint16_t *vb = vc + ((size_t)(slot >> 3) * D) * 8 + e;
+            vb[(size_t)cl * 8] = (uint16_t)(vr & 0xffffu);
+            vb[(size_t)(cl + 1) * 8] = (uint16_t)(vr >> 16);
+          }
         }
       }
     }

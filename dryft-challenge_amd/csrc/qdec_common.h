@@ -248,27 +248,32 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
-// Per-head RMSNorm (weight w) and RoPE of one 128-channel head row spread
-// over a wavefront: this lane holds channels 2*lane and 2*lane+1 (raw, w,
-// cos cw and sin sw as packed bf16 pairs); channel i pairs with i +- 64,
-// held by lane ^ 32.  rotate_half(y) = [-y[64:], y[:64]].  Returns the two
-// rotated channels as packed bf16:
+// Per-head RMSNorm (weight w) and RoPE of one D-channel head row spread
+// over a wavefront: lane l < D/2 holds channels 2l and 2l+1 (raw, w, cos cw
+// and sin sw as packed bf16 pairs; the lanes past D/2 pass raw = 0 and their
+// result is not used); channel i pairs with i +- D/2, held by lane ^ D/4.
+// rotate_half(y) = [-y[D/2:], y[:D/2]].  Returns the two rotated channels as
+// packed bf16:
 //   y = bf16(w * bf16(x * rstd)),  out = bf16(bf16(y * cos) + bf16(rot * sin)).
-__device__ __forceinline__ uint32_t head_norm_rope2(uint32_t raw, uint32_t w, uint32_t cw, uint32_t sw,
-                                                    float eps) {
+template <int D>
+__device__ __forceinline__ uint32_t head_norm_rope(uint32_t raw, uint32_t w, uint32_t cw, uint32_t sw, float eps) {
+  static_assert(D == 128 || D == 64, "head_dim 128 or 64");
   const int lane = threadIdx.x & 63;
   const float x0 = lo16(raw), x1 = hi16(raw);
   const float ss = wave_sum(x0 * x0 + x1 * x1);
-  const float rstd = 1.0f / sqrtf(ss / 128.0f + eps);
+  const float rstd = 1.0f / sqrtf(ss / (float)D + eps);
   const float y0 = rbf(lo16(w) * rbf(x0 * rstd));
   const float y1 = rbf(hi16(w) * rbf(x1 * rstd));
-  const float p0 = shfl_xor(y0, 32), p1 = shfl_xor(y1, 32);
-  const bool first_half = lane < 32;
+  const float p0 = shfl_xor(y0, D / 4), p1 = shfl_xor(y1, D / 4);
+  const bool first_half = (lane & (D / 2 - 1)) < D / 4;
   const float r0 = first_half ? -p0 : p0;
   const float r1 = first_half ? -p1 : p1;
   const float o0 = rbf(y0 * lo16(cw)) + rbf(r0 * lo16(sw));
   const float o1 = rbf(y1 * hi16(cw)) + rbf(r1 * hi16(sw));
   return pack2(o0, o1);
+}
+__device__ __forceinline__ uint32_t head_norm_rope2(uint32_t raw, uint32_t w, uint32_t cw, uint32_t sw, float eps) {
+  return head_norm_rope<128>(raw, w, cw, sw, eps);
 }
 
 }  // namespace qdec

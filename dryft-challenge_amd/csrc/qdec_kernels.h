@@ -108,6 +108,7 @@ struct AttnParams {
   int batch, t_rows, nq, nkv, cap, chunk, nchunks, waves;
   int out_partials;
   int ofrag;  // > 0: out is written in fragment order with this many M tiles
+  int head_dim;  // 128, or 64 (four waves)
 };
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 

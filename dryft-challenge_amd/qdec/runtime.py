@@ -138,15 +138,15 @@ class ModelConfig:
     @property
     def prefill_kernels(self):
         """Whether the prefill attention and head-norm kernels take this
-        shape (2, 4 or 8 query heads per kv head, at most 80 heads of q and
+        shape (head_dim 128, 2, 4 or 8 query heads per kv head, at most 80 heads of q and
         k); otherwise prompts go through the decode kernels
         (DecodeState.prefill_steps)."""
-        return self.group in (2, 4, 8) and self.nq + self.nkv <= 80
+        return self.head_dim == 128 and self.group in (2, 4, 8) and self.nq + self.nkv <= 80
 
     def check_supported(self):
         problems = []
-        if self.head_dim != 128:
-            problems.append(f"head_dim {self.head_dim} (kernels implement 128)")
+        if self.head_dim not in (128, 64):
+            problems.append(f"head_dim {self.head_dim} (kernels implement 128 and 64)")
         if not 1 <= self.group <= 16:
             problems.append(f"{self.nq} q heads / {self.nkv} kv heads (kernels take 1..16 query heads per kv head)")
         for name, v, m in (("hidden", self.hidden, 32), ("intermediate", self.inter, 32),
@@ -389,7 +389,9 @@ class DecodeState:
         dev, bf = model.device, torch.bfloat16
         L, H, D = c.n_layers, c.hidden, c.head_dim
         self.chunk = attn_chunk(batch, c.nkv, self.cap)
-        self.attn_waves = attn_waves(batch)
+        # head_dim 64 (the tiny test configurations): four 16-channel output
+        # tiles, one per wave of a 4-wave workgroup
+        self.attn_waves = attn_waves(batch) if c.head_dim == 128 else 4
         assert self.attn_waves == 4 or self.max_t <= 8
         cache_shape = (L, batch, c.nkv, self.cap, D)
         self.k_cache = torch.zeros(cache_shape, dtype=bf, device=dev)
@@ -448,7 +450,8 @@ class DecodeState:
         while staging its activations (no arrival pass); bit-identical to
         the merged output.  The O-side merge takes 4 query heads per kv
         head; other shapes merge in the attention."""
-        return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH and self.model.cfg.group == 4
+        c = self.model.cfg
+        return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH and c.group == 4 and c.head_dim == 128
 
     def _hb(self, layer):
         """Residual buffer of ``layer`` (hbuf[0] throughout when down does not
@@ -653,7 +656,7 @@ class DecodeState:
         """Whether qdec_layer takes this state's plain decode steps: up to
         LAYER_MAX_BATCH sequences (its O stage always merges the attention
         partials, whatever MERGE_IN_O_MAX_BATCH says for five launches)."""
-        return self.batch <= LAYER_MAX_BATCH and self.model.cfg.group == 4
+        return self.batch <= LAYER_MAX_BATCH and self.model.cfg.group == 4 and self.model.cfg.head_dim == 128
 
     def layer_gemm_args(self, role, layer, x_attn=None):
         """A GEMM stage of qdec_layer: the role's arguments under the layer

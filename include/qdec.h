@@ -269,7 +269,7 @@ typedef struct qdec_attn_args {
   int32_t t_rows;       /* query rows per sequence (1 = plain decode) */
   int32_t nq;           /* a multiple of nkv (G = nq / nkv query heads per */
   int32_t nkv;          /* kv head); t_rows * G <= 64, <= 32 with 8 waves  */
-  int32_t head_dim;     /* 128 */
+  int32_t head_dim;     /* 128, or 64 with waves = 4 */
   int32_t cap;          /* slots per sequence, multiple of 32 */
   int32_t chunk;        /* slots per workgroup, multiple of 32 */
   int32_t waves;        /* wavefronts per workgroup: 4, or 8 for t_rows <= 8;

@@ -167,7 +167,7 @@ def _attn(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(head_dim=64), -3), (dict(nq=20), -3), (dict(nq=4), -3), (dict(t_rows=17), -1), (dict(cap=100), -1),
+    (dict(head_dim=96), -3), (dict(head_dim=64, waves=8), -3), (dict(nq=20), -3), (dict(nq=4), -3), (dict(t_rows=17), -1), (dict(cap=100), -1),
     (dict(nq=64, t_rows=9), -3),  # 8 query heads per kv head: 72 query rows > 64
     (dict(nq=64, t_rows=5, waves=8), -3),  # 40 > 32 with 8 waves
     (dict(nq=40, t_rows=13), -3),  # 5 per kv head: 65 > 64

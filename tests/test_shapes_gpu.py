@@ -1,11 +1,12 @@
 """Other Qwen3 head layouts end to end on the GPU against the oracle.
 
 Qwen3-4B has 4 query heads per kv head; the rest of the family has 2
-(0.6B, 1.7B), 5 (14B) or 8 (32B), all at head_dim 128.  Each case is a
+(0.6B, 1.7B), 5 (14B) or 8 (32B), all at head_dim 128; BASELINE config 1's
+tiny model has head_dim 64 with 2 per kv head.  Each case is a
 2-layer random checkpoint with that layout (norm weights jittered
 N(1, 0.05)), prompts through whichever prefill route the shape takes (the
-prefill kernels for 2 and 8 query heads per kv head, the decode kernels for
-5), then decode steps with logits, judged
+prefill kernels for 2 and 8 query heads per kv head at head_dim 128, the
+decode kernels otherwise), then decode steps with logits, judged
 teacher-forced as tests/test_engine_gpu.py judges Qwen3-4B: logits within
 2e-2 of the row's max |logit|, every token the oracle's argmax or a
 documented near-tie.  Batch 8 runs the 8-wave attention.  The 40/8 and 64/8
@@ -31,6 +32,9 @@ SHAPES = {
     # Qwen3-32B's head layout (64 / 8) at a smaller width, untied lm_head as 32B
     "g8": dict(hidden_size=1024, intermediate_size=3072, num_attention_heads=64, num_key_value_heads=8,
                tie_word_embeddings=False),
+    # BASELINE config 1's tiny model: head_dim 64, 4 / 2 heads, vocab 1024
+    "tiny": dict(hidden_size=256, intermediate_size=768, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                 vocab_size=1024, tie_word_embeddings=True),
 }
 
 
