@@ -26,6 +26,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
 H, I, V, NQ, NKV, D = 2560, 9728, 151936, 32, 8, 128
+HEADS_4B = (NQ, NKV, D)
 
 
 @pytest.fixture(scope="module")
@@ -863,14 +864,18 @@ def test_gemm_epilogues_stay_in_bounds(lib, rows):
     assert bands_intact(lcnt_whole, max(lcb, 4) // 4, fill=0) and int(lcnt.abs().sum()) == 0, "argmax counters"
 
 
-@pytest.mark.parametrize("B,T,lens,cap,chunk,waves,frag,partials", [
-    (1, 1, [640], 800, 96, 4, 0, 1), (3, 1, [700, 31, 257], 800, 128, 4, 0, 0),
-    (20, 1, [100 + 37 * i for i in range(20)], 896, 896, 8, 1, 0), (4, 4, [60, 0, 7, 100], 128, 64, 4, 0, 0)])
-def test_attention_stays_in_bounds(lib, B, T, lens, cap, chunk, waves, frag, partials):
+@pytest.mark.parametrize("B,T,lens,cap,chunk,waves,frag,partials,layout", [
+    (1, 1, [640], 800, 96, 4, 0, 1, None), (3, 1, [700, 31, 257], 800, 128, 4, 0, 0, None),
+    (20, 1, [100 + 37 * i for i in range(20)], 896, 896, 8, 1, 0, None), (4, 4, [60, 0, 7, 100], 128, 64, 4, 0, 0, None),
+    # the tiny model's 4 / 2 heads at head_dim 64, and Qwen3-14B's 40 / 8
+    (1, 1, [300], 416, 96, 4, 0, 1, (4, 2, 64)), (5, 4, [60, 0, 7, 100, 33], 128, 64, 4, 1, 0, (4, 2, 64)),
+    (3, 1, [700, 31, 257], 800, 128, 8, 0, 0, (40, 8, 128))])
+def test_attention_stays_in_bounds(lib, B, T, lens, cap, chunk, waves, frag, partials, layout):
     """Attention output (row-major or fragment order), chunk partials and
     counters written into the middle of larger buffers: the bands and every
     cache slot outside the new ones stay untouched."""
     from qdec import capi
+    NQ, NKV, D = layout or HEADS_4B
     g = torch.Generator().manual_seed(cap + B)
     W = (NQ + 2 * NKV) * D
     qkv = (torch.randn(B * T, W, generator=g) * 2).to(torch.bfloat16).to(DEV)
