@@ -1,5 +1,5 @@
-"""BASELINE config 1's tiny model through the engine on the GPU, against the
-Transformers golden fixtures in tests/golden/.
+"""BASELINE.json configs[0]'s tiny model through the engine on the GPU,
+against the Transformers golden fixtures in tests/golden/.
 
 The fixtures were written by tests/golden/make_golden.py with Transformers'
 Qwen3ForCausalLM from the seed-0 tiny checkpoint (head_dim 64, 4 query / 2 kv

@@ -1,8 +1,8 @@
 """Other Qwen3 head layouts end to end on the GPU against the oracle.
 
 Qwen3-4B has 4 query heads per kv head; the rest of the family has 2
-(0.6B, 1.7B), 5 (14B) or 8 (32B), all at head_dim 128; BASELINE config 1's
-tiny model has head_dim 64 with 2 per kv head.  Each case is a
+(0.6B, 1.7B), 5 (14B) or 8 (32B), all at head_dim 128
+configs[0]'s tiny model has head_dim 64 with 2 per kv head.  Each case is a
 2-layer random checkpoint with that layout (norm weights jittered
 N(1, 0.05)), prompts through whichever prefill route the shape takes (the
 prefill kernels for 2 and 8 query heads per kv head at head_dim 128, the
@@ -32,7 +32,7 @@ SHAPES = {
     # Qwen3-32B's head layout (64 / 8) at a smaller width, untied lm_head as 32B
     "g8": dict(hidden_size=1024, intermediate_size=3072, num_attention_heads=64, num_key_value_heads=8,
                tie_word_embeddings=False),
-    # BASELINE config 1's tiny model: head_dim 64, 4 / 2 heads, vocab 1024
+    # BASELINE.json configs[0]'s tiny model: head_dim 64, 4 / 2 heads, vocab 1024
     "tiny": dict(hidden_size=256, intermediate_size=768, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
                  vocab_size=1024, tie_word_embeddings=True),
 }
