@@ -139,6 +139,10 @@ class Engine:
         torch.cuda.empty_cache()
         start = time.perf_counter()
         sh = _Shape(self, batch, prompt_len, new_tokens, self.speculate)
+        # Known-answer checks of this shape's own plans (every row count it
+        # replays) before it serves; raises, and the shape is not kept.
+        t_rows = (1, sh.spec_k + 1) if (self.speculate and sh.spec_k) else (1,)
+        selfcheck.run_shape(sh.state, t_rows)
         if self.use_graphs:
             sh.graph = self._capture(lambda: sh.state.step(t_rows=1))
             if self.mega and not self.speculate and sh.state.layer_supported():

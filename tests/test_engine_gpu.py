@@ -445,3 +445,63 @@ def test_selfcheck_detects_a_wrong_answer(engine, monkeypatch):
     monkeypatch.setattr(st.lib, "gemm", drop_o)
     with pytest.raises(selfcheck.SelfCheckError, match="^self-check failed .*o:"):
         selfcheck.run(st)
+
+
+@pytest.mark.parametrize("what", ["qkv", "attn", "o", "gate_up", "down", "lm"])
+def test_shape_selfcheck_detects_a_dropped_launch(engine, monkeypatch, what):
+    """Every new shape runs the known-answer checks through its own plans
+    before its first token (here batch 32: the 8-wave attention over one
+    whole-cache chunk, fragment-order hand-overs, the down projection's k
+    split merged by the next NORM_IN call, two tiles per wave, the 8-tile
+    lm_head).  Dropping one of its 32-row launches (simulated on the host)
+    makes generate raise before it yields anything, and the shape is not
+    kept; with the launch back the same shape serves."""
+    from qdec import capi, selfcheck
+    c = engine.model.cfg
+    B, S = 32, 24
+    lib = engine.model.lib
+    real_gemm, real_attn = lib.gemm, lib.attn
+
+    def role(a):
+        if a.flags & capi.ARGMAX:
+            return "lm"
+        if a.flags & capi.GLU:
+            return "gate_up"
+        if a.flags & capi.RES_OUT:
+            return "o" if a.k == c.nq * c.head_dim else "down"
+        return "qkv"
+
+    def gemm(a, s):
+        if not (role(a) == what and a.rows == B):
+            real_gemm(a, s)
+
+    def attn(a, s):
+        if not (what == "attn" and a.batch * a.t_rows == B):
+            real_attn(a, s)
+
+    prompt = prompts(B, S, 41).tolist()
+    engine.shape = None  # a new shape, checked before it serves
+    monkeypatch.setattr(lib, "gemm", gemm)
+    monkeypatch.setattr(lib, "attn", attn)
+    gen = engine.generate(prompt, 3)
+    with pytest.raises(selfcheck.SelfCheckError, match="^self-check failed"):
+        next(gen)
+    assert engine.shape is None
+    monkeypatch.undo()
+    toks = list(engine.generate(prompt, 3))
+    assert len(toks) == 3 and all(len(t) == B for t in toks)
+
+
+@pytest.mark.parametrize("B,spec", [(1, False), (3, True), (8, False), (12, False), (20, False), (64, False)])
+def test_shape_selfcheck_passes(ckpt, engine, B, spec):
+    """The per-shape checks pass on every plan family: merge in O (1),
+    verify rows of a speculative state (3: t = 1 and k + 1), register-staged
+    rows and 8-wave 512-slot chunks (8, 12), two tiles per wave and the down
+    split (20), four M tiles (64)."""
+    from engine import spec_k
+    from qdec import selfcheck
+    from qdec.runtime import DecodeState
+    k = spec_k(B) if spec else 0
+    st = DecodeState(engine.model, B, 1500, max_t=k + 1 if k else 1)
+    selfcheck.run_shape(st, (1, k + 1) if k else (1,))
+    assert int(st.k_cache.abs().sum()) == 0 and int(st.v_cache.abs().sum()) == 0

@@ -1,5 +1,15 @@
 """The full Qwen3-4B shape (36 layers) on the GPU, scored against fp32 truth.
 
+Two plans, both through the engine's own decode-step code:
+
+* config 2 of BASELINE.json (below);
+* config 4's batched plan (batch 32, capacity 4384: one whole-cache
+  attention chunk per (sequence, kv head) with 8 waves, attention and SwiGLU
+  outputs in fragment order, the down projection split four ways and merged
+  by the next NORM_IN call into the other residual buffer, two output tiles
+  per wave, the 8-tile lm_head), with short prompts so the CPU references
+  stay quick.
+
 the seed-0 random-init checkpoint (the one
 bench.py measures, written once to /tmp and reused), batch 1, a 512-token
 prompt drawn as bench.py draws it, then decode steps through the engine's
@@ -101,5 +111,63 @@ def test_full_depth_config2_vs_fp32():
     assert err.max().item() <= MARGIN * err_hf.max().item()
     d = _deficit(ref, toks)
     _say(f"emitted tokens vs fp32 argmax: {int((d > 0).sum())} of {toks.numel()} below it, "
+         f"by at most {d.max().item():.4f} logits")
+    assert d.max().item() <= TIE_MARGIN
+
+
+@pytest.mark.timeout(900)
+def test_full_depth_config4_plan_vs_fp32():
+    """Config 4's plan at full depth: 32 sequences of 24 tokens in a state
+    of config 4's capacity (4096 + 256 + 2), 4 decode steps after the first
+    token, scored like config 2 above."""
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    from engine import Engine
+    from qdec.runtime import FRAG_ROWS, DecodeState
+
+    t0 = time.perf_counter()
+    cfg = qwen3_config()
+    ensure_checkpoint(CKPT, cfg, seed=0)
+    eng = Engine(CKPT)
+    B, S, n = 32, 24, 5
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
+    st = DecodeState(eng.model, B, 4096 + 256 + 2, max_t=1, keep_logits=True)
+    assert st.cap == 4384 and st.chunk == 4384 and st.attn_waves == 8 and B >= FRAG_ROWS
+    assert st.down_parts is not None and st.plans["down"][0] == 4 and st.plans["qkv"][1] == 8
+    st.prefill(prompt.to(eng.device))
+    toks, logits = [st.ids[:B].cpu()], [st.logits[:B].float().cpu()]
+    for _ in range(n - 1):
+        st.run_step(t_rows=1)
+        toks.append(st.ids[:B].cpu())
+        logits.append(st.logits[:B].float().cpu())
+    torch.cuda.synchronize()
+    toks, logits = torch.stack(toks, 1), torch.stack(logits, 1)
+    _say(f"engine B={B}: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
+    del st, eng
+    torch.cuda.empty_cache()
+
+    tensors = load_tensors(CKPT)
+    oracle = Qwen3Oracle(cfg, tensors, mode="fp32")
+    with torch.no_grad():
+        ref = oracle.teacher_forced(prompt, toks)
+    del oracle
+    _say(f"fp32 oracle replayed ({time.perf_counter() - t0:.0f}s)")
+
+    from transformers import AutoModelForCausalLM
+    hf = AutoModelForCausalLM.from_pretrained(CKPT, dtype=torch.bfloat16, attn_implementation="sdpa",
+                                              local_files_only=True).eval()
+    with torch.no_grad():
+        hf_logits = hf(input_ids=torch.cat([prompt, toks[:, :-1]], 1), logits_to_keep=n).logits.float()
+    del hf, tensors
+    _say(f"transformers bf16 replayed ({time.perf_counter() - t0:.0f}s)")
+
+    err = normalized_max_err(logits, ref)
+    err_hf = normalized_max_err(hf_logits, ref)
+    _say(f"B={B} normalised max err vs fp32: engine {err.max().item():.4f} (mean {err.mean().item():.4f}), "
+         f"transformers bf16 {err_hf.max().item():.4f} (mean {err_hf.mean().item():.4f})")
+    assert err.max().item() <= MARGIN * err_hf.max().item()
+    d = _deficit(ref, toks)
+    _say(f"B={B} emitted tokens vs fp32 argmax: {int((d > 0).sum())} of {toks.numel()} below it, "
          f"by at most {d.max().item():.4f} logits")
     assert d.max().item() <= TIE_MARGIN
