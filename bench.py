@@ -20,6 +20,9 @@ Printed JSON fields beyond the driver contract:
   cpu_baseline  the Transformers CPU greedy loop on the same checkpoint
                 (the reference's own oracle path), on a bounded sample;
   step_hbm      algorithmic bytes per step (weights + KV read/write) / step time;
+  generate      the same workload through the public generate() (host loop
+                included): time per output token from the first yielded
+                token to the last;
   prefill       prompt processing of the headline prompt (time to first
                 token: the prompt through the 36 layers on the matrix cores,
                 lm_head + argmax of the last position), tok/s and TFLOP/s;
@@ -27,9 +30,10 @@ Printed JSON fields beyond the driver contract:
                 (38 launches instead of 182): its logit check against the
                 per-operation step and both graphs timed over the same
                 positions (skip with --no-layer);
-  batched       decode tok/s of configs[2] (batch 8, 1024 prompt tokens) and
-                configs[3] (batch 32, 4096), each after a real (timed)
-                prefill of its random prompts (skip with --no-batched);
+  batched       decode tok/s and step_hbm of configs[2] (batch 8, 1024
+                prompt tokens) and configs[3] (batch 32, 4096), each after a
+                real (timed) prefill of its random prompts (skip with
+                --no-batched);
   speculation   BASELINE.json configs[4] through the same engine: batch 4,
                 1024-token prompts tiling a seeded 64-token motif with 10%
                 random substitutions, 512 new tokens, n-gram drafter (n=3,
@@ -314,11 +318,43 @@ def layer_launch_bench(eng, sh, prompt, new_tokens, steps):
             "launches_per_step": {"per_op": 5 * n + 2, "layer": n + 2}}
 
 
-def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):
+def hbm_fraction(total_bytes, elapsed, ceiling):
+    """Achieved algorithmic HBM rate of a timed run, against the nominal
+    peak and the streaming-read ceiling measured on this device."""
+    tbs = total_bytes / elapsed / 1e12
+    out = {"achieved_TBs": round(tbs, 4), "peak_TBs": HBM_PEAK_GBS / 1e3, "frac": round(tbs * 1e3 / HBM_PEAK_GBS, 4)}
+    if ceiling:
+        out["measured_read_ceiling_TBs"] = round(ceiling / 1e12, 4)
+        out["frac_of_measured_ceiling"] = round(tbs * 1e12 / ceiling, 4)
+    return out
+
+
+def generate_tpot(eng, prompt, new_tokens):
+    """Time per output token through the public ``generate`` (host loop,
+    LOOKAHEAD queueing, pinned-ring copies and events included): from the
+    first yielded token to the last, second of two calls (the first captures
+    nothing new but warms the host path)."""
+    ids = prompt.tolist()
+    for _ in range(2):
+        t_first = None
+        n = 0
+        for i, _step in enumerate(eng.generate(ids, new_tokens)):
+            if i == 0:
+                t_first = time.perf_counter()
+            n += 1
+        dt = time.perf_counter() - t_first
+    tpot = dt / (n - 1)
+    return {"tpot_ms": round(tpot * 1e3, 4), "tok_s": round(prompt.shape[0] / tpot, 2), "decode_steps": n - 1,
+            "timed": "generate(): first yielded token to the last, wall clock"}
+
+
+def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed, ceiling=None):
     """Decode throughput of a batched configuration: its prompts (uniform
     random tokens from ``seed``) are prefilled for real (timed), every
     sequence then sits at ``prompt_len`` cached tokens, and the timed replays
-    walk the workload's positions like the headline measurement."""
+    walk the workload's positions like the headline measurement.  Its
+    ``step_hbm``: algorithmic bytes of the positions walked (weights + KV
+    read and write) over the timed region."""
     import torch
     mc = eng.model.cfg
     sh = eng._shape_for(batch, prompt_len, new_tokens)
@@ -340,6 +376,8 @@ def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):
 
     run(warmup)
     done[0] = 0
+    wbytes = eng.model.weight_bytes()
+    total_bytes = sum(step_bytes(mc, wbytes, batch, prompt_len + i % span) for i in range(steps))
     st.lens.fill_(prompt_len)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -353,6 +391,8 @@ def batched_decode(eng, batch, prompt_len, new_tokens, steps, warmup, seed):
     res = {"workload": f"qwen3-4b bf16 bs{batch} prompt{prompt_len} new{new_tokens}",
            "tok_s": round(batch * steps / elapsed, 2), "ms_per_step": round(1e3 * elapsed / steps, 4),
            "steps": steps, "cache": f"prefilled from the prompts, {kv_bytes / 1e9:.1f} GB allocated",
+           "step_hbm": dict(hbm_fraction(total_bytes, elapsed, ceiling),
+                            bytes_per_step_mean=int(total_bytes / steps)),
            "prefill": pf}
     eng.shape = None
     del sh, st
@@ -515,6 +555,8 @@ def main():
     log(f"{args.steps} steps: {ms:.4f} ms/step (events {1e3 * gpu_s / args.steps:.4f}), "
         f"{tok_s:.1f} tok/s, {step_tbs:.3f} TB/s algorithmic")
 
+    gen = generate_tpot(eng, prompt, N)
+    log(f"generate(): {gen}")
     ceiling = read_ceiling(eng.lib, eng.device)
     log(f"streaming-read ceiling (2 GiB, non-temporal 16-byte loads): {ceiling / 1e12:.3f} TB/s")
     # dominant kernel: gate/up (NORM_IN + GLU), bytes = both weight halves +
@@ -540,7 +582,7 @@ def main():
         torch.cuda.empty_cache()
         for name, seed in (("c3", 2), ("c4", 3)):
             bB, bS, bN, _ = CONFIGS[name]
-            batched[f"batch{bB}"] = r = batched_decode(eng, bB, bS, bN, max(10, args.steps // 4), 3, seed)
+            batched[f"batch{bB}"] = r = batched_decode(eng, bB, bS, bN, max(10, args.steps // 4), 3, seed, ceiling)
             log(f"{name}: {r}")
 
     spec = None
@@ -576,11 +618,9 @@ def main():
         "config": {"workload": desc, "batch": B, "prompt_len": S, "new_tokens": N,
                    "decode_positions": [S, last_pos], "graph": "hipGraph per decode step",
                    "parallelism": "single GPU"},
-        "step_hbm": {"achieved_TBs": round(step_tbs, 4), "peak_TBs": HBM_PEAK_GBS / 1e3,
-                     "frac": round(step_tbs * 1e3 / HBM_PEAK_GBS, 4),
-                     "measured_read_ceiling_TBs": round(ceiling / 1e12, 4),
-                     "frac_of_measured_ceiling": round(step_tbs * 1e12 / ceiling, 4),
-                     "bytes_per_step_mean": int(total_bytes / len(positions))},
+        "step_hbm": dict(hbm_fraction(total_bytes, elapsed, ceiling),
+                         bytes_per_step_mean=int(total_bytes / len(positions))),
+        "generate": gen,
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": GATE_UP_TRAFFIC_BYTES,
                      "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, calibrated on a "

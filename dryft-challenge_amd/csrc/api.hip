@@ -51,7 +51,7 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
     pb = sizeof(float) * (size_t)a->ksplit * a->rows * a->n * ((a->flags & QDEC_GLU) ? 2 : 1);
     cb = sizeof(uint32_t) * (size_t)ntiles;
   }
-  if (a->next_norm_w) cb = std::max(cb, (size_t)8);  // hand-over arrival / departure words
+  if (a->next_norm_w) cb = std::max(cb, (size_t)12);  // hand-over arrival, departure and give-up words
   size_t off = 0;
   if (p.xd && p.xpre) {
     off = (pb + 255) & ~(size_t)255;
@@ -472,6 +472,7 @@ int plan_layer(const qdec_layer_args *a, LayerParams *L, int *workgroups, size_t
   for (int i = 0; i < 4; ++i) blocks = std::max(blocks, L->nblk[i]);
   if (blocks > w)
     return set_error(QDEC_EUNSUPPORTED, "qdec_layer: a stage has %d blocks for %d workgroups", blocks, w);
+  L->nwg = w;
   L->key = fnv1a(L, sizeof *L) | 1ull;  // never 0, the value of zeroed memory
   *workgroups = w;
   *lds = need;

@@ -1,27 +1,8 @@
-// GQA decode attention with the head RMSNorm, RoPE and KV-cache write fused
-// in, for t_rows query rows per sequence (1 = plain decode, K+1 = verify).
-//
-// Grid (chunk, kv head, sequence); a workgroup of NW = 4 or 8 wavefronts per
-// cell.
-//   1. Every wave builds the normalised, rotated queries of the G heads x
-//      t_rows rows in registers, already in the B-operand layout of
-//      v_mfma_f32_16x16x32_bf16 (query row r = G*t + g sits in MFMA column
-//      r % 16 of M tile r / 16).
-//   2. If the chunk overlaps the new slots lens[b] .. lens[b]+t_rows-1, wave 0
-//      builds the new keys/values in LDS, and the chunk owning each new slot
-//      writes it to the cache (nobody reads those cache slots in this launch).
-//   3. The chunk's 32-slot blocks are dealt to the waves round robin (block j
-//      to wave j % NW); each wave walks its blocks with the next one already
-//      in flight: S^T = K . Q^T (two 16-slot MFMA tiles whose slot order makes
-//      the score registers exactly the B operand of the next product), online
-//      softmax in base 2, then O^T += V^T . P^T with V read from the
-//      channel-major V cache.
-//   4. The waves merge in LDS in wave order; a sequence that needs one chunk
-//      is written out directly, otherwise the workgroup stores (acc, m, l) and
-//      the last chunk to arrive merges all chunks in chunk order.
-// Block-to-wave dealing and chunk boundaries are keyed to absolute slot
-// numbers, and every row's arithmetic is the same whatever t_rows is, so
-// verify rows reproduce plain decode bit for bit.
+// Launcher of the GQA decode attention (head RMSNorm, RoPE and KV-cache
+// write fused in; t_rows query rows per sequence: 1 = plain decode, K+1 =
+// verify).  The kernel body and its dataflow are attn_block in attn_dev.h;
+// this file instantiates it per (head_dim, query heads per kv head, query
+// M tiles, waves) and picks the instantiation from the call.
 //
 // Reference behaviour replaced: engine/kernels/fused.py:360-479
 // (_attn_fused_split_kernel), engine/kernels/ops.py:84-431 (_qkv_post_kernel,

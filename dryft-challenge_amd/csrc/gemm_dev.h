@@ -207,7 +207,8 @@ static_assert(kHandMaxParts == kMergeParts, "a hand-over merges what the pre-pas
 // the row is bit-identical to the pre-pass's.  Rows past `rows` are zeros.
 // The row that leaves last (hsync[1]) resets both words.  A wait past
 // kHandSpin polls (a workgroup that never arrives) writes a NaN row instead
-// of hanging.
+// of hanging, and sets hsync[2], after which every hand-over row writes NaN
+// until the caller zeroes the counters.
 //
 // Its parameters are read from the kernel's argument segment (GemmParams is
 // gemm_kernel's only argument, at offset 0) through a pointer the compiler
@@ -245,6 +246,13 @@ __device__ __forceinline__ void hand_over_row(const int nblk, const int wave_s, 
         }
         __builtin_amdgcn_s_sleep(1);
       }
+      // A give-up is sticky (hsync[2]): late arrivals of that call leave
+      // hsync[0] off for every later call, so those write NaN rows too until
+      // the caller zeroes the counters.
+      if (!ok)
+        __hip_atomic_store(p.hsync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else if (__hip_atomic_load(p.hsync + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+        ok = 0u;
       const uint32_t d = __hip_atomic_fetch_add(p.hsync + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (d == (uint32_t)NR - 1u) {
         __hip_atomic_store(p.hsync, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -115,13 +115,16 @@ hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 // ---- one decode layer per launch (layer.hip)
 // Barrier state of the layer kernel: tickets that only grow, in two levels
 // (workgroup w arrives at group w % kLayerGroups, the last of a group at the
-// top), each counter on its own 128-byte line; and an error word (1: a
-// barrier wait ran out of polls, 2: a stale plan).
+// top), each counter on its own 128-byte line; an error word (1: a
+// barrier wait ran out of polls, 2: a stale plan, 3: a launch whose
+// workgroup count differs from the one the tickets were counted with); and
+// that workgroup count, recorded by the first launch on a zeroed ctl.
 constexpr int kLayerGroups = 8;
 struct LayerCtl {
   uint64_t ticket;  // top level: one arrival per group and barrier
   uint32_t err;
-  uint32_t pad0[29];
+  uint32_t nwg;     // workgroups per launch (0 until the first launch)
+  uint32_t pad0[28];
   struct Group {
     uint64_t arrive;   // one per workgroup and barrier
     uint64_t release;  // barriers this group has been released from
@@ -138,6 +141,7 @@ struct LayerParams {
   GemmParams g[4];
   AttnParams a;
   int nblk[4];
+  int nwg;  // workgroups of the launch (in the key: a plan is for one count)
 };
 constexpr int kLayerThreads = 256;  // 4 waves: the plans of every stage
 constexpr int kLayerMaxRows = 4;    // the GEMM stages stage their rows from registers

@@ -91,6 +91,8 @@ class _Shape:
         self.graph = None
         self.spec_graph = None
         self.host = torch.empty((new_tokens, batch), dtype=torch.int64, pin_memory=True)
+        # the layer kernel's error word after each step (one launch per layer only)
+        self.host_err = torch.zeros((new_tokens,), dtype=torch.int32, pin_memory=True)
         self.events = [torch.cuda.Event() for _ in range(new_tokens)]
 
 
@@ -216,9 +218,11 @@ class Engine:
         return (time.perf_counter() - t0) * 1e3 / reps
 
     def _try_mega(self, sh, prompt_len, new_tokens):
-        """Build the one-launch-per-layer step, check it against the
-        per-operation step and race the two; keep it only if it is faster by
-        MEGA_MARGIN, or MEGA_FORCE (engine/engine.py:856-884)."""
+        """Opt-in one-launch-per-layer path for this shape: write its layer
+        plans, compare its logits with the five-launch step's (_check_mega),
+        time both graphs over the same positions, and replay the layer graph
+        from now on only when its time is under MEGA_MARGIN of the other's
+        (or MEGA_FORCE); the reference's race, engine/engine.py:856-884."""
         start = time.perf_counter()
         st = sh.state
         st.enable_layer_launch()
@@ -254,15 +258,23 @@ class Engine:
 
     def _publish(self, sh, step):
         sh.host[step].copy_(sh.state.ids[:sh.batch], non_blocking=True)
+        if sh.state.layer_launch:
+            sh.host_err[step:step + 1].copy_(sh.state.layer_ctl[2:3], non_blocking=True)
         sh.events[step].record()
 
-    def _fetch(self, sh, step, last=False):
+    def _fetch(self, sh, step):
         sh.events[step].synchronize()
-        if last and sh.state.layer_launch and sh.state.layer_error():
-            # read once, after the last step (a read per step would wait for
-            # the steps queued behind it)
-            raise capi.QdecError("generate", -1, f"layer kernel error word {sh.state.layer_error()} (a grid "
-                                 "barrier wait ran out of polls, or a stale plan)")
+        if sh.state.layer_launch and int(sh.host_err[step]):
+            # The step's stages ran unsynchronised: refuse its tokens, clear
+            # the barrier state and drop the shape (its graph holds layer
+            # launches), so the next call builds the per-operation step.
+            err = int(sh.host_err[step])
+            torch.cuda.synchronize(self.device)
+            sh.state.reset_layer_ctl()
+            sh.state.disable_layer_launch()
+            self.shape = None
+            raise capi.QdecError("generate", -1, f"layer kernel error word {err} at step {step} (a grid barrier "
+                                 "wait ran out of polls, a stale plan, or another workgroup count)")
         return self._checked(sh.host[step].tolist())
 
     def _checked(self, toks):
@@ -277,12 +289,13 @@ class Engine:
         return toks
 
     def generate(self, input_ids: list[list[int]], max_new_tokens: int):
-        """Greedy continuation of every sequence, one step at a time.
+        """A generator of greedy decode steps over the batch ``input_ids``
+        (B prompts of one common length, ids in the vocabulary).
 
-        Yields a list with one token id per sequence for each output step,
-        exactly ``max_new_tokens`` times (nothing for ``max_new_tokens <=
-        0``).  Every sequence has the same length; end-of-sequence tokens do
-        not stop generation."""
+        Each ``next()`` hands back B token ids, the pick of every sequence at
+        that position; there are ``max_new_tokens`` of them in all (none when
+        it is not positive), whatever the tokens are -- an end-of-sequence id
+        is emitted like any other."""
         steps = int(max_new_tokens)
         if steps <= 0:
             return
@@ -308,7 +321,7 @@ class Engine:
             while launched < target:
                 self._launch(sh, launched)
                 launched += 1
-            yield self._fetch(sh, step, last=step == steps - 1)
+            yield self._fetch(sh, step)
 
     # --------------------------------------------------------- speculation
     def _generate_spec(self, ids, steps):

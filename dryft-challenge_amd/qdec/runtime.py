@@ -539,8 +539,6 @@ class DecodeState:
             a.x_frag = 1 if rows >= FRAG_ROWS else 0
             if self.down_parts is not None:
                 a.parts_out = self.down_parts.data_ptr()
-        if role in ("qkv", "down") and WIDE_MIN_ROWS <= rows <= 32 and (a.n // 16) % WIDE_TILES == 0:
-            a.tiles_per_wg = WIDE_TILES
         elif role == "lm":
             self._residual_in(a, c.n_layers, pending)
             a.w = m.lm_w.data_ptr()
@@ -558,6 +556,9 @@ class DecodeState:
             a.out = self.logits.data_ptr() if self.logits is not None else None
             a.ids_out = (ids_out if ids_out is not None else self.ids).data_ptr()
             a.lens_inc = lens_inc.data_ptr() if lens_inc is not None else None
+        # two output tiles per workgroup for QKV and down at two M tiles
+        if role in ("qkv", "down") and WIDE_MIN_ROWS <= rows <= 32 and (a.n // 16) % WIDE_TILES == 0:
+            a.tiles_per_wg = WIDE_TILES
         if hasattr(self, "gemm_partial"):
             a.partial = self.gemm_partial.data_ptr()
             a.counters = self.gemm_counters.data_ptr()
@@ -702,7 +703,9 @@ class DecodeState:
 
     def layer_error(self):
         """The layer kernel's error word: 0, 1 (a barrier wait ran out of
-        polls) or 2 (a launch whose plan was written for other arguments)."""
+        polls), 2 (a launch whose plan was written for other arguments) or 3
+        (a launch whose workgroup count differs from the one this ctl's
+        tickets were counted with)."""
         return int(self.layer_ctl[2].item()) if getattr(self, "layer_ctl", None) is not None else 0
 
     def reset_layer_ctl(self):

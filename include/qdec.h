@@ -206,8 +206,10 @@ typedef struct {
    * next_threads = that call's workgroup size (qdec_gemm_prepass).  The
    * result is bit-identical to the consumer's own pre-pass.  The last
    * ceil(rows / 16) * 16 workgroups of this call to finish each take one
-   * row, after every workgroup has arrived (two words of the counters
-   * workspace; a wait longer than about 2^22 polls writes NaN rows).
+   * row, after every workgroup has arrived (three words of the counters
+   * workspace; a wait longer than about 2^22 polls writes NaN rows and sets
+   * the third word, after which every hand-over row of every later call is
+   * NaN until the caller zeroes the counters).
    * Needs next_threads a multiple of 64 and at most twice this call's
    * workgroup size, n / 8 at most 2 * next_threads (at most next_threads
    * when that exceeds this call's workgroup size), and at least
@@ -319,11 +321,14 @@ int qdec_attn_noalloc(const qdec_attn_args *a, qdec_stream_t stream);
  *   every qdec_layer call with the same arguments (a call whose arguments
  *   differ from the prepared ones runs nothing and sets the error word to 2).
  * ctl: barrier state, zeroed before the first call, then left to the
- *   library (tickets that only grow, and an error word, uint32 at ctl + 8).  A workgroup that waits longer than spin_limit polls sets the
- *   word to 1 and every later wait gives up, so a launch whose workgroups
- *   cannot all be resident ends with wrong numbers and the flag, never with
- *   a hang; zero ctl again before reusing it.  Calls sharing ctl must use one
- *   workgroup count and must not overlap in time.
+ *   library (tickets that only grow, an error word, uint32 at ctl + 8, and
+ *   the workgroup count of the first launch on it, uint32 at ctl + 12).  A
+ *   workgroup that waits longer than spin_limit polls sets the word to 1 and
+ *   every later wait gives up, so a launch whose workgroups cannot all be
+ *   resident ends with wrong numbers and the flag, never with a hang; zero
+ *   ctl again before reusing it.  Calls sharing ctl must use one workgroup
+ *   count (a launch of another count runs nothing and sets the word to 3)
+ *   and must not overlap in time.
  * Replaces the reference's one-launch layer (engine/kernels/layer.py:46-285:
  * _arrive_and_wait with SPIN_LIMIT, _layer_kernel) and its engine hook
  * (engine/engine.py:834-884; MEGA_ENABLED = False there, :81). */

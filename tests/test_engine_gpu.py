@@ -355,7 +355,9 @@ def test_layer_wait_limit_and_stale_plan(engine):
     """The bounded barrier wait, forced from the host: with a limit of one
     poll a wait runs out, the error word says 1 and every workgroup still
     finishes.  A call whose arguments differ from the prepared plan runs
-    nothing and says 2.  After a reset the same state steps correctly."""
+    nothing and says 2.  After a reset the same state steps correctly; then
+    a launch of another workgroup count on the same ctl runs nothing and
+    says 3."""
     st = _layer_state(engine, 1, 64, 61, spin_limit=1)
     snap = _snapshot(st)
     st.run_step(t_rows=1, lm_head=False, advance=False)
@@ -379,6 +381,17 @@ def test_layer_wait_limit_and_stale_plan(engine):
     torch.cuda.synchronize()
     assert st.layer_error() == 0
     assert all(_same(g, w) for g, w in zip(_snapshot(st), want))
+    # A launch with another workgroup count on a ctl whose tickets were
+    # counted with the first launch's: nothing runs and the word says 3.
+    n_first = int(st.layer_ctl[3].item())  # uint32 at ctl + 12
+    assert n_first >= 8
+    st.enable_layer_launch(workgroups=n_first - 8)
+    before = _snapshot(st)
+    st.run_step(t_rows=1, lm_head=False, advance=False)
+    torch.cuda.synchronize()
+    assert st.layer_error() == 3
+    assert all(_same(g, w) for g, w in zip(_snapshot(st), before))
+    st.reset_layer_ctl()
 
 
 def test_engine_mega_check_race_and_force(ckpt, engine, oracle):

@@ -1,7 +1,12 @@
 """qdec_attn_noalloc (library-owned scratch) against qdec_attn (caller
 workspace), through the C ABI: the same output and cache bits on two calls
-in a row, the second smaller, and a clear error for calls the scratch cannot
-hold."""
+in a row, the second smaller; a first call made under hipGraph capture (in a
+fresh process, so the library sets its scratch up inside the capture),
+replayed; and a clear error for calls the scratch cannot hold."""
+
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -94,3 +99,69 @@ def test_noalloc_attention_rejects_what_it_cannot_hold():
                       chunk=64, waves=4, out_partials=1)
     with pytest.raises(capi.QdecError, match="out_partials"):
         lib.attn_noalloc(a, None)
+
+
+_CAPTURE_SCRIPT = r"""
+import sys
+import torch
+sys.path[:0] = [{pkg!r}, {repo!r}, {tests!r}]
+from qdec import capi
+import test_zz_no_alloc as T
+
+lib = capi.lib()
+s = torch.cuda.current_stream()
+# 11 chunks merged across workgroups through the scratch's arrival counters
+t, a = T._case(4, 1, [1000, 1017, 31, 64], 1056, 96, 4, seed=77)
+ref_out, ref_k, ref_v, cnt = T._run(lib, t, a, noalloc=False)
+assert int(cnt.abs().sum()) == 0
+kc, vc = t["kc"].clone(), t["vc"].clone()
+out = torch.full((4, T.NQ * T.D), 3.0, dtype=torch.bfloat16, device=T.DEV)
+a.qkv, a.q_norm_w, a.k_norm_w = t["qkv"].data_ptr(), t["qn"].data_ptr(), t["kn"].data_ptr()
+a.cos_tab, a.sin_tab, a.lens = t["cos"].data_ptr(), t["sin"].data_ptr(), t["lens"].data_ptr()
+a.k_cache, a.v_cache, a.out = kc.data_ptr(), vc.data_ptr(), out.data_ptr()
+a.partial, a.counters = None, None
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    # the process's first noalloc call: the scratch address is taken and the
+    # counter-clearing kernel recorded into the graph
+    lib.attn_noalloc(a, torch.cuda.current_stream().cuda_stream)
+torch.cuda.synchronize()
+for rep in range(3):
+    out.fill_(3.0)
+    kc.copy_(t["kc"])
+    vc.copy_(t["vc"])
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    for name, got, want in (("out", out, ref_out), ("k", kc, ref_k), ("v", vc, ref_v)):
+        assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16)), (rep, name)
+    print(f"replay {{rep}}: bits equal to qdec_attn", flush=True)
+# eager calls after the replays, several chunks: the counters were left at zero
+for B, T_, lens, cap, chunk, waves in ((3, 1, [700, 31, 257], 800, 128, 4), (2, 2, [300, 77], 512, 64, 8)):
+    t2, a2 = T._case(B, T_, lens, cap, chunk, waves, seed=B + 5)
+    r_out, r_k, r_v, _ = T._run(lib, t2, a2, noalloc=False)
+    o2, k2, v2, _ = T._run(lib, t2, a2, noalloc=True)
+    assert torch.equal(o2.view(torch.int16), r_out.view(torch.int16)) and torch.equal(k2.view(torch.int16), r_k.view(torch.int16))
+    assert torch.equal(v2.view(torch.int16), r_v.view(torch.int16))
+    print(f"eager B={{B}} T={{T_}} after the replays: bits equal", flush=True)
+print("CAPTURE_OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The header's use case: a caller under hipGraph capture.  In a fresh
+    process the first qdec_attn_noalloc call is made inside a
+    torch.cuda.graph capture (the library takes the scratch address and
+    records its counter-clearing kernel there); the graph is replayed three
+    times with eager work between the replays, each replay bit-equal to
+    qdec_attn with a caller workspace; eager noalloc calls with several
+    chunks afterwards still match, so the counters were left at zero."""
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    here = os.path.dirname(os.path.abspath(__file__))
+    repo = os.path.dirname(here)
+    script = _CAPTURE_SCRIPT.format(pkg=os.path.join(repo, "dryft-challenge_amd"), repo=repo, tests=here)
+    print("[no-alloc] capture case in a fresh process", flush=True)
+    res = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=240)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0 and "CAPTURE_OK" in res.stdout
