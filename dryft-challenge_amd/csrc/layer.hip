@@ -89,16 +89,20 @@ __global__ void __launch_bounds__(kLayerThreads, 2)
   // The tickets count arrivals per group of gridDim.x / 8 workgroups: a ctl
   // keeps the count of its first launch, and a launch of another size runs
   // nothing (every workgroup sees the same recorded count) and says 3.
-  __shared__ uint32_t s_nwg;
+  // (The word goes through the dynamic LDS, which no stage has touched yet:
+  // a static array would add to every workgroup's LDS and halve residency.)
+  uint32_t *s_nwg = reinterpret_cast<uint32_t *>(smem);
   if (threadIdx.x == 0) {
     uint32_t want = 0u;
     __hip_atomic_compare_exchange_strong(&ctl->nwg, &want, gridDim.x, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
-    s_nwg = want == 0u ? gridDim.x : want;  // on failure `want` holds the recorded count
-    if (s_nwg != gridDim.x) __hip_atomic_store(&ctl->err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_nwg = want == 0u ? gridDim.x : want;  // on failure `want` holds the recorded count
+    if (*s_nwg != gridDim.x) __hip_atomic_store(&ctl->err, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (s_nwg != gridDim.x) return;
+  const bool same_count = *s_nwg == gridDim.x;
+  __syncthreads();  // every wave has read the word before the first stage writes LDS
+  if (!same_count) return;
   // Every stage has at most one block per workgroup (the host admits no
   // more blocks than workgroups): a loop over blocks would keep its state
   // live across the body, and the attention body would spill.

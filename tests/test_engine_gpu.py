@@ -387,7 +387,7 @@ def test_layer_wait_limit_and_stale_plan(engine):
     assert n_first >= 8
     st.enable_layer_launch(workgroups=n_first - 8)
     before = _snapshot(st)
-    st.run_step(t_rows=1, lm_head=False, advance=False)
+    st.lib.layer(st._layer_args[0], torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert st.layer_error() == 3
     assert all(_same(g, w) for g, w in zip(_snapshot(st), before))
