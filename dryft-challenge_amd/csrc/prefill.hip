@@ -475,10 +475,10 @@ __global__ void __launch_bounds__(256) pnorm_kernel(const uint16_t *__restrict__
 }
 
 // ---------------------------------------------------------------- attention
-// A workgroup takes kPaRows positions of the G query heads of one kv head of
-// one sequence; wave w takes head G*kvh + w % G and its share of the
-// positions, 2 or 4 M tiles of 16 rows (G = 2 and 4: two waves per head, 4
-// and 8 waves; G = 8: one wave per head, 8 waves).  Blocks of 32 cache slots
+// A workgroup takes kPaRows positions of G = 2 or 4 query heads of one kv
+// head of one sequence; wave w takes head w % G of them and its share of
+// the positions, 2 M tiles of 16 rows (two waves per head: 4 or 8 waves).
+// Eight query heads per kv head run as two such workgroups.  Blocks of 32 cache slots
 // go from global memory straight into LDS (global_load_lds_dwordx4 with
 // per-lane gather addresses, so every fragment lands in MFMA operand
 // order), three blocks in a ring, two ahead of the compute, shared by the
@@ -500,17 +500,22 @@ __global__ void __launch_bounds__(256) pnorm_kernel(const uint16_t *__restrict__
 constexpr int kPaKFrags = 8, kPaVFrags = 8;
 constexpr int kPaBlockVec = (kPaKFrags + kPaVFrags) * 64;  // uint4 per staged block
 constexpr int kPaRing = 3;
-// Waves per query head for G query heads per kv head (so that every wave
-// takes 2 or 4 M tiles and the workgroup at most 8 waves).
-constexpr int pa_wph(int G) { return G == 8 ? 1 : 2; }
+// Waves per query head: two, each taking 2 M tiles (a workgroup of G = 2
+// or 4 query heads has 4 or 8 waves).
+constexpr int pa_wph(int G) { return 2; }
 
-template <int G>
+// G query heads per workgroup out of GS per kv head: GS = 8 (Qwen3-32B's
+// layout) runs as two workgroups of 4 heads per (kv head, row block), each
+// reading the kv head's K/V (8 heads in one workgroup would need 64
+// accumulator rows per wave and spill).
+template <int G, int GS = G>
 __global__ void __launch_bounds__(64 * G * pa_wph(G), 1) pattn_kernel(const PattnParams p) {
   constexpr int D = 128;
   constexpr int WPH = pa_wph(G);
   constexpr int MT = 4 / WPH;                  // M tiles of 16 positions per wave
   constexpr int NWV = G * WPH;                 // waves
-  static_assert(MT % 2 == 0 && (G == 2 || G == 4 || G == 8), "tiles taken in pairs; 2, 4 or 8 heads");
+  constexpr int NSUB = GS / G;                 // workgroups per (kv head, row block)
+  static_assert(MT % 2 == 0 && (G == 2 || G == 4) && GS % G == 0, "tiles taken in pairs; 2 or 4 heads");
   constexpr int FPW = (kPaKFrags + kPaVFrags) / NWV;  // fragments each wave loads per block
   __shared__ uint4 lds[kPaRing * kPaBlockVec];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -518,11 +523,12 @@ __global__ void __launch_bounds__(64 * G * pa_wph(G), 1) pattn_kernel(const Patt
   const int head = wave % G, half = wave / G;  // query head of the group, which 16*MT positions
   const int T = p.t_rows;
   const int nqb = (T + kPaRows - 1) / kPaRows;
-  const int cells = p.batch * p.nkv;
+  const int cells = p.batch * p.nkv * NSUB;
   const int qb = nqb - 1 - (int)(blockIdx.x / cells);  // longest rows first
   const int cell = (int)(blockIdx.x % cells);
-  const int b = cell / p.nkv, kvh = cell - b * p.nkv;
-  const int hq = kvh * G + head;
+  const int bk = cell / NSUB, sub = cell - bk * NSUB;
+  const int b = bk / p.nkv, kvh = bk - b * p.nkv;
+  const int hq = kvh * GS + sub * G + head;
   const int width = (p.nq + 2 * p.nkv) * D;
   const int t0 = qb * kPaRows;
   const int tw = t0 + half * 16 * MT;  // this wave's first position
@@ -758,7 +764,7 @@ hipError_t launch_prefill_attn(const PattnParams &p, hipStream_t s) {
   switch (p.nq / p.nkv) {
     case 2: hipLaunchKernelGGL(pattn_kernel<2>, grid, dim3(64 * 2 * pa_wph(2)), 0, s, p); break;
     case 4: hipLaunchKernelGGL(pattn_kernel<4>, grid, dim3(64 * 4 * pa_wph(4)), 0, s, p); break;
-    case 8: hipLaunchKernelGGL(pattn_kernel<8>, grid, dim3(64 * 8 * pa_wph(8)), 0, s, p); break;
+    case 8: hipLaunchKernelGGL((pattn_kernel<4, 8>), dim3(2 * grid.x), dim3(64 * 4 * pa_wph(4)), 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipSuccess;
