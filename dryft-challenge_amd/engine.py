@@ -117,6 +117,23 @@ class Engine:
         self._setup(cfg, tensors, speculate, use_graphs, mega=mega)
         return self
 
+    @classmethod
+    def from_model(cls, model, device="cuda:0", use_triton=True, use_graphs=True):
+        """The reference's test hook (engine/engine.py:243-248): build around
+        an already-loaded Transformers Qwen3 model (its config and weights).
+        The engine runs its HIP kernels on ``device`` (a HIP device) or
+        nothing: ``use_triton=False``, which selects the reference's PyTorch
+        ops, and a CPU device are refused, since there is no other path."""
+        dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError(f"Engine runs on a HIP device (got {device!r}); it has no CPU path")
+        if not use_triton:
+            raise ValueError("use_triton=False selects the reference's PyTorch ops; this engine only has its HIP "
+                             "kernels (use_triton=True runs them)")
+        cfg = model.config.to_dict()
+        tensors = {k: v.detach() for k, v in model.state_dict().items()}
+        return cls.from_tensors(cfg, tensors, use_graphs=use_graphs)
+
     def _setup(self, cfg, tensors, speculate, use_graphs=True, mega=None):
         self.device = torch.device("cuda:0")
         torch.cuda.set_device(self.device)

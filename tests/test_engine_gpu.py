@@ -518,3 +518,20 @@ def test_shape_selfcheck_passes(ckpt, engine, B, spec):
     st = DecodeState(engine.model, B, 1500, max_t=k + 1 if k else 1)
     selfcheck.run_shape(st, (1, k + 1) if k else (1,))
     assert int(st.k_cache.abs().sum()) == 0 and int(st.v_cache.abs().sum()) == 0
+
+
+def test_from_model_hook(ckpt, engine):
+    """Engine.from_model (the reference's test hook, engine/engine.py:243-248)
+    on a Transformers Qwen3 model loaded from the test checkpoint emits the
+    same tokens as the engine built from the checkpoint directory; a CPU
+    device or use_triton=False is refused (no other path)."""
+    from transformers import AutoModelForCausalLM
+    from engine import Engine
+    hf = AutoModelForCausalLM.from_pretrained(ckpt[0], dtype=torch.bfloat16, local_files_only=True).eval()
+    eng2 = Engine.from_model(hf, "cuda:0")
+    prompt = prompts(2, 19, 81).tolist()
+    assert list(eng2.generate(prompt, 5)) == list(engine.generate(prompt, 5))
+    with pytest.raises(ValueError):
+        Engine.from_model(hf, "cpu", use_triton=False)
+    with pytest.raises(ValueError):
+        Engine.from_model(hf, "cuda:0", use_triton=False)
