@@ -4,10 +4,12 @@
 // Grid (chunk, kv head, sequence); a workgroup of NW = 4 or 8 wavefronts per
 // cell (the wave count, like the chunk, is part of the call: a row's
 // arithmetic depends on both, never on t_rows).
-//   1. Every wave issues the K/V loads of its first two 32-slot blocks, then
-//      the raw loads of its share of the query rows (row r = G*t + g goes to
-//      wave r % NW) and of the new key/value rows (t % NW), all before the
-//      sequence length arrives (no address depends on it); a lane holds two
+//   1. Every wave issues the K/V loads of its first 32-slot block (of its
+//      first two in chunk 0; a later chunk issues the second once the length
+//      says the chunk needs it), then the raw loads of its share of the query
+//      rows (row r = G*t + g goes to wave r % NW) and of the new key/value
+//      rows (t % NW), all before the sequence length arrives (no address
+//      depends on it); a lane holds two
 //      channels of a row, so the head RMSNorm is one wave reduction and the
 //      rotate_half partner sits in lane ^ 32.  Normalised, rotated queries
 //      go to LDS; new keys go to LDS in row layout, new values in the
@@ -128,15 +130,19 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
     for (int dt = 0; dt < DT; ++dt)
       f.vf[dt] = ld_nt(vblk + (size_t)(dt * 16 + col) * 8);
   };
-  // The first two blocks of this wave and the raw query / new key / new
-  // value rows go out before the sequence length is known: none of their
-  // addresses depends on it (blocks are issued when they lie inside the
-  // chunk and the cache; the ones past the length are never used).
+  // The first block of this wave (both, in chunk 0) and the raw query / new
+  // key / new value rows go out before the sequence length is known: none
+  // of their addresses depends on it (blocks are issued when they lie inside
+  // the chunk and the cache; the ones past the length are never used).  A
+  // later chunk's second block waits for the length: the chunk holding the
+  // newest slots is usually part-filled, and the one after it empty
+  // (MI355X, ms per step: batch 8 at 1300 tokens 2.987 -> 2.963, batch 4 at
+  // 1024 2.486 -> 2.464).
   auto block_in = [&](int j) { return 32 * j < p.chunk && c0 + 32 * (j + 1) <= p.cap; };
   Frag f0, f1;
   if (block_in(wave)) load_block(c0 + 32 * wave, f0);
   if constexpr (DB) {
-    if (block_in(wave + NW)) load_block(c0 + 32 * (wave + NW), f1);
+    if (c == 0 && block_in(wave + NW)) load_block(c0 + 32 * (wave + NW), f1);
   }
   uint32_t qraw[QPW], kraw[KPW], vraw[KPW];
 #pragma unroll
@@ -177,6 +183,9 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   if (c0 > last) return;
   const int n_active = last / p.chunk + 1;
   const int nb = (min(c1, last + 1) - c0 + 31) / 32;  // blocks in this chunk
+  if constexpr (DB) {
+    if (c > 0 && wave + NW < nb) load_block(c0 + 32 * (wave + NW), f1);
+  }
 
   // ---- 1. rotation tables of the rows' positions.
   const bool overlap = c1 > L;  // this chunk holds some of the new slots
