@@ -1,8 +1,10 @@
 """The full Qwen3-4B shape (36 layers) on the GPU, scored against fp32 truth.
 
-Two plans, both through the engine's own decode-step code:
+Three plans, all through the engine's own decode-step code:
 
 * config 2 of BASELINE.json (below);
+* config 3's batched plan (batch 8: 8-wave attention over 512-slot chunks,
+  row-major activations), with short prompts;
 * config 4's batched plan (batch 32, capacity 4384: one whole-cache
   attention chunk per (sequence, kv head) with 8 waves, attention and SwiGLU
   outputs in fragment order, the down projection split four ways and merged
@@ -58,43 +60,29 @@ def _deficit(ref, toks):
     return ref.amax(-1) - ref.gather(-1, toks[..., None]).squeeze(-1)
 
 
-@pytest.mark.timeout(900)
-def test_full_depth_config2_vs_fp32():
-    if not torch.cuda.is_available():
-        pytest.fail("GPU tests need a HIP device")
-    from engine import spec_k
-    from engine import Engine
-    from qdec.runtime import DecodeState
-
-    t0 = time.perf_counter()
-    cfg = qwen3_config()
-    assert cfg["num_hidden_layers"] == 36
-    ensure_checkpoint(CKPT, cfg, seed=0)
-    _say(f"checkpoint ready ({time.perf_counter() - t0:.0f}s)")
-    eng = Engine(CKPT)
-    B, S, N, n = 1, 512, 256, 9
-    g = torch.Generator().manual_seed(1)  # bench.py's config-2 prompt
-    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
-    st = DecodeState(eng.model, B, S + N + 2 * (spec_k(B) + 1), max_t=16, keep_logits=True)
-    assert st.cap == 800 and st.chunk == 96 and st.attn_waves == 4 and st._merge_in_o(1)
-    st.prefill(prompt.to(eng.device))
+def _run_engine(st, prompt, n):
+    """Prefill, then n - 1 plain decode steps; tokens and logits per step."""
+    B = prompt.shape[0]
+    st.prefill(prompt.to(st.ids.device))
     toks, logits = [st.ids[:B].cpu()], [st.logits[:B].float().cpu()]
     for _ in range(n - 1):
         st.run_step(t_rows=1)
         toks.append(st.ids[:B].cpu())
         logits.append(st.logits[:B].float().cpu())
     torch.cuda.synchronize()
-    toks, logits = torch.stack(toks, 1), torch.stack(logits, 1)
-    _say(f"engine: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
-    del st, eng
-    torch.cuda.empty_cache()
+    return torch.stack(toks, 1), torch.stack(logits, 1)
 
+
+def _score(cfg, prompt, toks, logits, label, t0):
+    """The engine's logits and Transformers-bf16's against the fp32 oracle,
+    teacher-forced on the engine's tokens; asserts both bounds."""
+    n = toks.shape[1]
     tensors = load_tensors(CKPT)
     oracle = Qwen3Oracle(cfg, tensors, mode="fp32")
     with torch.no_grad():
         ref = oracle.teacher_forced(prompt, toks)
     del oracle
-    _say(f"fp32 oracle replayed ({time.perf_counter() - t0:.0f}s)")
+    _say(f"{label}: fp32 oracle replayed ({time.perf_counter() - t0:.0f}s)")
 
     from transformers import AutoModelForCausalLM
     hf = AutoModelForCausalLM.from_pretrained(CKPT, dtype=torch.bfloat16, attn_implementation="sdpa",
@@ -102,17 +90,75 @@ def test_full_depth_config2_vs_fp32():
     with torch.no_grad():
         hf_logits = hf(input_ids=torch.cat([prompt, toks[:, :-1]], 1), logits_to_keep=n).logits.float()
     del hf, tensors
-    _say(f"transformers bf16 replayed ({time.perf_counter() - t0:.0f}s)")
+    _say(f"{label}: transformers bf16 replayed ({time.perf_counter() - t0:.0f}s)")
 
     err = normalized_max_err(logits, ref)
     err_hf = normalized_max_err(hf_logits, ref)
-    _say(f"normalised max err vs fp32: engine {err.max().item():.4f} (mean {err.mean().item():.4f}), "
+    _say(f"{label} normalised max err vs fp32: engine {err.max().item():.4f} (mean {err.mean().item():.4f}), "
          f"transformers bf16 {err_hf.max().item():.4f} (mean {err_hf.mean().item():.4f})")
     assert err.max().item() <= MARGIN * err_hf.max().item()
     d = _deficit(ref, toks)
-    _say(f"emitted tokens vs fp32 argmax: {int((d > 0).sum())} of {toks.numel()} below it, "
+    _say(f"{label} emitted tokens vs fp32 argmax: {int((d > 0).sum())} of {toks.numel()} below it, "
          f"by at most {d.max().item():.4f} logits")
     assert d.max().item() <= TIE_MARGIN
+
+
+def _engine():
+    from engine import Engine
+    cfg = qwen3_config()
+    assert cfg["num_hidden_layers"] == 36
+    ensure_checkpoint(CKPT, cfg, seed=0)
+    return cfg, Engine(CKPT)
+
+
+@pytest.mark.timeout(900)
+def test_full_depth_config2_vs_fp32():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    from engine import spec_k
+    from qdec.runtime import DecodeState
+
+    t0 = time.perf_counter()
+    cfg, eng = _engine()
+    _say(f"checkpoint ready ({time.perf_counter() - t0:.0f}s)")
+    B, S, N, n = 1, 512, 256, 9
+    g = torch.Generator().manual_seed(1)  # bench.py's config-2 prompt
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
+    st = DecodeState(eng.model, B, S + N + 2 * (spec_k(B) + 1), max_t=16, keep_logits=True)
+    assert st.cap == 800 and st.chunk == 96 and st.attn_waves == 4 and st._merge_in_o(1)
+    toks, logits = _run_engine(st, prompt, n)
+    _say(f"engine: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
+    del st, eng
+    torch.cuda.empty_cache()
+    _score(cfg, prompt, toks, logits, "B=1", t0)
+
+
+@pytest.mark.timeout(900)
+def test_full_depth_config3_plan_vs_fp32():
+    """Config 3's plan at full depth: 8 sequences of 24 tokens in a state of
+    config 3's capacity (1024 + 512 + the speculation slack -> 1568): 8-wave
+    attention over 512-slot chunks merged by the last chunk to finish (no
+    merge in O past 2 sequences), 8 register-staged rows for QKV and
+    row-major activations (below the fragment-order threshold), the down
+    projection unsplit; 4 decode steps after the first token."""
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a HIP device")
+    from engine import spec_k
+    from qdec.runtime import FRAG_ROWS, DecodeState
+
+    t0 = time.perf_counter()
+    cfg, eng = _engine()
+    B, S, n = 8, 24, 5
+    g = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
+    st = DecodeState(eng.model, B, 1024 + 512 + 2 * (spec_k(B) + 1), max_t=1, keep_logits=True)
+    assert st.cap == 1568 and st.chunk == 512 and st.attn_waves == 8 and not st._merge_in_o(1)
+    assert B < FRAG_ROWS and st.down_parts is None and st.plans["down"][0] == 1
+    toks, logits = _run_engine(st, prompt, n)
+    _say(f"engine B={B}: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
+    del st, eng
+    torch.cuda.empty_cache()
+    _score(cfg, prompt, toks, logits, f"B={B}", t0)
 
 
 @pytest.mark.timeout(900)
@@ -122,52 +168,18 @@ def test_full_depth_config4_plan_vs_fp32():
     token, scored like config 2 above."""
     if not torch.cuda.is_available():
         pytest.fail("GPU tests need a HIP device")
-    from engine import Engine
     from qdec.runtime import FRAG_ROWS, DecodeState
 
     t0 = time.perf_counter()
-    cfg = qwen3_config()
-    ensure_checkpoint(CKPT, cfg, seed=0)
-    eng = Engine(CKPT)
+    cfg, eng = _engine()
     B, S, n = 32, 24, 5
     g = torch.Generator().manual_seed(4)
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
     st = DecodeState(eng.model, B, 4096 + 256 + 2, max_t=1, keep_logits=True)
     assert st.cap == 4384 and st.chunk == 4384 and st.attn_waves == 8 and B >= FRAG_ROWS
     assert st.down_parts is not None and st.plans["down"][0] == 4 and st.plans["qkv"][1] == 8
-    st.prefill(prompt.to(eng.device))
-    toks, logits = [st.ids[:B].cpu()], [st.logits[:B].float().cpu()]
-    for _ in range(n - 1):
-        st.run_step(t_rows=1)
-        toks.append(st.ids[:B].cpu())
-        logits.append(st.logits[:B].float().cpu())
-    torch.cuda.synchronize()
-    toks, logits = torch.stack(toks, 1), torch.stack(logits, 1)
+    toks, logits = _run_engine(st, prompt, n)
     _say(f"engine B={B}: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
     del st, eng
     torch.cuda.empty_cache()
-
-    tensors = load_tensors(CKPT)
-    oracle = Qwen3Oracle(cfg, tensors, mode="fp32")
-    with torch.no_grad():
-        ref = oracle.teacher_forced(prompt, toks)
-    del oracle
-    _say(f"fp32 oracle replayed ({time.perf_counter() - t0:.0f}s)")
-
-    from transformers import AutoModelForCausalLM
-    hf = AutoModelForCausalLM.from_pretrained(CKPT, dtype=torch.bfloat16, attn_implementation="sdpa",
-                                              local_files_only=True).eval()
-    with torch.no_grad():
-        hf_logits = hf(input_ids=torch.cat([prompt, toks[:, :-1]], 1), logits_to_keep=n).logits.float()
-    del hf, tensors
-    _say(f"transformers bf16 replayed ({time.perf_counter() - t0:.0f}s)")
-
-    err = normalized_max_err(logits, ref)
-    err_hf = normalized_max_err(hf_logits, ref)
-    _say(f"B={B} normalised max err vs fp32: engine {err.max().item():.4f} (mean {err.mean().item():.4f}), "
-         f"transformers bf16 {err_hf.max().item():.4f} (mean {err_hf.mean().item():.4f})")
-    assert err.max().item() <= MARGIN * err_hf.max().item()
-    d = _deficit(ref, toks)
-    _say(f"B={B} emitted tokens vs fp32 argmax: {int((d > 0).sum())} of {toks.numel()} below it, "
-         f"by at most {d.max().item():.4f} logits")
-    assert d.max().item() <= TIE_MARGIN
+    _score(cfg, prompt, toks, logits, f"B={B}", t0)
