@@ -90,6 +90,9 @@ HAND_OVER = False
 # k splits of the down projection from this batch size (see role_plan).
 DOWN_SPLIT = 4
 DOWN_SPLIT_MIN_BATCH = 16
+# From this batch the O projection runs 4 waves per workgroup instead of 8
+# (see role_plan).
+O_FOUR_WAVES_MIN_BATCH = 8
 # Output tiles per workgroup of QKV and down at two M tiles (WIDE_MIN_ROWS..32
 # rows).  Paired tiles run two per wave, so each activation fragment a wave
 # loads feeds both (the sums do not change).  MI355X, 32 rows, us per launch
@@ -178,7 +181,8 @@ def role_plan(n, k, role, batch=1):
     reduction cost more than it won back on MI355X.  The roles with few
     tiles (N = hidden: O and down, 160 tiles for 256 CUs) run 8 waves per
     workgroup, which doubles the weight blocks each busy CU keeps in flight
-    (O 7.6 -> 7.0 us, down 14.2 -> 13.5 us at batch 1).  The lm_head runs 4
+    (O 7.6 -> 7.0 us, down 14.2 -> 13.5 us at batch 1); O goes back to 4
+    from O_FOUR_WAVES_MIN_BATCH.  The lm_head runs 4
     tiles per workgroup (137 us against 144 us with 8 and 146 us with 2,
     non-temporal weight loads).  Only (n, k, role) and the batch decide it,
     never the row count, so a verify pass over batch x (k + 1) rows sums
@@ -200,6 +204,15 @@ def role_plan(n, k, role, batch=1):
     if role == "qkv" and batch >= WIDE_MIN_ROWS:
         # two tiles per wave (WIDE_TILES): 192 workgroups, 8 waves each
         waves = 8
+    if role == "o" and batch >= O_FOUR_WAVES_MIN_BATCH:
+        # From 8 rows O's activations no longer fit the LDS and it takes the
+        # direct path (fragments loaded beside each weight block), where 4
+        # waves of 32 k steps beat 8 of 16.  Same-box A/B, ms per step at
+        # 1024-token prompts (8 waves / 4): batch 8 2.969 / 2.943, 10 3.091 /
+        # 3.073, 12 3.143 / 3.123, 16 3.126 / 3.096, 32 3.609 / 3.610; below
+        # 8 (LDS-staged rows) 4 waves lose: batch 7 2.993 / 3.073, 5 2.710 /
+        # 2.802, 3 2.404 / 2.449.
+        waves = 4
     while ks % waves:
         waves //= 2
     tiles = 1
@@ -409,6 +422,7 @@ class DecodeState:
         self.plans = dict(model.plans)
         self.plans["down"] = role_plan(H, c.inter, "down", batch)
         self.plans["qkv"] = role_plan(c.n_qkv, H, "qkv", batch)
+        self.plans["o"] = role_plan(H, c.nq * c.head_dim, "o", batch)
         ks, _, _ = self.plans["down"]
         self.down_parts = torch.zeros((ks, R, H), dtype=torch.float32, device=dev) if ks > 1 else None
         self.qkv = torch.zeros((R, c.n_qkv), dtype=bf, device=dev)

@@ -260,6 +260,7 @@ def test_role_plans_do_not_depend_on_rows():
     assert role_plan(2560, 9728, "down") == (1, 8, 1) and role_plan(2560, 4096, "o")[0] == 1
     assert role_plan(2560, 9728, "down", batch=16)[:2] == (4, 4)
     assert role_plan(2560, 9728, "down", batch=8) == (1, 8, 1)
+    assert role_plan(2560, 4096, "o", batch=7) == (1, 8, 1) and role_plan(2560, 4096, "o", batch=8) == (1, 4, 1)
     assert role_plan(6144, 2560, "qkv", batch=17)[:2] == (1, 8) and role_plan(6144, 2560, "qkv", batch=16)[:2] == (1, 4)
     # the 160-tile roles run 8 waves, the others 4; the lm_head 4 tiles per workgroup
     assert [role_plan(n, k, r)[1] for r, n, k in (("qkv", 6144, 2560), ("o", 2560, 4096),
