@@ -179,7 +179,10 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   // Past its register-staged rows a NORM_IN call does better on the direct
   // path: one normalisation pre-pass instead of every workgroup reading
   // whole rows for the statistics and then again for staging (gate/up at 8
-  // rows 25.2 us vs 27.6 on MI355X).
+  // rows 25.2 us vs 27.6 on MI355X; ms per step staged / direct, two
+  // same-box A/Bs in either order: batch 6 2.914 / 2.880 and 2.917 / 2.868,
+  // batch 7 2.986 / 2.917 and 2.983 / 2.907, batch 5 even (+-0.3%), and at
+  // 4 rows, still from registers, 2.476 / 2.617).
   const bool stage_norm = !(f & QDEC_NORM_IN) || a->rows < (glu ? kGemmDirectGluRows : kGemmDirectNormRows);
   if (a->x_frag) {
     // x already in fragment order: the direct path reads it as it is.

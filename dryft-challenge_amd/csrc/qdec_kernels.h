@@ -16,9 +16,9 @@ constexpr int kGemmLdsX = 64 * 1024;
 // launch costs more than the uncoalesced fragment loads.
 constexpr int kGemmRetileRows = 17;
 // NORM_IN calls of at least this many rows take the direct path (with GLU,
-// whose staged path stops at 4 register rows, from 8).
+// whose staged path stops at 4 register rows, from 6).
 constexpr int kGemmDirectNormRows = 9;
-constexpr int kGemmDirectGluRows = 8;
+constexpr int kGemmDirectGluRows = 6;
 // Rows the pass path stages from registers (kFastRows of gemm_dev.h).
 constexpr int kFastRowsMax = 4;
 // 64-bit argmax keys per row (ARGMAX), each workgroup folding into one.

@@ -75,7 +75,7 @@ LAYER_MAX_BATCH = 4
 # batch 8 (8-row plain steps) 2.96 / 2.95; batch 32 3.86 vs 4.09 row-major.
 FRAG_ROWS = 9
 # Norm hand-over: a RES_OUT call (O, or down) that feeds a NORM_IN call which
-# would normalise its rows in a pre-pass launch of its own (gate/up from 8
+# would normalise its rows in a pre-pass launch of its own (gate/up from 6
 # rows; the next QKV or the lm_head from 9) writes those rows itself, as its
 # last workgroups finish (qdec_gemm's next_norm_w), and the consumer runs as
 # a plain fragment-order call: one launch fewer, the same bits.  Off: on

@@ -104,6 +104,8 @@ def test_gemm_prepass_query(qlib):
     consumers a norm hand-over serves), and with how many threads."""
     gu = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4)
     assert qlib.gemm_prepass(_gemm(rows=4, **gu)) == (False, 256)  # rows staged from registers
+    assert qlib.gemm_prepass(_gemm(rows=5, **gu)) == (False, 256)  # staged through LDS
+    assert qlib.gemm_prepass(_gemm(rows=6, **gu)) == (True, 256)  # GLU: direct path from 6 rows
     assert qlib.gemm_prepass(_gemm(rows=8, **gu)) == (True, 256)
     assert qlib.gemm_prepass(_gemm(rows=8, flags=capi.NORM_IN, n=6144, k=2560)) == (False, 256)
     assert qlib.gemm_prepass(_gemm(rows=20, flags=capi.NORM_IN, n=6144, k=2560, waves=8, tiles_per_wg=2)) == (True, 512)
