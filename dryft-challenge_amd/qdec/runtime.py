@@ -269,9 +269,14 @@ def attn_chunk(batch, nkv, cap):
     2.241 at 192; at batch 8, 512 stays ahead of 256, 384 and 768).
 
     From ATTN8_MIN_BATCH (8-wave workgroups, one per CU) every workgroup of the
-    launch should be resident at once: 512-slot chunks (all 16 blocks in
-    flight, two per wave) while batch x kv heads x chunks fits the 256 CUs,
-    else the cache in as many equal chunks as fit, down to one.  Attention
+    launch should be resident at once: the cache in as many equal chunks as
+    the 256 CUs hold (batch x kv heads x chunks), down to one, and at most
+    one per 256 slots (rounded up).  A workgroup's K/V streams through
+    one CU, so equal chunks over every CU beat 512-slot chunks that leave
+    CUs idle or end in a short one: ms per step (512-slot chunks while they
+    fit one round / equal chunks), 1024-token prompts batch 6 2.862 / 2.771
+    (320 slots), 7 2.905 / 2.833 (416), 8 2.928 / 2.860 (416); batch 8 at
+    512 tokens 2.894 / 2.773 (224), at 128 tokens 2.705 / 2.607.  Attention
     alone, 8 kv heads, us per launch: batch 16 at 4200 cached slots 69.0 in
     one chunk, 50.5 in two (57.4 in four, 64.8 in three); batch 16 at 1300
     slots 25.4 / 23.5; batch 12 at 1300 slots 24.4 in one, 33.0 in 512-slot
@@ -282,9 +287,7 @@ def attn_chunk(batch, nkv, cap):
     cap = round_up(cap, 32)
     if batch >= ATTN8_MIN_BATCH:
         pairs = batch * nkv
-        if pairs * -(-cap // 512) <= 256:
-            return min(cap, 512)
-        n_chunks = max(1, 256 // pairs)
+        n_chunks = max(1, min(256 // pairs, -(-cap // 256)))
         return round_up(-(-cap // n_chunks), 32)
     if batch * nkv >= 128:
         return cap

@@ -272,8 +272,10 @@ def test_role_plans_do_not_depend_on_rows():
     for b, cap in ((1, 800), (4, 1568), (32, 4384)):
         c = attn_chunk(b, 8, cap)
         assert c % 32 == 0 and 64 <= c <= cap
-    # from batch 8 every workgroup resident at once (8 kv heads, 256 CUs)
-    assert attn_chunk(8, 8, 1568) == 512 and attn_chunk(32, 8, 4384) == 4384
+    # from batch 6 every workgroup resident at once (8 kv heads, 256 CUs), in
+    # equal chunks, at most one per 256 slots of the cache
+    assert attn_chunk(8, 8, 1568) == 416 and attn_chunk(32, 8, 4384) == 4384
+    assert attn_chunk(6, 8, 1568) == 320 and attn_chunk(8, 8, 800) == 224 and attn_chunk(8, 8, 256) == 256
     assert attn_chunk(16, 8, 4384) == 2208 and attn_chunk(16, 8, 1568) == 800
     assert attn_chunk(12, 8, 1568) == 800 and attn_chunk(20, 8, 4384) == 4384
     for b in range(6, 65):
@@ -281,6 +283,7 @@ def test_role_plans_do_not_depend_on_rows():
             c = attn_chunk(b, 8, cap)
             assert c % 32 == 0 and c <= round_up(cap, 32)
             assert b * 8 * -(-round_up(cap, 32) // c) <= max(256, b * 8)
+            assert -(-round_up(cap, 32) // c) <= -(-round_up(cap, 32) // 256)  # chunks: at most one per 256 slots
 
 
 def _pgemm(**kw):

@@ -3,7 +3,7 @@
 Three plans, all through the engine's own decode-step code:
 
 * config 2 of BASELINE.json (below);
-* config 3's batched plan (batch 8: 8-wave attention over 512-slot chunks,
+* config 3's batched plan (batch 8: 8-wave attention over 416-slot chunks,
   row-major activations), with short prompts;
 * config 4's batched plan (batch 32, capacity 4384: one whole-cache
   attention chunk per (sequence, kv head) with 8 waves, attention and SwiGLU
@@ -137,7 +137,7 @@ def test_full_depth_config2_vs_fp32():
 def test_full_depth_config3_plan_vs_fp32():
     """Config 3's plan at full depth: 8 sequences of 24 tokens in a state of
     config 3's capacity (1024 + 512 + the speculation slack -> 1568): 8-wave
-    attention over 512-slot chunks merged by the last chunk to finish (no
+    attention over four 416-slot chunks merged by the last chunk to finish (no
     merge in O past 2 sequences), 8 register-staged rows for QKV and
     row-major activations (below the fragment-order threshold), the down
     projection unsplit; 4 decode steps after the first token."""
@@ -152,7 +152,7 @@ def test_full_depth_config3_plan_vs_fp32():
     g = torch.Generator().manual_seed(3)
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
     st = DecodeState(eng.model, B, 1024 + 512 + 2 * (spec_k(B) + 1), max_t=1, keep_logits=True)
-    assert st.cap == 1568 and st.chunk == 512 and st.attn_waves == 8 and not st._merge_in_o(1)
+    assert st.cap == 1568 and st.chunk == 416 and st.attn_waves == 8 and not st._merge_in_o(1)
     assert B < FRAG_ROWS and st.down_parts is None and st.plans["down"][0] == 1
     toks, logits = _run_engine(st, prompt, n)
     _say(f"engine B={B}: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
