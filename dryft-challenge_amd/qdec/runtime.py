@@ -259,10 +259,10 @@ def max_rows_per_seq(batch, requested=ATTN_MAX_T, group=4):
 def attn_chunk(batch, nkv, cap):
     """Slots per attention workgroup (a multiple of 32; absolute-slot
     chunking).  Measured on MI355X with 4-wave workgroups (graph-replayed,
-    36 layers): once batch x kv heads fills half the CUs one chunk per
-    sequence is fastest (no merge); below that, smaller chunks trade the
-    cross-workgroup merge against parallelism -- 512 slots at batch 8, 256 at
-    batch 2..7 and at batch 1 with long caches, 96 at batch 1 up to 1024
+    36 layers; below ATTN8_MIN_BATCH now): once batch x kv heads fills half
+    the CUs one chunk per sequence is fastest (no merge); below that,
+    smaller chunks trade the cross-workgroup merge against parallelism --
+    256 at batch 2..5 and at batch 1 with long caches, 96 at batch 1 up to 1024
     slots (10.4 us at 128 vs 12.0 us at 256 for 640 cached slots; 21.5 vs
     17.1 us at 4000; with two attention workgroups per CU a batch-1 step at
     512..766 cached slots takes 2.187 ms at 96, 2.203 at 128, 2.250 at 64,
