@@ -226,8 +226,13 @@ def role_plan(n, k, role, batch=1):
 
 # From this batch the attention runs 8 waves per workgroup with the
 # residency chunking of attn_chunk.  Same-box A/B, ms per step at 1024-token
-# prompts, 8 waves / 4 waves: batch 8 2.964 / 3.017, batch 6 2.891 / 2.953.
-ATTN8_MIN_BATCH = 6
+# prompts, 8 waves / 4 waves: batch 8 2.964 / 3.017, batch 6 2.891 / 2.953;
+# once the 8-wave chunks were equal over all CUs also batch 5 2.685 /
+# 2.718 (2048 tokens 2.833 / 2.962), batch 4 2.460 / 2.482 (2048 tokens
+# 2.545 / 2.554, 4096 tokens 2.728 / 2.774).  Batch 3 is mixed (1024
+# tokens 2.388 / 2.414, 2048 tokens 2.506 / 2.468), and batch 2 2.281 /
+# 2.275 and batch 1 2.163 / 2.130 stay on 4.
+ATTN8_MIN_BATCH = 4
 # Rows per sequence an 8-wave attention workgroup takes (two M tiles of
 # query rows per kv head).
 ATTN8_MAX_T = 8
@@ -238,8 +243,8 @@ def attn_waves(batch):
     blocks of a 512-slot chunk (or two per wave of a whole-cache one) are in
     flight at once (MI355X, ms/step: batch 8 3.100 -> 3.076, batch 32 6.129
     -> 6.098; with 1024-token prompts batch 6 2.970 -> 2.893 and batch 7
-    3.070 -> 2.978, but batch 5 2.717 -> 2.790 and batch 4 2.58 -> 2.65), else
-    4.  A row's arithmetic depends on the count, so it is a function of the
+    3.070 -> 2.978; batch 4 and 5 once its chunks were spread over every
+    CU, see ATTN8_MIN_BATCH), else 4.  A row's arithmetic depends on the count, so it is a function of the
     batch alone: plain and speculative states of one batch agree.  8 waves
     take at most ATTN8_MAX_T rows per sequence (max_rows_per_seq)."""
     return 8 if batch >= ATTN8_MIN_BATCH else 4
@@ -677,6 +682,14 @@ class DecodeState:
         partials, whatever MERGE_IN_O_MAX_BATCH says for five launches)."""
         return self.batch <= LAYER_MAX_BATCH and self.model.cfg.group == 4 and self.model.cfg.head_dim == 128
 
+    def layer_attn_args(self, layer):
+        """The attention stage of qdec_layer: this state's arguments with
+        the layer kernel's 4 waves (its one block size), partials left for
+        the O stage."""
+        at = self._attn_args(layer, 1, partials=True)
+        at.waves = 4
+        return at
+
     def layer_gemm_args(self, role, layer, x_attn=None):
         """A GEMM stage of qdec_layer: the role's arguments under the layer
         kernel's plan (4 waves, no k split; gate/up two tiles per workgroup
@@ -701,7 +714,7 @@ class DecodeState:
             self.layer_ctl = torch.zeros((capi.LAYER_CTL_BYTES // 4,), dtype=torch.int32, device=dev)
         self._layer_args = []
         for i in range(c.n_layers):
-            at = self._attn_args(i, 1, partials=True)
+            at = self.layer_attn_args(i)
             g = [self.layer_gemm_args("qkv", i), self.layer_gemm_args("o", i, x_attn=at),
                  self.layer_gemm_args("gate_up", i), self.layer_gemm_args("down", i)]
             la = capi.LayerArgs()

@@ -243,7 +243,7 @@ def _stage_launches(st):
     e.rows, e.hidden, e.vocab = st.batch, c.hidden, c.vocab
     lib.embed(e, s)
     for i in range(c.n_layers):
-        at = st._attn_args(i, 1, partials=True)
+        at = st.layer_attn_args(i)
         lib.gemm(st.layer_gemm_args("qkv", i), s)
         lib.attn(at, s)
         lib.gemm(st.layer_gemm_args("o", i, x_attn=at), s)
