@@ -464,6 +464,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-spec", action="store_true")
     ap.add_argument("--no-batched", action="store_true")
+    ap.add_argument("--no-generate", action="store_true",
+                    help="skip timing generate() after the replays (so a kernel trace ends with the timed steps)")
     ap.add_argument("--no-layer", action="store_true",
                     help="skip timing the one-launch-per-layer step (qdec_layer) beside the per-op step")
     ap.add_argument("--pmc-role", choices=ROLES + ("all",),
@@ -555,7 +557,7 @@ def main():
     log(f"{args.steps} steps: {ms:.4f} ms/step (events {1e3 * gpu_s / args.steps:.4f}), "
         f"{tok_s:.1f} tok/s, {step_tbs:.3f} TB/s algorithmic")
 
-    gen = generate_tpot(eng, prompt, N)
+    gen = None if args.no_generate else generate_tpot(eng, prompt, N)
     log(f"generate(): {gen}")
     ceiling = read_ceiling(eng.lib, eng.device)
     log(f"streaming-read ceiling (2 GiB, non-temporal 16-byte loads): {ceiling / 1e12:.3f} TB/s")
