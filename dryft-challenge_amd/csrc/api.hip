@@ -65,6 +65,7 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
 // Derive the launch plan of a GEMM call; returns QDEC_OK or an error code.
 static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) {
   if (!a) return set_error(QDEC_EINVAL, "qdec_gemm: null args");
+  *p = GemmParams{};
   const uint32_t f = a->flags;
   if (!gemm_flags_supported(f)) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: flags 0x%x not supported", f);
   if (a->rows < 1 || a->rows > 64) return set_error(QDEC_EINVAL, "qdec_gemm: rows %d not in [1, 64]", a->rows);
@@ -138,6 +139,28 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->ofrag = a->out_frag ? (a->rows + 15) / 16 : 0;
   p->ksw = KS / a->ksplit / a->waves;
   p->up_tiles = ntiles;
+  p->resident = 0;
+  if (a->resident) {
+    // One workgroup per CU normalising the rows into LDS (gemm_resident.hip);
+    // its arithmetic is that of the plan below (pre-pass + direct path).
+    if (a->resident != 1) return set_error(QDEC_EINVAL, "qdec_gemm: resident %d not 0 or 1", a->resident);
+    if (f != (QDEC_NORM_IN | QDEC_GLU) || a->ksplit != 1 || a->waves != 4 || a->tiles_per_wg != 1 || a->x_frag ||
+        xa || a->x_parts || a->next_norm_w)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs NORM_IN | GLU, ksplit 1, 4 waves, one tile per "
+                       "workgroup and row-major x (no x_frag, x_attn, x_parts or next_norm_w)");
+    if (a->rows < kResMinRows || a->rows > kResMaxRows)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d rows, not %d", kResMinRows, kResMaxRows,
+                       a->rows);
+    if (KS > kResMaxKSteps || p->ksw % kResRing)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs k <= %d with k/128 a multiple of %d (k %d)",
+                       kResMaxKSteps * 32, kResRing, a->k);
+    p->resident = 1;
+    p->rw = kResRing;
+    p->kp = 0;
+    p->npass = 0;
+    p->lds_bytes = 0;  // static LDS
+    return QDEC_OK;
+  }
   const int kpmax = glu ? kGemmKpMaxGlu : kGemmKpMax;
   // k steps per pass: register budget, then LDS budget for rows x waves x kp x 32.
   const size_t red_bytes = (size_t)(a->waves - 1) * nacc * mt * 64 * 16;

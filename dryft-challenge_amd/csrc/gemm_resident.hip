@@ -1,0 +1,263 @@
+// Gate/up projection (NORM_IN | GLU) of a few rows with the normalised rows
+// resident in LDS: one workgroup per compute unit.
+//
+// The per-operation call above its register-staged rows normalises the rows
+// in a pre-pass launch, and each of its workgroups (one tile pair, 608 for
+// Qwen3-4B, two or three per CU) then reads the whole normalised matrix from
+// L2 as its MFMA B operands.  Here the grid is one workgroup per CU, each
+// owning a contiguous run of tile pairs (two or three), and the workgroup
+// normalises the raw rows itself, once, into LDS in fragment order; every
+// wave then reads its B operands from LDS.  The pre-pass launch and the
+// per-tile activation reads from L2 are gone.
+//
+// The arithmetic is the pre-pass + direct path's, step for step, so the
+// output is bit-identical to it (and therefore row-invariant like it):
+//  * the row statistic is the pre-pass's (rownorm_kernel at 256 threads):
+//    virtual thread t sums the squares of vectors t and t + 256 of the row,
+//    the 64 lanes of each virtual wave are added by wave_sum, and the four
+//    virtual waves in order; here the workgroup's last four waves compute
+//    virtual wave w % 4 of every row;
+//  * x' = bf16(norm_w * bf16(x * rstd)) per element (norm8);
+//  * wave q of a pair streams k steps [q ksw, (q + 1) ksw) of the pair's gate
+//    and up tiles through an RW-slot register ring, the MFMA chain in k
+//    order; the pair's four waves are added in wave order; then the SwiGLU
+//    epilogue of the direct path.
+// A pair's sums do not depend on which workgroup computes it, so the grid
+// (the device's CU count) does not change a bit.
+//
+// Measured on MI355X (Qwen3-4B gate/up, 8 rows): 21.0 us per launch against
+// 24.0 for the pre-pass and the direct call, and batch-8 decode 2.912 ->
+// 2.797 ms per step (config 3, same box).
+//
+// Reference behaviour replaced: the NORM_IN + GLU path of
+// engine/kernels/fused.py:33-172 (_gemv_kernel with the RMSNorm prologue and
+// the SiLU-gated epilogue).
+#include <algorithm>
+
+#include "gemm_dev.h"
+
+namespace qdec {
+namespace {
+
+constexpr int kResVThreads = 256;  // the pre-pass workgroup whose statistic order is followed
+
+// Position of fragment slot `slot` (B operand lane: row slot % 16, k group
+// slot / 16) within the LDS KiB of k step s.  A bijection of the 64 slots
+// that XORs the row bits with the k group and s % 4: the 16 lanes of every
+// group the LDS serves together then touch 16 different 16-byte bank groups,
+// both when a lane of the MFMA reads its slot and when the normalisation
+// writes a row's 16 consecutive vectors (in plain fragment order those all
+// sit in one bank group: measured on MI355X, the writes took about 8 us per
+// launch).
+__device__ __forceinline__ int res_pos(int slot, int s) { return slot ^ (((slot >> 4) & 3) | ((s & 3) << 2)); }
+
+// Polls of an LDS flag before a wave gives up waiting (a bound that a
+// correct launch never reaches: the flags are set by waves of the same
+// workgroup that wait on nothing but their own loads).
+constexpr uint32_t kResSpin = 1u << 22;
+
+__device__ __forceinline__ void res_wait(const uint32_t *flag, uint32_t target) {
+  for (uint32_t i = 0; i < kResSpin; ++i) {
+    if (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// One arrival of this wave at an LDS flag, after its own LDS writes are done
+// (s_waitcnt lgkmcnt(0)).
+__device__ __forceinline__ void res_signal(uint32_t *flag) {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+template <int RW>
+__global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident_kernel(const GemmParams p) {
+  __shared__ __align__(16) uint4 s_x[kResMaxKSteps * 64];                  // [k step][slot]
+  __shared__ __align__(16) float4 s_red[kResMaxPairs * 3 * 2 * 64];       // [pair][wave 1..3][gate, up][lane]
+  __shared__ float s_part[kResMaxRows * 4];                               // [row][virtual wave]
+  // Arrivals of the four normalising waves: [0] row loads issued, [1]
+  // statistic partials written, [2] rows normalised into s_x.
+  __shared__ uint32_t s_sync[3];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = p.res_waves;  // blockDim.x / 64, from the kernel arguments (a scalar load)
+  const int rows = p.rows, k = p.k, KS = p.KS, ksw = p.ksw;
+  const int col = lane & 15, grp = lane >> 4;
+  const unsigned P = (unsigned)p.n >> 4;  // tile pairs
+  const unsigned pair0 = blockIdx.x * P / gridDim.x;
+  const int npairs = (int)((blockIdx.x + 1) * P / gridDim.x - pair0);
+  const int j = wave >> 2, q = wave & 3;  // pair within the workgroup, k quarter
+  const bool active = j < npairs;
+  const int tile = (int)pair0 + j;
+  if (tid == 0) s_sync[0] = s_sync[1] = s_sync[2] = 0u;
+  __syncthreads();
+
+  const uint4 *W = reinterpret_cast<const uint4 *>(p.w);
+  const size_t up_off = (size_t)p.up_tiles * KS * 64;
+  const int ksw_w = active ? ksw : 0;
+  const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + lane;
+  uint4 wg[RW], wu[RW];
+  // The first RW k steps of this wave's range.
+  auto issue_ring = [&]() {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      wg[r] = ldw(wq + r * 64);
+      wu[r] = ldw(wq + r * 64 + up_off);
+    }
+  };
+
+  // Two roles, so that the weight stream starts at once and the
+  // normalisation still runs at full speed (measured on MI355X: a wave that
+  // has issued its ring stalls in the issue of those loads for several us,
+  // and every instruction behind them waits with it).
+  //  * the last four waves (pair nw/4 - 1, or no pair at all in a workgroup
+  //    with fewer pairs) load the rows, compute the statistic and write the
+  //    normalised rows to LDS, and only then issue their own ring;
+  //  * every other wave issues its ring as soon as the row loads have gone
+  //    out ahead of it, and waits for the rows.
+  if (wave >= nw - 4) {
+    // Virtual wave vw = wave % 4 of every row: lane l holds vectors
+    // vw * 64 + l and vw * 64 + l + 256 of the row.  Loads are unconditional
+    // (clamped to a valid address, the value discarded).
+    const int vw = wave & 3;
+    const int v0 = vw * 64 + lane, v1 = v0 + kResVThreads;
+    const bool ok0 = v0 < (k >> 3), ok1 = v1 < (k >> 3);
+    const int c0 = ok0 ? v0 : 0, c1 = ok1 ? v1 : 0;
+    const uint16_t *X = reinterpret_cast<const uint16_t *>(p.x);
+    const uint16_t *NW = reinterpret_cast<const uint16_t *>(p.norm_w);
+    uint4 xa[kResMaxRows], xb[kResMaxRows];
+#pragma unroll
+    for (int m = 0; m < kResMaxRows; ++m) {
+      const uint16_t *xr = X + (size_t)(m < rows ? m : 0) * k;
+      xa[m] = *reinterpret_cast<const uint4 *>(xr + 8 * c0);
+      xb[m] = *reinterpret_cast<const uint4 *>(xr + 8 * c1);
+    }
+    const uint4 nw0 = *reinterpret_cast<const uint4 *>(NW + 8 * c0);
+    const uint4 nw1 = *reinterpret_cast<const uint4 *>(NW + 8 * c1);
+    res_signal(&s_sync[0]);
+
+    // Statistic partial of every row for this virtual wave.
+#pragma unroll
+    for (int m = 0; m < kResMaxRows; ++m) {
+      float ss = 0.f;
+      if (ok0) {
+        float f[8];
+        unpack8(xa[m], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+      }
+      if (ok1) {  // uniform per wave: only virtual wave 0 has a second vector
+        float f[8];
+        unpack8(xb[m], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+      }
+      const float s = wave_sum(ss);
+      if (lane == 0 && m < rows) s_part[m * 4 + vw] = s;
+    }
+    res_signal(&s_sync[1]);
+    res_wait(&s_sync[1], 4u);
+
+    // Normalise this virtual wave's vectors of every row into LDS, fragment
+    // order with the slots of each k step's KiB permuted: vector v of row m
+    // is k step s = v / 4, slot m + 16 (v % 4), at position res_pos(slot, s).
+#pragma unroll
+    for (int m = 0; m < kResMaxRows; ++m) {
+      if (m >= rows) continue;
+      float t = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) t += s_part[m * 4 + w2];
+      const float rs = 1.0f / sqrtf(t / (float)k + p.eps);
+      if (ok0) s_x[(v0 >> 2) * 64 + res_pos(m + 16 * (v0 & 3), v0 >> 2)] = norm8(xa[m], nw0, rs);
+      if (ok1) s_x[(v1 >> 2) * 64 + res_pos(m + 16 * (v1 & 3), v1 >> 2)] = norm8(xb[m], nw1, rs);
+    }
+    res_signal(&s_sync[2]);
+    if (active) issue_ring();
+  } else {
+    res_wait(&s_sync[0], 4u);
+    if (active) issue_ring();
+  }
+  res_wait(&s_sync[2], 4u);
+
+  // ---- the ring: slot r holds k step r (mod RW) of the wave's range.
+  f32x4_t ag = f32x4_t{0.f, 0.f, 0.f, 0.f}, au = ag;
+  const bool xrow_ok = col < rows;  // lanes past the last row multiply zeros
+  for (int i0 = 0; i0 < ksw_w; i0 += RW) {
+    const bool refill = i0 + RW < ksw_w;
+    const uint4 *qn = wq + (size_t)(i0 + RW) * 64;
+    uint4 bq[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int s = q * ksw + i0 + r;  // k step
+      bq[r] = xrow_ok ? s_x[s * 64 + res_pos(lane, s)] : zero4();
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      ag = mfma16x16x32(wg[r], bq[r], ag);
+      au = mfma16x16x32(wu[r], bq[r], au);
+      if (refill) {
+        wg[r] = ldw(qn + r * 64);
+        wu[r] = ldw(qn + r * 64 + up_off);
+      }
+    }
+  }
+  if (active && q > 0) {
+    s_red[((j * 3 + q - 1) * 2 + 0) * 64 + lane] = make_float4(ag[0], ag[1], ag[2], ag[3]);
+    s_red[((j * 3 + q - 1) * 2 + 1) * 64 + lane] = make_float4(au[0], au[1], au[2], au[3]);
+  }
+  __syncthreads();
+  if (!active || q != 0) return;
+
+  // ---- the pair's four waves in wave order, then SwiGLU (the direct path's
+  // epilogue).
+#pragma unroll
+  for (int w2 = 1; w2 < 4; ++w2) {
+    const float4 rg = s_red[((j * 3 + w2 - 1) * 2 + 0) * 64 + lane];
+    const float4 ru = s_red[((j * 3 + w2 - 1) * 2 + 1) * 64 + lane];
+    ag[0] += rg.x; ag[1] += rg.y; ag[2] += rg.z; ag[3] += rg.w;
+    au[0] += ru.x; au[1] += ru.y; au[2] += ru.z; au[3] += ru.w;
+  }
+  const int m = col;
+  if (m >= rows) return;
+  const int n0 = tile * 16 + grp * 4;
+  float o4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float g = rbf(ag[i]);
+    const float u = rbf(au[i]);
+    const float sg = rbf(g / (1.0f + expf(-g)));
+    o4[i] = sg * u;
+  }
+  uint2 o;
+  o.x = pack2(o4[0], o4[1]);
+  o.y = pack2(o4[2], o4[3]);
+  uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
+  *reinterpret_cast<uint2 *>(p.ofrag ? out + frag_off(m, n0, p.ofrag) : out + (size_t)m * p.n + n0) = o;
+}
+
+}  // namespace
+
+hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
+  int dev = 0, ncu = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int P = p.n / 16;
+  // One workgroup per CU, each with at most kResMaxPairs tile pairs; a larger
+  // matrix gets more workgroups than CUs (the planner bounds the pairs).
+  const int grid = std::max(ncu, (P + kResMaxPairs - 1) / kResMaxPairs);
+  const int pairs = (P + grid - 1) / grid;
+  if (pairs > kResMaxPairs || p.rw != kResRing || p.ksw % kResRing) return hipErrorInvalidValue;
+  // The last four waves normalise the rows, so the other waves are at least
+  // one pair's (rows up to kResMaxRows, the planner's bound).
+  if (pairs < 2 || p.rows > kResMaxRows) return hipErrorInvalidValue;
+  GemmParams q = p;
+  q.res_waves = 4 * pairs;
+  hipLaunchKernelGGL((glu_resident_kernel<kResRing>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+  return hipSuccess;
+}
+
+}  // namespace qdec

@@ -23,6 +23,15 @@ constexpr int kGemmDirectGluRows = 6;
 constexpr int kFastRowsMax = 4;
 // 64-bit argmax keys per row (ARGMAX), each workgroup folding into one.
 constexpr int kArgSlots = 16;
+// Resident gate/up (gemm_resident.hip): NORM_IN | GLU calls of
+// kResMinRows..kResMaxRows rows with one workgroup per CU holding the
+// normalised rows in LDS; at most kResMaxPairs tile pairs (4 waves each) per
+// workgroup and kResMaxKSteps k steps (k <= 2560).
+constexpr int kResMinRows = 6;
+constexpr int kResMaxRows = 8;
+constexpr int kResMaxPairs = 3;
+constexpr int kResMaxKSteps = 80;
+constexpr int kResRing = 10;  // weight ring slots (gate|up block pairs) per wave
 
 struct GemmParams {
   const void *x;
@@ -75,6 +84,8 @@ struct GemmParams {
   uint16_t *hmerged;
   int hthreads, hxt;
   uint32_t *hsync;
+  int resident;  // NORM_IN | GLU with the normalised rows resident in LDS (gemm_resident.hip)
+  int res_waves;  // resident: waves per workgroup (set by the launcher)
   size_t lds_bytes;
 };
 // Template flag of the hand-over instantiations (beside the QDEC_* flags).
@@ -90,6 +101,7 @@ int gemm_ring(int ksw, uint32_t flags);
 int gemm_ring_direct(int mt, uint32_t flags, int tw, int ksw, int groups);
 hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStream_t s);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
+hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s);
 
 struct AttnParams {
   const void *qkv;

@@ -48,7 +48,8 @@ class GemmArgs(ctypes.Structure):
                 ("n", I32), ("k", I32), ("flags", ctypes.c_uint32), ("ksplit", I32), ("waves", I32),
                 ("tiles_per_wg", I32), ("x_attn", P), ("x_frag", I32), ("out_frag", I32),
                 ("parts_out", P), ("x_parts", P), ("x_nparts", I32), ("x_merged", P),
-                ("next_norm_w", P), ("next_xn", P), ("next_merged", P), ("next_threads", I32)]
+                ("next_norm_w", P), ("next_xn", P), ("next_merged", P), ("next_threads", I32),
+                ("resident", I32)]
 
 
 class AttnArgs(ctypes.Structure):

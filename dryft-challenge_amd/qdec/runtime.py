@@ -100,6 +100,13 @@ O_FOUR_WAVES_MIN_BATCH = 8
 # 16.1 / 15.0; gate/up (28.4 / 30.4) and O (10.5 / 13.5) keep one.
 WIDE_TILES = 2
 WIDE_MIN_ROWS = 17
+# gate/up at RESIDENT_MIN_ROWS..RESIDENT_MAX_ROWS rows runs with its rows
+# resident in LDS (qdec_gemm's resident: one workgroup per CU normalises the
+# rows itself, no pre-pass launch, no per-tile activation reads; the same
+# bits as the pre-pass path) wherever the library's plan takes the shape.
+RESIDENT_GLU = True
+RESIDENT_MIN_ROWS = 6
+RESIDENT_MAX_ROWS = 8
 
 
 def round_up(x, m):
@@ -447,6 +454,9 @@ class DecodeState:
         # Norm hand-over target: the consumer's rows in fragment order.
         self.hand_over = HAND_OVER
         self._hand_cache = {}
+        # gate/up with its rows resident in LDS (RESIDENT_GLU; a state may
+        # turn it off before its first step)
+        self.resident_glu = RESIDENT_GLU
         self.xn_hand = torch.zeros((round_up(R, 16) * H,), dtype=bf, device=dev)
         # scratch: sized for the largest call of every kernel.
         gw = 0
@@ -475,6 +485,24 @@ class DecodeState:
         head; other shapes merge in the attention."""
         c = self.model.cfg
         return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH and c.group == 4 and c.head_dim == 128
+
+    def _resident(self, a):
+        """Whether the gate/up call ``a`` (resident still 0) runs with its
+        rows resident in LDS: resident_glu, its row count in
+        RESIDENT_MIN_ROWS..RESIDENT_MAX_ROWS and a plan the library accepts
+        for this shape (asked once per row count)."""
+        if not self.resident_glu or not (RESIDENT_MIN_ROWS <= a.rows <= RESIDENT_MAX_ROWS):
+            return False
+        cache = self.__dict__.setdefault("_resident_cache", {})
+        if a.rows not in cache:
+            a.resident = 1
+            try:
+                self.lib.gemm_workspace(a)
+                cache[a.rows] = True
+            except capi.QdecError:
+                cache[a.rows] = False
+            a.resident = 0
+        return cache[a.rows]
 
     def _hb(self, layer):
         """Residual buffer of ``layer`` (hbuf[0] throughout when down does not
@@ -555,6 +583,7 @@ class DecodeState:
             a.norm_w = m.post_w[layer].data_ptr()
             a.n, a.k, a.flags = c.inter, c.hidden, capi.NORM_IN | capi.GLU
             a.out_frag = 1 if rows >= FRAG_ROWS else 0
+            a.resident = 1 if self._resident(a) else 0
         elif role == "down":
             a.x, a.w, a.res = self.act.data_ptr(), m.w_down[layer].data_ptr(), h.data_ptr()
             a.n, a.k, a.flags = c.hidden, c.inter, capi.RES_OUT

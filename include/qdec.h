@@ -221,6 +221,20 @@ typedef struct {
   void *next_xn;
   void *next_merged;
   int32_t next_threads;
+  /* 1: gate/up with its rows resident in LDS.  For NORM_IN | GLU with
+   * ksplit 1, 4 waves, one tile per workgroup, row-major x (no x_frag,
+   * x_attn, x_parts or next_norm_w), 6..8 rows, k <= 2560 and k / 128 a
+   * multiple of 10: one workgroup per compute unit takes a contiguous run
+   * of (gate, up) tile pairs, normalises the rows once into LDS and reads
+   * its MFMA operands from there, so no normalisation pre-pass is launched
+   * and no workgroup re-reads the activations from L2.  The output is
+   * bit-identical to the same call with resident = 0 (the statistic, the
+   * k split over 4 waves and the epilogue are the same); the workspace is
+   * none.  QDEC_EUNSUPPORTED outside those bounds.  0: off.
+   * No counterpart in the reference: its fused.gemv launches one program
+   * per output block, each normalising the rows itself
+   * (engine/kernels/fused.py:33-172). */
+  int32_t resident;
 } qdec_gemm_args;
 int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream);
 /* Scratch sizes (bytes) a qdec_gemm call with these arguments needs. */

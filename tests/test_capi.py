@@ -113,6 +113,37 @@ def test_gemm_prepass_query(qlib):
     assert qlib.so.qdec_gemm_prepass(ctypes.byref(_gemm(rows=0)), None) == -1
 
 
+GU_RES = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4, rows=8, resident=1)
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(resident=2), -1, "resident 2"),
+    (dict(flags=capi.NORM_IN), -3, "NORM_IN | GLU"),
+    (dict(ksplit=2), -3, "ksplit 1"),
+    (dict(waves=8), -3, "4 waves"),
+    (dict(tiles_per_wg=2), -3, "one tile"),
+    (dict(x_frag=1, flags=capi.GLU), -3, "row-major x"),
+    (dict(rows=5), -3, "6..8 rows"),
+    (dict(rows=9), -3, "6..8 rows"),
+    (dict(k=4096), -3, "k <= 2560"),
+    (dict(k=1024), -3, "multiple of 10"),
+])
+def test_gemm_resident_validation(qlib, kw, code, needle):
+    """The resident gate/up plan takes exactly the shapes its kernel was
+    built for and refuses the rest before any launch."""
+    args = dict(GU_RES, **kw)
+    rc = qlib.so.qdec_gemm(ctypes.byref(_gemm(**args)), None)
+    assert rc == code
+    assert needle in qlib.last_error()
+
+
+def test_gemm_resident_needs_no_workspace_or_prepass(qlib):
+    for rows in (6, 7, 8):
+        assert qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows))) == (0, 0)
+        assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows))) == (False, 256)
+        assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows, resident=0))) == (True, 256)
+
+
 def test_gemm_glu_argmax_alone_need_fragment_order(qlib):
     for f in (capi.GLU, capi.ARGMAX):
         assert qlib.so.qdec_gemm(ctypes.byref(_gemm(flags=f, rows=20, n=9728 if f == capi.GLU else 151936,

@@ -447,6 +447,42 @@ def test_glu_to_down_in_fragment_order_bitexact(lib, rows):
     assert torch.equal(results[0].view(torch.int16), results[1].view(torch.int16))
 
 
+@pytest.mark.parametrize("frag", [0, 1])
+@pytest.mark.parametrize("rows", [6, 7, 8])
+def test_glu_resident_bitexact(lib, rows, frag):
+    """gate/up with its rows resident in LDS (one workgroup per CU normalising
+    the rows itself, no pre-pass) gives the bits of the pre-pass + direct
+    path, in row-major and fragment-order output, and agrees with the oracle.
+    Rows of very different magnitude check that each row keeps its own
+    statistic."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    ks, waves, _ = role_plan(I, H, "gate_up")
+    x = rnd(rows, H, scale=3.0, seed=90 + rows)
+    x[1] = (x[1].float() * 40.0).to(torch.bfloat16)
+    x[rows - 1] = (x[rows - 1].float() * 0.01).to(torch.bfloat16)
+    W = rnd(2 * I, H, scale=0.02, seed=91)
+    nw = bf16(1 + 0.2 * torch.randn(H, generator=torch.Generator().manual_seed(92))).to(torch.bfloat16)
+    xd, Wt, nwd = x.to(DEV), pack(lib, W.to(DEV)), nw.to(DEV)
+    g = Gemm(lib, capi.NORM_IN | capi.GLU, I, H, ksplit=ks, waves=waves)
+    outs = []
+    for resident in (0, 1):
+        out = torch.full(((rows + 15) // 16 * 16, I), float("nan"), dtype=torch.bfloat16, device=DEV)
+        a = capi.GemmArgs(x=xd.data_ptr(), w=Wt.data_ptr(), out=out.data_ptr(), norm_w=nwd.data_ptr(), eps=1e-6,
+                          rows=rows, n=I, k=H, flags=capi.NORM_IN | capi.GLU, ksplit=ks, waves=waves,
+                          tiles_per_wg=1, out_frag=frag, resident=resident, partial=g.partial.data_ptr(),
+                          counters=g.counters.data_ptr())
+        pb, _ = lib.gemm_workspace(a)
+        assert (pb == 0) == bool(resident)
+        assert lib.gemm_prepass(a)[0] == (0 if resident else 1)
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        outs.append(frag_to_rows(out, rows, I).cpu() if frag else out[:rows].cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    xin = rms_norm(x.float(), nw.float(), 1e-6)
+    agree(outs[1], silu_mul(linear(xin, W[:I].float()), linear(xin, W[I:].float())), min_exact=0.97)
+
+
 def attn_oracle(c, B, T):
     qkv = c["qkv"].float().view(B, T, NQ + 2 * NKV, D)
     kc, vc = c["kc"].float().clone(), c["vc"].float().clone()
