@@ -53,7 +53,7 @@ static void gemm_scratch(const qdec_gemm_args *a, const GemmParams &p, size_t *p
   }
   if (a->next_norm_w) cb = std::max(cb, (size_t)12);  // hand-over arrival, departure and give-up words
   size_t off = 0;
-  if (p.xd && p.xpre) {
+  if ((p.xd || p.resident) && p.xpre) {
     off = (pb + 255) & ~(size_t)255;
     pb = off + sizeof(uint16_t) * (size_t)(p.xt ? p.xt * 16 : a->rows) * a->k;
   }
@@ -148,17 +148,28 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
         xa || a->x_parts || a->next_norm_w)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs NORM_IN | GLU, ksplit 1, 4 waves, one tile per "
                        "workgroup and row-major x (no x_frag, x_attn, x_parts or next_norm_w)");
-    if (a->rows < kResMinRows || a->rows > kResMaxRows)
-      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d rows, not %d", kResMinRows, kResMaxRows,
-                       a->rows);
+    const bool two = a->rows >= kResMinRows2 && a->rows <= kResMaxRows2;
+    if (!two && (a->rows < kResMinRows || a->rows > kResMaxRows))
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d or %d..%d rows, not %d", kResMinRows,
+                       kResMaxRows, kResMinRows2, kResMaxRows2, a->rows);
     if (KS > kResMaxKSteps || p->ksw % kResRing)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs k <= %d with k/128 a multiple of %d (k %d)",
                        kResMaxKSteps * 32, kResRing, a->k);
+    if (ntiles < 2) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs at least two tile pairs");
     p->resident = 1;
     p->rw = kResRing;
     p->kp = 0;
     p->npass = 0;
     p->lds_bytes = 0;  // static LDS
+    if (two) {
+      // the normalisation pre-pass writes the rows in fragment order first
+      p->xpre = 1;
+      p->xt = 2;
+    }
+    size_t pb = 0, cb = 0, xn_off = 0;
+    gemm_scratch(a, *p, &pb, &cb, &xn_off);
+    if (need_scratch && pb && !a->partial) return set_error(QDEC_EINVAL, "qdec_gemm: this call needs a partial workspace");
+    if (p->xpre && a->partial) p->xn = reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(a->partial) + xn_off);
     return QDEC_OK;
   }
   const int kpmax = glu ? kGemmKpMaxGlu : kGemmKpMax;
@@ -576,7 +587,7 @@ int qdec_gemm_prepass(const qdec_gemm_args *a, int32_t *threads) {
   const int rc = plan_gemm(a, &p, false);
   if (rc != QDEC_OK) return rc;
   if (threads) *threads = 64 * a->waves;
-  return (p.xd && p.xpre) ? 1 : 0;
+  return ((p.xd || p.resident) && p.xpre) ? 1 : 0;
 }
 
 int qdec_gemm(const qdec_gemm_args *a, qdec_stream_t stream) {

@@ -288,7 +288,13 @@ hipError_t launch_rownorm_rows(const void *x, const void *norm_w, void *out, flo
 }
 
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
-  if (p.resident) return launch_glu_resident(p, s);
+  if (p.resident) {
+    if (p.xpre) {
+      const hipError_t e = launch_rownorm(p, dim3(64 * p.waves), true, s);
+      if (e != hipSuccess) return e;
+    }
+    return launch_glu_resident(p, s);
+  }
   const int mt = (p.rows + 15) / 16;
   const int ntiles = p.n / 16;
   dim3 grid((ntiles / p.tiles_per_wg) * p.ksplit);

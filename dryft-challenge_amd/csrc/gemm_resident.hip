@@ -237,6 +237,152 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident_kernel(con
   *reinterpret_cast<uint2 *>(p.ofrag ? out + frag_off(m, n0, p.ofrag) : out + (size_t)m * p.n + n0) = o;
 }
 
+// 16 bytes per lane from global memory into LDS at byte address lds_addr +
+// 16 * lane (global_load_lds_dwordx4; M0 holds the wave's LDS address),
+// from inline assembly: the compiler does not count these loads, so the
+// caller waits for them (vmcnt) itself.  They are issued before any load the
+// compiler counts, so its own waits stay correct (loads complete in order).
+__device__ __forceinline__ void res_dma16(const void *g, uint32_t lds_addr) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+      : "memory");
+}
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+constexpr int res_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// Two M tiles (17..32 rows): the rows, normalised in fragment order by the
+// pre-pass (p.xn), are copied once per workgroup into LDS -- the whole
+// 160 KiB of LDS for k = 2560, so nothing else lives there until the k loop
+// is done -- instead of every tile pair's workgroup reading them from L2 as
+// ring operands (608 x 164 KB per launch for Qwen3-4B at 32 rows).  The
+// ring then holds weights only (RW slots of gate and up blocks).  Sums,
+// order and epilogue are the direct path's at two M tiles.
+template <int RW>
+__global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(const GemmParams p) {
+  constexpr int MT = 2;
+  __shared__ __align__(16) uint4 s_x[kResMaxKSteps * MT * 64];  // [k step][M tile][lane]; then the wave merge
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = p.res_waves;
+  const int rows = p.rows, KS = p.KS, ksw = p.ksw;
+  const int col = lane & 15, grp = lane >> 4;
+  const unsigned P = (unsigned)p.n >> 4;
+  const unsigned pair0 = blockIdx.x * P / gridDim.x;
+  const int npairs = (int)((blockIdx.x + 1) * P / gridDim.x - pair0);
+  const int j = wave >> 2, q = wave & 3;
+  const bool active = j < npairs;
+  const int tile = (int)pair0 + j;
+
+  // ---- the rows into LDS: fragment f = (k step, M tile) is one KiB, wave w
+  // copies fragments w, w + nw, ...  (LDS DMA, no registers).
+  const uint4 *xn = reinterpret_cast<const uint4 *>(p.xn);
+  const int nfrag = KS * MT;
+  const uint32_t xbase = (uint32_t)reinterpret_cast<uintptr_t>(s_x);
+  int ndma = 0;
+  for (int f = wave; f < nfrag; f += nw, ++ndma) res_dma16(xn + (size_t)f * 64 + lane, xbase + (uint32_t)f * 1024u);
+
+  // ---- the ring: the first RW k steps of this wave's range.
+  const uint4 *W = reinterpret_cast<const uint4 *>(p.w);
+  const size_t up_off = (size_t)p.up_tiles * KS * 64;
+  const int ksw_w = active ? ksw : 0;
+  const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + lane;
+  uint4 wg[RW], wu[RW];
+  if (active) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      wg[r] = ldw(wq + r * 64);
+      wu[r] = ldw(wq + r * 64 + up_off);
+    }
+  }
+  // The copies are older than every ring load: once at most 2 RW loads are
+  // outstanding (RW when the wave has no pair), they have landed.
+  if (active)
+    __builtin_amdgcn_s_waitcnt(res_vmcnt(2 * RW));
+  else
+    __builtin_amdgcn_s_waitcnt(res_vmcnt(0));
+  (void)ndma;
+  __syncthreads();
+
+  f32x4_t ag[MT], au[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) ag[mt] = au[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool xrow0 = col < rows, xrow1 = 16 + col < rows;
+  constexpr int CH = 5;  // k steps whose B operands are read from LDS ahead
+  static_assert(RW % CH == 0, "chunks within a ring pass");
+  for (int i0 = 0; i0 < ksw_w; i0 += RW) {
+    const bool refill = i0 + RW < ksw_w;
+    const uint4 *qn = wq + (size_t)(i0 + RW) * 64;
+#pragma unroll
+    for (int c0 = 0; c0 < RW; c0 += CH) {
+      uint4 b0[CH], b1[CH];
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int s = q * ksw + i0 + c0 + c;
+        b0[c] = xrow0 ? s_x[(s * MT + 0) * 64 + lane] : zero4();
+        b1[c] = xrow1 ? s_x[(s * MT + 1) * 64 + lane] : zero4();
+      }
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int r = c0 + c;
+        ag[0] = mfma16x16x32(wg[r], b0[c], ag[0]);
+        ag[1] = mfma16x16x32(wg[r], b1[c], ag[1]);
+        au[0] = mfma16x16x32(wu[r], b0[c], au[0]);
+        au[1] = mfma16x16x32(wu[r], b1[c], au[1]);
+        if (refill) {
+          wg[r] = ldw(qn + r * 64);
+          wu[r] = ldw(qn + r * 64 + up_off);
+        }
+      }
+    }
+  }
+
+  // ---- the pair's four waves in wave order (the merge reuses the rows' LDS),
+  // then SwiGLU.
+  __syncthreads();
+  float4 *red = reinterpret_cast<float4 *>(s_x);  // [pair][wave 1..3][gate, up][M tile][lane]
+  if (active && q > 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      red[((((j * 3 + q - 1) * 2 + 0) * MT + mt) * 64) + lane] = make_float4(ag[mt][0], ag[mt][1], ag[mt][2], ag[mt][3]);
+      red[((((j * 3 + q - 1) * 2 + 1) * MT + mt) * 64) + lane] = make_float4(au[mt][0], au[mt][1], au[mt][2], au[mt][3]);
+    }
+  }
+  __syncthreads();
+  if (!active || q != 0) return;
+#pragma unroll
+  for (int w2 = 1; w2 < 4; ++w2) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float4 rg = red[((((j * 3 + w2 - 1) * 2 + 0) * MT + mt) * 64) + lane];
+      const float4 ru = red[((((j * 3 + w2 - 1) * 2 + 1) * MT + mt) * 64) + lane];
+      ag[mt][0] += rg.x; ag[mt][1] += rg.y; ag[mt][2] += rg.z; ag[mt][3] += rg.w;
+      au[mt][0] += ru.x; au[mt][1] += ru.y; au[mt][2] += ru.z; au[mt][3] += ru.w;
+    }
+  }
+  const int n0 = tile * 16 + grp * 4;
+  uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + col;
+    if (m >= rows) continue;
+    float o4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float g = rbf(ag[mt][i]);
+      const float u = rbf(au[mt][i]);
+      const float sg = rbf(g / (1.0f + expf(-g)));
+      o4[i] = sg * u;
+    }
+    uint2 o;
+    o.x = pack2(o4[0], o4[1]);
+    o.y = pack2(o4[2], o4[3]);
+    *reinterpret_cast<uint2 *>(p.ofrag ? out + frag_off(m, n0, p.ofrag) : out + (size_t)m * p.n + n0) = o;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
@@ -246,17 +392,23 @@ hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
   e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
   const int P = p.n / 16;
-  // One workgroup per CU, each with at most kResMaxPairs tile pairs; a larger
-  // matrix gets more workgroups than CUs (the planner bounds the pairs).
-  const int grid = std::max(ncu, (P + kResMaxPairs - 1) / kResMaxPairs);
+  // One workgroup per CU with two or three tile pairs each: more workgroups
+  // than CUs for a matrix past kResMaxPairs per CU, fewer for one below two.
+  const int grid = std::max((P + kResMaxPairs - 1) / kResMaxPairs, std::min(ncu, P / 2));
+  if (grid < 1) return hipErrorInvalidValue;
   const int pairs = (P + grid - 1) / grid;
   if (pairs > kResMaxPairs || p.rw != kResRing || p.ksw % kResRing) return hipErrorInvalidValue;
-  // The last four waves normalise the rows, so the other waves are at least
-  // one pair's (rows up to kResMaxRows, the planner's bound).
-  if (pairs < 2 || p.rows > kResMaxRows) return hipErrorInvalidValue;
   GemmParams q = p;
   q.res_waves = 4 * pairs;
-  hipLaunchKernelGGL((glu_resident_kernel<kResRing>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+  if (p.rows <= kResMaxRows) {
+    // The last four waves normalise the rows, so the others are at least one
+    // pair's.
+    if (pairs < 2) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((glu_resident_kernel<kResRing>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+  } else {
+    if (p.rows > 32 || !p.xn || p.KS > kResMaxKSteps) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((glu_resident2_kernel<kResRing>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+  }
   return hipSuccess;
 }
 

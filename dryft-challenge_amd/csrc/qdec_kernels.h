@@ -23,12 +23,16 @@ constexpr int kGemmDirectGluRows = 6;
 constexpr int kFastRowsMax = 4;
 // 64-bit argmax keys per row (ARGMAX), each workgroup folding into one.
 constexpr int kArgSlots = 16;
-// Resident gate/up (gemm_resident.hip): NORM_IN | GLU calls of
-// kResMinRows..kResMaxRows rows with one workgroup per CU holding the
-// normalised rows in LDS; at most kResMaxPairs tile pairs (4 waves each) per
-// workgroup and kResMaxKSteps k steps (k <= 2560).
+// Resident gate/up (gemm_resident.hip): NORM_IN | GLU calls with one
+// workgroup per CU holding the normalised rows in LDS -- kResMinRows..
+// kResMaxRows rows normalised by the workgroup itself, kResMinRows2..
+// kResMaxRows2 rows (two M tiles) normalised by the pre-pass and copied in;
+// at most kResMaxPairs tile pairs (4 waves each) per workgroup and
+// kResMaxKSteps k steps (k <= 2560).
 constexpr int kResMinRows = 6;
 constexpr int kResMaxRows = 8;
+constexpr int kResMinRows2 = 17;
+constexpr int kResMaxRows2 = 32;
 constexpr int kResMaxPairs = 3;
 constexpr int kResMaxKSteps = 80;
 constexpr int kResRing = 10;  // weight ring slots (gate|up block pairs) per wave

@@ -100,13 +100,13 @@ O_FOUR_WAVES_MIN_BATCH = 8
 # 16.1 / 15.0; gate/up (28.4 / 30.4) and O (10.5 / 13.5) keep one.
 WIDE_TILES = 2
 WIDE_MIN_ROWS = 17
-# gate/up at RESIDENT_MIN_ROWS..RESIDENT_MAX_ROWS rows runs with its rows
-# resident in LDS (qdec_gemm's resident: one workgroup per CU normalises the
-# rows itself, no pre-pass launch, no per-tile activation reads; the same
-# bits as the pre-pass path) wherever the library's plan takes the shape.
+# gate/up at RESIDENT_ROWS rows runs with its rows resident in LDS
+# (qdec_gemm's resident: one workgroup per CU reads its operands from one
+# LDS copy of the normalised rows; at 6..8 rows it normalises them itself,
+# no pre-pass launch; the same bits as the pre-pass path) wherever the
+# library's plan takes the shape.
 RESIDENT_GLU = True
-RESIDENT_MIN_ROWS = 6
-RESIDENT_MAX_ROWS = 8
+RESIDENT_ROWS = ((6, 8), (17, 32))
 
 
 def round_up(x, m):
@@ -488,10 +488,10 @@ class DecodeState:
 
     def _resident(self, a):
         """Whether the gate/up call ``a`` (resident still 0) runs with its
-        rows resident in LDS: resident_glu, its row count in
-        RESIDENT_MIN_ROWS..RESIDENT_MAX_ROWS and a plan the library accepts
+        rows resident in LDS: resident_glu, its row count in one of
+        RESIDENT_ROWS and a plan the library accepts
         for this shape (asked once per row count)."""
-        if not self.resident_glu or not (RESIDENT_MIN_ROWS <= a.rows <= RESIDENT_MAX_ROWS):
+        if not self.resident_glu or not any(lo <= a.rows <= hi for lo, hi in RESIDENT_ROWS):
             return False
         cache = self.__dict__.setdefault("_resident_cache", {})
         if a.rows not in cache:

@@ -123,8 +123,11 @@ GU_RES = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4, rows=8, re
     (dict(waves=8), -3, "4 waves"),
     (dict(tiles_per_wg=2), -3, "one tile"),
     (dict(x_frag=1, flags=capi.GLU), -3, "row-major x"),
-    (dict(rows=5), -3, "6..8 rows"),
-    (dict(rows=9), -3, "6..8 rows"),
+    (dict(rows=5), -3, "6..8 or 17..32 rows"),
+    (dict(rows=9), -3, "6..8 or 17..32 rows"),
+    (dict(rows=16), -3, "6..8 or 17..32 rows"),
+    (dict(rows=33), -3, "6..8 or 17..32 rows"),
+    (dict(n=16), -3, "two tile pairs"),
     (dict(k=4096), -3, "k <= 2560"),
     (dict(k=1024), -3, "multiple of 10"),
 ])
@@ -137,11 +140,19 @@ def test_gemm_resident_validation(qlib, kw, code, needle):
     assert needle in qlib.last_error()
 
 
-def test_gemm_resident_needs_no_workspace_or_prepass(qlib):
+def test_gemm_resident_workspace_and_prepass(qlib):
+    """At 6..8 rows the resident call normalises its rows itself (no
+    workspace, no pre-pass); at 17..32 the pre-pass still writes the two M
+    tiles of normalised rows into the workspace, as without resident."""
     for rows in (6, 7, 8):
         assert qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows))) == (0, 0)
         assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows))) == (False, 256)
         assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows, resident=0))) == (True, 256)
+    for rows in (17, 32):
+        ws = qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows)))
+        assert ws == qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows, resident=0)))
+        assert ws[0] >= 32 * 2560 * 2
+        assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows))) == (True, 256)
 
 
 def test_gemm_glu_argmax_alone_need_fragment_order(qlib):
