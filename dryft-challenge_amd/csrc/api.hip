@@ -140,6 +140,23 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->ksw = KS / a->ksplit / a->waves;
   p->up_tiles = ntiles;
   p->resident = 0;
+  if (a->resident && f == QDEC_RES_OUT) {
+    // The rows copied into LDS by each workgroup, weights-only ring
+    // (gemm_resident.hip); the direct path's arithmetic.
+    if (a->resident != 1) return set_error(QDEC_EINVAL, "qdec_gemm: resident %d not 0 or 1", a->resident);
+    if (a->ksplit != 1 || a->tiles_per_wg != 1 || a->x_frag || xa || a->parts_out || a->next_norm_w)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT needs ksplit 1, one tile per workgroup and "
+                       "row-major x (no x_frag, x_attn, parts_out or next_norm_w)");
+    if (a->rows < 2 || a->rows > kResLdsRows)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT takes 2..%d rows, not %d", kResLdsRows, a->rows);
+    if (KS > kResLdsKSteps || (KS & 1))
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT needs k/32 even and at most %d (k %d)",
+                       kResLdsKSteps, a->k);
+    p->resident = 2;
+    p->rw = kResLdsRing;
+    p->lds_bytes = 0;  // static LDS
+    return QDEC_OK;
+  }
   if (a->resident) {
     // One workgroup per CU normalising the rows into LDS (gemm_resident.hip);
     // its arithmetic is that of the plan below (pre-pass + direct path).

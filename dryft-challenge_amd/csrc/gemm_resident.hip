@@ -383,7 +383,103 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   }
 }
 
+// RES_OUT without a k split at 2..kResLdsRows rows, x row-major: each
+// workgroup (one output tile, its waves splitting k as in the direct path)
+// first copies the rows into LDS with LDS DMA -- 8 rows x 64 bytes per k
+// step, 152 KiB for the down projection's k = 9728 -- and its weight ring
+// then holds weights only.  In the direct path every ring slot also loads
+// the k step's B fragment from x, 16 row pieces of 64 bytes per load (a
+// cache access per lane); here one DMA instruction gathers two k steps.
+// The MFMA chain, the wave merge and the RES_OUT epilogue are the direct
+// path's, so the result is bit-identical to it.
+template <int RW>
+__global__ void __launch_bounds__(512) res_rows_kernel(const GemmParams p) {
+  __shared__ __align__(16) uint4 s_x[kResLdsKSteps * 32];  // [k step][row 0..7][k group]; then the wave merge
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = p.waves;
+  const int rows = p.rows, k = p.k, KS = p.KS, ksw = p.ksw;
+  const int col = lane & 15, grp = lane >> 4;
+  const int tile = blockIdx.x;
+  const uint16_t *X = reinterpret_cast<const uint16_t *>(p.x);
+
+  // Residual values of this lane's outputs, loaded first (the direct path's
+  // res_early): the epilogue then waits on no dependent load.
+  uint2 res_v = make_uint2(0u, 0u);
+  if (wave == 0) res_v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p.res) +
+                                                         (size_t)(col < rows ? col : 0) * p.n + tile * 16 + grp * 4);
+
+  // ---- the rows into LDS: DMA instruction i covers k steps 2i and 2i + 1;
+  // lane L takes k step 2i + L / 32, row (L / 4) % 8, k group L % 4 (rows
+  // past the last read row 0; their B lanes use zeros).
+  const uint32_t xbase = (uint32_t)reinterpret_cast<uintptr_t>(s_x);
+  {
+    const int r = (lane >> 2) & 7, g = lane & 3;
+    const uint16_t *src = X + (size_t)(r < rows ? r : 0) * k + (lane >> 5) * 32 + g * 8;
+    for (int i = wave; i < KS / 2; i += nw) res_dma16(src + (size_t)i * 64, xbase + (uint32_t)i * 1024u);
+  }
+
+  // ---- the ring: the first RW k steps of this wave's range.
+  const uint4 *W = reinterpret_cast<const uint4 *>(p.w);
+  const uint4 *wq = W + ((size_t)tile * KS + (size_t)wave * ksw) * 64 + lane;
+  uint4 wb[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) wb[r] = ldw(wq + min(r, ksw - 1) * 64);
+  // The copies are older than every ring load (and the residual load):
+  // once at most RW loads are outstanding they have landed.
+  __builtin_amdgcn_s_waitcnt(res_vmcnt(RW));
+  __syncthreads();
+
+  f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool xrow_ok = col < rows;
+  const int kb = wave * ksw;  // first k step of this wave
+  for (int i0 = 0; i0 < ksw; i0 += RW) {
+    uint4 bq[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int s = kb + min(i0 + r, ksw - 1);
+      bq[r] = xrow_ok ? s_x[s * 32 + col * 4 + grp] : zero4();
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int i = i0 + r;
+      if (i < ksw) {
+        acc = mfma16x16x32(wb[r], bq[r], acc);
+        if (i + RW < ksw) wb[r] = ldw(wq + (size_t)(i + RW) * 64);
+      }
+    }
+  }
+
+  // ---- waves in order (the merge reuses the rows' LDS), then RES_OUT.
+  __syncthreads();
+  float4 *red = reinterpret_cast<float4 *>(s_x);
+  if (wave > 0) red[(wave - 1) * 64 + lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w2 = 1; w2 < nw; ++w2) {
+    const float4 r = red[(w2 - 1) * 64 + lane];
+    acc[0] += r.x;
+    acc[1] += r.y;
+    acc[2] += r.z;
+    acc[3] += r.w;
+  }
+  const int m = col;
+  if (m >= rows) return;
+  uint16_t *rp = reinterpret_cast<uint16_t *>(p.res) + (size_t)m * p.n + tile * 16 + grp * 4;
+  uint2 o;
+  o.x = pack2(lo16(res_v.x) + rbf(acc[0]), hi16(res_v.x) + rbf(acc[1]));
+  o.y = pack2(lo16(res_v.y) + rbf(acc[2]), hi16(res_v.y) + rbf(acc[3]));
+  *reinterpret_cast<uint2 *>(rp) = o;
+}
+
 }  // namespace
+
+hipError_t launch_res_rows(const GemmParams &p, hipStream_t s) {
+  if (p.rw != kResLdsRing || p.rows > kResLdsRows || p.KS > kResLdsKSteps || (p.KS & 1) || p.tiles_per_wg != 1 ||
+      p.ksplit != 1)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL((res_rows_kernel<kResLdsRing>), dim3(p.n / 16), dim3(64 * p.waves), 0, s, p);
+  return hipSuccess;
+}
 
 hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
   int dev = 0, ncu = 0;

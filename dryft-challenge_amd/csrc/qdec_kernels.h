@@ -36,6 +36,12 @@ constexpr int kResMaxRows2 = 32;
 constexpr int kResMaxPairs = 3;
 constexpr int kResMaxKSteps = 80;
 constexpr int kResRing = 10;  // weight ring slots (gate|up block pairs) per wave
+// RES_OUT with its rows staged in LDS by DMA (gemm_resident.hip): 2..
+// kResLdsRows rows, at most kResLdsKSteps k steps (8 rows x 64 bytes each),
+// kResLdsRing weight blocks in flight per wave.
+constexpr int kResLdsRows = 8;
+constexpr int kResLdsKSteps = 304;
+constexpr int kResLdsRing = 20;
 
 struct GemmParams {
   const void *x;
@@ -88,7 +94,7 @@ struct GemmParams {
   uint16_t *hmerged;
   int hthreads, hxt;
   uint32_t *hsync;
-  int resident;  // NORM_IN | GLU with the normalised rows resident in LDS (gemm_resident.hip)
+  int resident;  // gemm_resident.hip: 1 NORM_IN | GLU with the normalised rows in LDS, 2 RES_OUT with the rows in LDS
   int res_waves;  // resident: waves per workgroup (set by the launcher)
   size_t lds_bytes;
 };
@@ -106,6 +112,7 @@ int gemm_ring_direct(int mt, uint32_t flags, int tw, int ksw, int groups);
 hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStream_t s);
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s);
+hipError_t launch_res_rows(const GemmParams &p, hipStream_t s);
 
 struct AttnParams {
   const void *qkv;

@@ -107,6 +107,12 @@ WIDE_MIN_ROWS = 17
 # library's plan takes the shape.
 RESIDENT_GLU = True
 RESIDENT_ROWS = ((6, 8), (17, 32))
+# The RES_OUT roles that copy their 2..8 rows into LDS first (qdec_gemm's
+# resident for RES_OUT: a weights-only ring; the same bits).  Same-box A/B,
+# ms per step at 1024-token prompts (neither / down / down and O): batch 8
+# 2.794 / 2.696 / 2.661, batch 4 2.469 / 2.420 / 2.398.
+RESIDENT_RES_ROLES = ("down", "o")
+RESIDENT_RES_ROWS = (2, 8)
 
 
 def round_up(x, m):
@@ -454,9 +460,10 @@ class DecodeState:
         # Norm hand-over target: the consumer's rows in fragment order.
         self.hand_over = HAND_OVER
         self._hand_cache = {}
-        # gate/up with its rows resident in LDS (RESIDENT_GLU; a state may
-        # turn it off before its first step)
-        self.resident_glu = RESIDENT_GLU
+        # the resident plans of qdec_gemm (RESIDENT_GLU: gate/up at
+        # RESIDENT_ROWS, the RESIDENT_RES_ROLES at RESIDENT_RES_ROWS); a state
+        # may turn them off before its first step
+        self.resident = RESIDENT_GLU
         self.xn_hand = torch.zeros((round_up(R, 16) * H,), dtype=bf, device=dev)
         # scratch: sized for the largest call of every kernel.
         gw = 0
@@ -486,23 +493,31 @@ class DecodeState:
         c = self.model.cfg
         return t_rows == 1 and self.batch <= MERGE_IN_O_MAX_BATCH and c.group == 4 and c.head_dim == 128
 
-    def _resident(self, a):
-        """Whether the gate/up call ``a`` (resident still 0) runs with its
-        rows resident in LDS: resident_glu, its row count in one of
-        RESIDENT_ROWS and a plan the library accepts
-        for this shape (asked once per row count)."""
-        if not self.resident_glu or not any(lo <= a.rows <= hi for lo, hi in RESIDENT_ROWS):
+    def _resident(self, a, role):
+        """Whether the call ``a`` of ``role`` (resident still 0) runs
+        resident: self.resident, the role and its row count in the resident
+        plans (gate/up at RESIDENT_ROWS, RESIDENT_RES_ROLES at
+        RESIDENT_RES_ROWS), and a plan the library accepts for this shape
+        (asked once per role and row count)."""
+        if not self.resident or a.x_attn or a.x_frag or a.parts_out or a.next_norm_w:
+            return False
+        if role == "gate_up":
+            ok = any(lo <= a.rows <= hi for lo, hi in RESIDENT_ROWS)
+        else:
+            ok = role in RESIDENT_RES_ROLES and RESIDENT_RES_ROWS[0] <= a.rows <= RESIDENT_RES_ROWS[1]
+        if not ok:
             return False
         cache = self.__dict__.setdefault("_resident_cache", {})
-        if a.rows not in cache:
+        key = (role, a.rows)
+        if key not in cache:
             a.resident = 1
             try:
                 self.lib.gemm_workspace(a)
-                cache[a.rows] = True
+                cache[key] = True
             except capi.QdecError:
-                cache[a.rows] = False
+                cache[key] = False
             a.resident = 0
-        return cache[a.rows]
+        return cache[key]
 
     def _hb(self, layer):
         """Residual buffer of ``layer`` (hbuf[0] throughout when down does not
@@ -554,6 +569,7 @@ class DecodeState:
         a.flags &= ~capi.NORM_IN
         a.x, a.x_frag, a.norm_w = self.xn_hand.data_ptr(), 1, None
         a.x_parts, a.x_nparts, a.x_merged = None, 0, None
+        a.resident = 0
 
     def _gemm_args(self, role, layer, rows, ids_out=None, lens_inc=None, x_attn=None, pending=True, hand=False):
         """qdec_gemm arguments of ``role`` in ``layer`` over ``rows`` rows.
@@ -583,7 +599,6 @@ class DecodeState:
             a.norm_w = m.post_w[layer].data_ptr()
             a.n, a.k, a.flags = c.inter, c.hidden, capi.NORM_IN | capi.GLU
             a.out_frag = 1 if rows >= FRAG_ROWS else 0
-            a.resident = 1 if self._resident(a) else 0
         elif role == "down":
             a.x, a.w, a.res = self.act.data_ptr(), m.w_down[layer].data_ptr(), h.data_ptr()
             a.n, a.k, a.flags = c.hidden, c.inter, capi.RES_OUT
@@ -613,6 +628,8 @@ class DecodeState:
         if hasattr(self, "gemm_partial"):
             a.partial = self.gemm_partial.data_ptr()
             a.counters = self.gemm_counters.data_ptr()
+        if role in ("gate_up",) + RESIDENT_RES_ROLES:
+            a.resident = 1 if self._resident(a, role) else 0
         if hand:
             L = c.n_layers
             if role in ("o", "down"):
@@ -726,6 +743,7 @@ class DecodeState:
         a = self._gemm_args(role, layer, self.batch, x_attn=x_attn)
         a.ksplit, a.waves = 1, 4
         a.tiles_per_wg = 2 if role == "gate_up" else 1
+        a.resident = 0  # the layer kernel's stages run the per-block code of the plain plans
         return a
 
     def enable_layer_launch(self, spin_limit=0, workgroups=0):

@@ -140,6 +140,30 @@ def test_gemm_resident_validation(qlib, kw, code, needle):
     assert needle in qlib.last_error()
 
 
+DN_RES = dict(flags=capi.RES_OUT, res=16, n=2560, k=9728, waves=8, rows=8, resident=1)
+
+
+@pytest.mark.parametrize("kw,code,needle", [
+    (dict(ksplit=2), -3, "ksplit 1"),
+    (dict(tiles_per_wg=2), -3, "one tile"),
+    (dict(x_frag=1), -3, "row-major x"),
+    (dict(rows=1), -3, "2..8 rows"),
+    (dict(rows=9), -3, "2..8 rows"),
+    (dict(k=9696, waves=1), -3, "k/32 even"),
+    (dict(k=10240), -3, "at most 304"),
+    (dict(resident=3), -1, "resident 3"),
+])
+def test_gemm_resident_res_out_validation(qlib, kw, code, needle):
+    rc = qlib.so.qdec_gemm(ctypes.byref(_gemm(**dict(DN_RES, **kw))), None)
+    assert rc == code
+    assert needle in qlib.last_error()
+
+
+def test_gemm_resident_res_out_needs_no_workspace(qlib):
+    for rows in (2, 5, 8):
+        assert qlib.gemm_workspace(_gemm(**dict(DN_RES, rows=rows))) == (0, 0)
+
+
 def test_gemm_resident_workspace_and_prepass(qlib):
     """At 6..8 rows the resident call normalises its rows itself (no
     workspace, no pre-pass); at 17..32 the pre-pass still writes the two M

@@ -274,7 +274,7 @@ def test_norm_hand_over_equals_the_pre_pass(engine, B, S, t_rows, seed):
         st.hand_over = hand
         # With the hand-over, gate/up keeps its pre-pass plan at 6..8 rows (O
         # hands it the rows); without, it runs resident: the same bits.
-        st.resident_glu = not hand
+        st.resident = not hand
         if hand:
             assert st._hand_threads("o", rows) == 256
             assert st._hand_threads("down", rows) == (None if rows < 9 else 64 * st.plans["qkv"][1])

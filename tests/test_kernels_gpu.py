@@ -485,6 +485,33 @@ def test_glu_resident_bitexact(lib, rows, frag):
     agree(outs[1], silu_mul(linear(xin, W[:I].float()), linear(xin, W[I:].float())), min_exact=0.97)
 
 
+@pytest.mark.parametrize("role,rows", [("down", 2), ("down", 5), ("down", 8), ("o", 3), ("o", 8)])
+def test_res_out_rows_in_lds_bitexact(lib, role, rows):
+    """A RES_OUT call with its rows copied into LDS first (resident: a
+    weights-only ring) gives the bits of the same call without, and agrees
+    with the oracle."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    n, k = {"down": (H, I), "o": (H, 4096)}[role]
+    ks, waves, _ = role_plan(n, k, role, batch=rows)
+    x = rnd(rows, k, scale=1.0, seed=95 + rows)
+    W = rnd(n, k, scale=0.02, seed=96)
+    res0 = rnd(rows, n, scale=2.0, seed=97)
+    xd, Wt = x.to(DEV), pack(lib, W.to(DEV))
+    g = Gemm(lib, capi.RES_OUT, n, k, ksplit=ks, waves=waves)
+    outs = []
+    for resident in (0, 1):
+        res = res0.to(DEV).clone()
+        a = capi.GemmArgs(x=xd.data_ptr(), w=Wt.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=rows, n=n, k=k,
+                          flags=capi.RES_OUT, ksplit=ks, waves=waves, tiles_per_wg=1, resident=resident,
+                          partial=g.partial.data_ptr(), counters=g.counters.data_ptr())
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        outs.append(res.cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    agree(outs[1], bf16(res0.float() + linear(x.float(), W.float())))
+
+
 def attn_oracle(c, B, T):
     qkv = c["qkv"].float().view(B, T, NQ + 2 * NKV, D)
     kc, vc = c["kc"].float().clone(), c["vc"].float().clone()
