@@ -147,10 +147,10 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     if (a->ksplit != 1 || a->tiles_per_wg != 1 || a->x_frag || xa || a->parts_out || a->next_norm_w)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT needs ksplit 1, one tile per workgroup and "
                        "row-major x (no x_frag, x_attn, parts_out or next_norm_w)");
-    if (a->rows < 2 || a->rows > kResLdsRows)
-      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT takes 2..%d rows, not %d", kResLdsRows, a->rows);
-    if (KS > kResLdsKSteps || (KS & 1))
-      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT needs k/32 even and at most %d (k %d)",
+    if (a->rows > kResLdsRows)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT takes 1..%d rows, not %d", kResLdsRows, a->rows);
+    if (KS > kResLdsKSteps || (KS & 15))
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT needs k/32 a multiple of 16 and at most %d (k %d)",
                        kResLdsKSteps, a->k);
     p->resident = 2;
     p->rw = kResLdsRing;

@@ -383,13 +383,13 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   }
 }
 
-// RES_OUT without a k split at 2..kResLdsRows rows, x row-major: each
+// RES_OUT without a k split at 1..kResLdsRows rows, x row-major: each
 // workgroup (one output tile, its waves splitting k as in the direct path)
-// first copies the rows into LDS with LDS DMA -- 8 rows x 64 bytes per k
-// step, 152 KiB for the down projection's k = 9728 -- and its weight ring
+// first copies the rows into LDS with LDS DMA -- up to 8 rows x 64 bytes per
+// k step, 152 KiB for the down projection's k = 9728 -- and its weight ring
 // then holds weights only.  In the direct path every ring slot also loads
 // the k step's B fragment from x, 16 row pieces of 64 bytes per load (a
-// cache access per lane); here one DMA instruction gathers two k steps.
+// cache access per lane); here one DMA instruction gathers 2 to 16 k steps.
 // The MFMA chain, the wave merge and the RES_OUT epilogue are the direct
 // path's, so the result is bit-identical to it.
 template <int RW>
@@ -408,14 +408,19 @@ __global__ void __launch_bounds__(512) res_rows_kernel(const GemmParams p) {
   if (wave == 0) res_v = *reinterpret_cast<const uint2 *>(reinterpret_cast<const uint16_t *>(p.res) +
                                                          (size_t)(col < rows ? col : 0) * p.n + tile * 16 + grp * 4);
 
-  // ---- the rows into LDS: DMA instruction i covers k steps 2i and 2i + 1;
-  // lane L takes k step 2i + L / 32, row (L / 4) % 8, k group L % 4 (rows
-  // past the last read row 0; their B lanes use zeros).
+  // ---- the rows into LDS, R = rows rounded up to 1, 2, 4 or 8 of them per
+  // k step (R x 64 bytes): DMA instruction i covers the 16 / R k steps from
+  // i * 16 / R; lane L takes k step L / (4 R) of them, row (L / 4) % R, k
+  // group L % 4 (rows past the last read row 0; their B lanes use zeros).
+  const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+  const int lr = R == 1 ? 0 : R == 2 ? 1 : R == 4 ? 2 : 3;  // log2 R
   const uint32_t xbase = (uint32_t)reinterpret_cast<uintptr_t>(s_x);
   {
-    const int r = (lane >> 2) & 7, g = lane & 3;
-    const uint16_t *src = X + (size_t)(r < rows ? r : 0) * k + (lane >> 5) * 32 + g * 8;
-    for (int i = wave; i < KS / 2; i += nw) res_dma16(src + (size_t)i * 64, xbase + (uint32_t)i * 1024u);
+    const int r = (lane >> 2) & (R - 1), g = lane & 3;
+    const int sl = lane >> (2 + lr);  // k step within the instruction
+    const uint16_t *src = X + (size_t)(r < rows ? r : 0) * k + sl * 32 + g * 8;
+    const int per = 16 >> lr;  // k steps per instruction
+    for (int i = wave; i < KS / per; i += nw) res_dma16(src + (size_t)i * per * 32, xbase + (uint32_t)i * 1024u);
   }
 
   // ---- the ring: the first RW k steps of this wave's range.
@@ -437,7 +442,7 @@ __global__ void __launch_bounds__(512) res_rows_kernel(const GemmParams p) {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       const int s = kb + min(i0 + r, ksw - 1);
-      bq[r] = xrow_ok ? s_x[s * 32 + col * 4 + grp] : zero4();
+      bq[r] = xrow_ok ? s_x[((s << lr) + col) * 4 + grp] : zero4();
     }
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
@@ -474,8 +479,8 @@ __global__ void __launch_bounds__(512) res_rows_kernel(const GemmParams p) {
 }  // namespace
 
 hipError_t launch_res_rows(const GemmParams &p, hipStream_t s) {
-  if (p.rw != kResLdsRing || p.rows > kResLdsRows || p.KS > kResLdsKSteps || (p.KS & 1) || p.tiles_per_wg != 1 ||
-      p.ksplit != 1)
+  if (p.rw != kResLdsRing || p.rows < 1 || p.rows > kResLdsRows || p.KS > kResLdsKSteps || (p.KS & 15) ||
+      p.tiles_per_wg != 1 || p.ksplit != 1)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL((res_rows_kernel<kResLdsRing>), dim3(p.n / 16), dim3(64 * p.waves), 0, s, p);
   return hipSuccess;

@@ -107,12 +107,13 @@ WIDE_MIN_ROWS = 17
 # library's plan takes the shape.
 RESIDENT_GLU = True
 RESIDENT_ROWS = ((6, 8), (17, 32))
-# The RES_OUT roles that copy their 2..8 rows into LDS first (qdec_gemm's
+# The RES_OUT roles that copy their 1..8 rows into LDS first (qdec_gemm's
 # resident for RES_OUT: a weights-only ring; the same bits).  Same-box A/B,
 # ms per step at 1024-token prompts (neither / down / down and O): batch 8
-# 2.794 / 2.696 / 2.661, batch 4 2.469 / 2.420 / 2.398.
+# 2.794 / 2.696 / 2.661, batch 4 2.469 / 2.420 / 2.398; down at one row (O
+# takes the attention partials there): batch 1 2.138 -> 2.113.
 RESIDENT_RES_ROLES = ("down", "o")
-RESIDENT_RES_ROWS = (2, 8)
+RESIDENT_RES_ROWS = (1, 8)
 
 
 def round_up(x, m):

@@ -234,9 +234,10 @@ typedef struct {
    * call with resident = 0 (the statistic, the k split over 4 waves and the
    * epilogue are the same).
    * For RES_OUT with ksplit 1, one tile per workgroup, row-major x (no
-   * x_frag, x_attn, parts_out or next_norm_w), 2..8 rows and k / 32 even
-   * and at most 304: every workgroup first copies the rows into LDS (LDS
-   * DMA, 8 rows x 64 bytes per k step) and its weight ring then holds
+   * x_frag, x_attn, parts_out or next_norm_w), 1..8 rows and k / 32 a
+   * multiple of 16 and at most 304: every workgroup first copies the rows
+   * into LDS (LDS DMA, up to 8 rows x 64 bytes per k step) and its weight
+   * ring then holds
    * weights only, where the direct path loads each k step's rows beside
    * its weight block; the same bits as resident = 0.
    * QDEC_EUNSUPPORTED outside those bounds.  0: off.

@@ -147,9 +147,8 @@ DN_RES = dict(flags=capi.RES_OUT, res=16, n=2560, k=9728, waves=8, rows=8, resid
     (dict(ksplit=2), -3, "ksplit 1"),
     (dict(tiles_per_wg=2), -3, "one tile"),
     (dict(x_frag=1), -3, "row-major x"),
-    (dict(rows=1), -3, "2..8 rows"),
-    (dict(rows=9), -3, "2..8 rows"),
-    (dict(k=9696, waves=1), -3, "k/32 even"),
+    (dict(rows=9), -3, "1..8 rows"),
+    (dict(k=9696, waves=1), -3, "a multiple of 16"),
     (dict(k=10240), -3, "at most 304"),
     (dict(resident=3), -1, "resident 3"),
 ])
@@ -160,7 +159,7 @@ def test_gemm_resident_res_out_validation(qlib, kw, code, needle):
 
 
 def test_gemm_resident_res_out_needs_no_workspace(qlib):
-    for rows in (2, 5, 8):
+    for rows in (1, 2, 5, 8):
         assert qlib.gemm_workspace(_gemm(**dict(DN_RES, rows=rows))) == (0, 0)
 
 

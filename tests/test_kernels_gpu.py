@@ -485,7 +485,8 @@ def test_glu_resident_bitexact(lib, rows, frag):
     agree(outs[1], silu_mul(linear(xin, W[:I].float()), linear(xin, W[I:].float())), min_exact=0.97)
 
 
-@pytest.mark.parametrize("role,rows", [("down", 2), ("down", 5), ("down", 8), ("o", 3), ("o", 8)])
+@pytest.mark.parametrize("role,rows", [("down", 1), ("down", 2), ("down", 3), ("down", 5), ("down", 8), ("o", 1),
+                                      ("o", 3), ("o", 4), ("o", 8)])
 def test_res_out_rows_in_lds_bitexact(lib, role, rows):
     """A RES_OUT call with its rows copied into LDS first (resident: a
     weights-only ring) gives the bits of the same call without, and agrees
