@@ -140,6 +140,24 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->ksw = KS / a->ksplit / a->waves;
   p->up_tiles = ntiles;
   p->resident = 0;
+  if (a->resident && f == QDEC_RES_OUT && a->parts_out) {
+    // k parts left to the next NORM_IN call, each part's rows copied into
+    // LDS once per workgroup (gemm_resident.hip); the direct path's
+    // arithmetic.
+    if (a->resident != 1) return set_error(QDEC_EINVAL, "qdec_gemm: resident %d not 0 or 1", a->resident);
+    const int kp = a->ksplit > 0 ? KS / a->ksplit : 0;
+    if (a->ksplit < 2 || a->waves != 4 || !a->x_frag || xa || a->next_norm_w || a->rows < 17 || a->rows > 32 ||
+        kp > kResSplitKSteps)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident RES_OUT with parts_out needs ksplit > 1, 4 waves, "
+                       "x_frag = 1, 17..32 rows and at most %d k steps per split (no x_attn or next_norm_w)",
+                       kResSplitKSteps);
+    p->resident = 3;
+    p->rw = kResSplitRing;
+    p->xt = 2;
+    p->parts_out = a->parts_out;
+    p->lds_bytes = 0;  // static LDS
+    return QDEC_OK;
+  }
   if (a->resident && f == QDEC_RES_OUT) {
     // The rows copied into LDS by each workgroup, weights-only ring
     // (gemm_resident.hip); the direct path's arithmetic.

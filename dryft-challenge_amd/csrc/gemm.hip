@@ -289,6 +289,7 @@ hipError_t launch_rownorm_rows(const void *x, const void *norm_w, void *out, flo
 
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s) {
   if (p.resident == 2) return launch_res_rows(p, s);
+  if (p.resident == 3) return launch_res_split(p, s);
   if (p.resident) {
     if (p.xpre) {
       const hipError_t e = launch_rownorm(p, dim3(64 * p.waves), true, s);

@@ -476,7 +476,133 @@ __global__ void __launch_bounds__(512) res_rows_kernel(const GemmParams p) {
   *reinterpret_cast<uint2 *>(rp) = o;
 }
 
+// RES_OUT with its k split S ways into partials (parts_out) at two M tiles
+// (17..32 rows), x in fragment order: the workgroups of one k part share its
+// slice of the rows.  Workgroup w takes k part w % S and a contiguous run of
+// 2 or 3 output tiles (the S parts of the grid interleave over the XCDs);
+// its waves are four per tile, wave (j, q) streaming k steps [q kw, (q + 1)
+// kw) of its part of tile j, where the direct path gives the same k steps
+// to wave q of the tile's (or tile pair's) workgroup.  The part's rows are
+// copied into LDS once per workgroup by DMA (152 KiB for the down
+// projection's quarter of k = 9728), and the ring holds weights only.  A
+// tile's partial is each wave's MFMA chain in k order, the four waves added
+// in order, stored to parts_out[part] -- the direct path's arithmetic, the
+// same bits.
+template <int RW>
+__global__ void __launch_bounds__(64 * 4 * kResMaxPairs) res_split_kernel(const GemmParams p) {
+  constexpr int MT = 2;
+  __shared__ __align__(16) uint4 s_x[kResSplitKSteps * MT * 64];  // [k step of the part][M tile][lane]; then the merge
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = p.res_waves;
+  const int rows = p.rows, KS = p.KS, S = p.ksplit;
+  const int kp = KS / S;       // k steps of a part
+  const int kw = p.ksw;        // k steps of a wave (kp / 4)
+  const int col = lane & 15, grp = lane >> 4;
+  const int part = blockIdx.x % S;
+  const unsigned G = gridDim.x / S, g = blockIdx.x / S;
+  const unsigned T = (unsigned)p.n >> 4;
+  const unsigned t0 = g * T / G;
+  const int ntile = (int)((g + 1) * T / G - t0);
+  const int j = wave >> 2, q = wave & 3;
+  const bool active = j < ntile;
+  const int tile = (int)t0 + j;
+
+  // ---- the part's rows into LDS: fragment f = (k step of the part, M tile).
+  const uint4 *xf = reinterpret_cast<const uint4 *>(p.x) + (size_t)part * kp * MT * 64;
+  const uint32_t xbase = (uint32_t)reinterpret_cast<uintptr_t>(s_x);
+  for (int f = wave; f < kp * MT; f += nw) res_dma16(xf + (size_t)f * 64 + lane, xbase + (uint32_t)f * 1024u);
+
+  // ---- the ring: the first RW k steps of this wave's range (a range
+  // shorter than the ring repeats its last block).
+  const uint4 *W = reinterpret_cast<const uint4 *>(p.w);
+  const int kb = q * kw;  // first k step of this wave within the part
+  const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)part * kp + kb) * 64 + lane;
+  const int kw_w = active ? kw : 0;
+  uint4 wb[RW];
+  if (active) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) wb[r] = ldw(wq + min(r, kw - 1) * 64);
+  }
+  if (active)
+    __builtin_amdgcn_s_waitcnt(res_vmcnt(RW));
+  else
+    __builtin_amdgcn_s_waitcnt(res_vmcnt(0));
+  __syncthreads();
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool xrow0 = col < rows, xrow1 = 16 + col < rows;
+  for (int i0 = 0; i0 < kw_w; i0 += RW) {
+    uint4 b0[RW], b1[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int s2 = kb + min(i0 + r, kw - 1);
+      b0[r] = xrow0 ? s_x[(s2 * MT + 0) * 64 + lane] : zero4();
+      b1[r] = xrow1 ? s_x[(s2 * MT + 1) * 64 + lane] : zero4();
+    }
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int i = i0 + r;
+      if (i < kw_w) {
+        acc[0] = mfma16x16x32(wb[r], b0[r], acc[0]);
+        acc[1] = mfma16x16x32(wb[r], b1[r], acc[1]);
+        if (i + RW < kw_w) wb[r] = ldw(wq + (size_t)(i + RW) * 64);
+      }
+    }
+  }
+
+  // ---- the tile's four waves in order (the merge reuses the rows' LDS),
+  // then the partial to parts_out[part].
+  __syncthreads();
+  float4 *red = reinterpret_cast<float4 *>(s_x);  // [tile][wave 1..3][M tile][lane]
+  if (active && q > 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      red[((j * 3 + q - 1) * MT + mt) * 64 + lane] = make_float4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]);
+  }
+  __syncthreads();
+  if (!active || q != 0) return;
+#pragma unroll
+  for (int w2 = 1; w2 < 4; ++w2)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float4 r = red[((j * 3 + w2 - 1) * MT + mt) * 64 + lane];
+      acc[mt][0] += r.x;
+      acc[mt][1] += r.y;
+      acc[mt][2] += r.z;
+      acc[mt][3] += r.w;
+    }
+  const int n0 = tile * 16 + grp * 4;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + col;
+    if (m < rows) *reinterpret_cast<f32x4_t *>(p.parts_out + ((size_t)part * rows + m) * p.n + n0) = acc[mt];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_res_split(const GemmParams &p, hipStream_t s) {
+  int dev = 0, ncu = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return e;
+  const int S = p.ksplit, T = p.n / 16;
+  if (S < 1 || p.KS % S || (p.KS / S) % 4 || p.KS / S > kResSplitKSteps || p.ksw * 4 != p.KS / S || p.rows < 17 ||
+      p.rows > 32 || !p.parts_out || !p.xt || p.rw != kResSplitRing)
+    return hipErrorInvalidValue;
+  // Workgroups per part: one per CU in all, 2 or 3 tiles each.
+  const int G = std::max((T + kResMaxPairs - 1) / kResMaxPairs, std::min(ncu / S, T / 2));
+  if (G < 1) return hipErrorInvalidValue;
+  const int tiles = (T + G - 1) / G;
+  if (tiles > kResMaxPairs) return hipErrorInvalidValue;
+  GemmParams q = p;
+  q.res_waves = 4 * tiles;
+  hipLaunchKernelGGL((res_split_kernel<kResSplitRing>), dim3(G * S), dim3(64 * q.res_waves), 0, s, q);
+  return hipSuccess;
+}
 
 hipError_t launch_res_rows(const GemmParams &p, hipStream_t s) {
   if (p.rw != kResLdsRing || p.rows < 1 || p.rows > kResLdsRows || p.KS > kResLdsKSteps || (p.KS & 15) ||

@@ -42,6 +42,11 @@ constexpr int kResRing = 10;  // weight ring slots (gate|up block pairs) per wav
 constexpr int kResLdsRows = 8;
 constexpr int kResLdsKSteps = 304;
 constexpr int kResLdsRing = 20;
+// RES_OUT split into k parts at two M tiles with each part's rows in LDS
+// (gemm_resident.hip): at most kResSplitKSteps k steps per part (2 KiB each),
+// kResSplitRing weight blocks in flight per wave.
+constexpr int kResSplitKSteps = 76;
+constexpr int kResSplitRing = 10;
 
 struct GemmParams {
   const void *x;
@@ -94,7 +99,8 @@ struct GemmParams {
   uint16_t *hmerged;
   int hthreads, hxt;
   uint32_t *hsync;
-  int resident;  // gemm_resident.hip: 1 NORM_IN | GLU with the normalised rows in LDS, 2 RES_OUT with the rows in LDS
+  int resident;  // gemm_resident.hip: 1 NORM_IN | GLU with the normalised rows in LDS, 2 RES_OUT with the rows in LDS,
+                 // 3 RES_OUT split into k parts, each part's rows in LDS
   int res_waves;  // resident: waves per workgroup (set by the launcher)
   size_t lds_bytes;
 };
@@ -113,6 +119,7 @@ hipError_t launch_rownorm(const GemmParams &p, dim3 block, bool do_norm, hipStre
 hipError_t launch_gemm(const GemmParams &p, uint32_t flags, hipStream_t s);
 hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s);
 hipError_t launch_res_rows(const GemmParams &p, hipStream_t s);
+hipError_t launch_res_split(const GemmParams &p, hipStream_t s);
 
 struct AttnParams {
   const void *qkv;

@@ -114,6 +114,11 @@ RESIDENT_ROWS = ((6, 8), (17, 32))
 # takes the attention partials there): batch 1 2.138 -> 2.113.
 RESIDENT_RES_ROLES = ("down", "o")
 RESIDENT_RES_ROWS = (1, 8)
+# ... and the split down projection (DOWN_SPLIT parts) at these rows, each
+# part's rows copied into LDS once per workgroup (same-box A/B, ms per step:
+# batch 32 at 4096-token prompts 5.635 -> 5.551, batch 20 at 1024 3.393 ->
+# 3.311; down 15.1 -> 12.7 us per launch).
+RESIDENT_SPLIT_ROWS = (17, 32)
 
 
 def round_up(x, m):
@@ -500,16 +505,20 @@ class DecodeState:
         plans (gate/up at RESIDENT_ROWS, RESIDENT_RES_ROLES at
         RESIDENT_RES_ROWS), and a plan the library accepts for this shape
         (asked once per role and row count)."""
-        if not self.resident or a.x_attn or a.x_frag or a.parts_out or a.next_norm_w:
+        if not self.resident or a.x_attn or a.next_norm_w:
             return False
         if role == "gate_up":
-            ok = any(lo <= a.rows <= hi for lo, hi in RESIDENT_ROWS)
+            ok = not a.x_frag and any(lo <= a.rows <= hi for lo, hi in RESIDENT_ROWS)
+        elif role not in RESIDENT_RES_ROLES:
+            ok = False
+        elif a.parts_out:
+            ok = RESIDENT_SPLIT_ROWS[0] <= a.rows <= RESIDENT_SPLIT_ROWS[1]
         else:
-            ok = role in RESIDENT_RES_ROLES and RESIDENT_RES_ROWS[0] <= a.rows <= RESIDENT_RES_ROWS[1]
+            ok = not a.x_frag and RESIDENT_RES_ROWS[0] <= a.rows <= RESIDENT_RES_ROWS[1]
         if not ok:
             return False
         cache = self.__dict__.setdefault("_resident_cache", {})
-        key = (role, a.rows)
+        key = (role, a.rows, bool(a.parts_out), bool(a.x_frag))
         if key not in cache:
             a.resident = 1
             try:

@@ -240,6 +240,12 @@ typedef struct {
    * ring then holds
    * weights only, where the direct path loads each k step's rows beside
    * its weight block; the same bits as resident = 0.
+   * For RES_OUT with parts_out (ksplit > 1, 4 waves, x_frag = 1, 17..32
+   * rows, at most 76 k steps per split): the workgroups of each k split
+   * share its slice of the rows -- workgroup w takes split w % ksplit and
+   * 2 or 3 output tiles, copies that slice into LDS once (LDS DMA) and
+   * streams weights only; parts_out receives the same bits as with
+   * resident = 0.
    * QDEC_EUNSUPPORTED outside those bounds.  0: off.
    * No counterpart in the reference: its fused.gemv launches one program
    * per output block, each normalising the rows itself

@@ -158,6 +158,25 @@ def test_gemm_resident_res_out_validation(qlib, kw, code, needle):
     assert needle in qlib.last_error()
 
 
+DS_RES = dict(DN_RES, rows=32, waves=4, ksplit=4, tiles_per_wg=2, x_frag=1, parts_out=16)
+
+
+@pytest.mark.parametrize("kw,needle", [
+    (dict(rows=16), "17..32 rows"),
+    (dict(rows=33), "rows"),
+    (dict(waves=2), "4 waves"),
+    (dict(x_frag=0), "x_frag = 1"),
+    (dict(ksplit=2), "76 k steps per split"),
+])
+def test_gemm_resident_split_validation(qlib, kw, needle):
+    """The split RES_OUT resident plan (k parts left in parts_out) takes
+    only the shapes its kernel was built for."""
+    rc = qlib.so.qdec_gemm(ctypes.byref(_gemm(**dict(DS_RES, **kw))), None)
+    assert rc < 0
+    assert needle in qlib.last_error()
+    assert qlib.gemm_workspace(_gemm(**DS_RES)) == (0, 0)
+
+
 def test_gemm_resident_res_out_needs_no_workspace(qlib):
     for rows in (1, 2, 5, 8):
         assert qlib.gemm_workspace(_gemm(**dict(DN_RES, rows=rows))) == (0, 0)

@@ -513,6 +513,40 @@ def test_res_out_rows_in_lds_bitexact(lib, role, rows):
     agree(outs[1], bf16(res0.float() + linear(x.float(), W.float())))
 
 
+@pytest.mark.parametrize("rows", [17, 24, 32])
+def test_down_split_parts_in_lds_bitexact(lib, rows):
+    """The split down projection with each k part's rows copied into LDS once
+    per workgroup (resident) leaves the same fp32 partials as without, and
+    their sum agrees with the oracle."""
+    from qdec import capi
+    from qdec.runtime import DOWN_SPLIT, role_plan
+    ks, waves, _ = role_plan(H, I, "down", batch=32)
+    assert ks == DOWN_SPLIT and waves == 4
+    mt = (rows + 15) // 16
+    x = rnd(rows, I, scale=1.0, seed=101 + rows)
+    W = rnd(H, I, scale=0.02, seed=102)
+    xf = torch.zeros(mt * 16 * I, dtype=torch.bfloat16)
+    for m in range(rows):  # fragment order (include/qdec.h)
+        for c0 in range(0, I, 8):
+            off = ((c0 // 32 * mt + m // 16) * 64 + m % 16 + 16 * (c0 % 32 // 8)) * 8
+            xf[off:off + 8] = x[m, c0:c0 + 8]
+    xd, Wt = xf.to(DEV), pack(lib, W.to(DEV))
+    outs = []
+    for resident in (0, 1):
+        parts = torch.full((ks, rows, H), float("nan"), dtype=torch.float32, device=DEV)
+        res = torch.zeros(rows, H, dtype=torch.bfloat16, device=DEV)
+        a = capi.GemmArgs(x=xd.data_ptr(), w=Wt.data_ptr(), res=res.data_ptr(), eps=1e-6, rows=rows, n=H, k=I,
+                          flags=capi.RES_OUT, ksplit=ks, waves=waves, tiles_per_wg=2, x_frag=1,
+                          parts_out=parts.data_ptr(), resident=resident)
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        outs.append(parts.cpu())
+    assert torch.equal(outs[0].view(torch.int32), outs[1].view(torch.int32))
+    ref = linear(x.float(), W.float())
+    got = outs[1].sum(0)
+    assert (got - ref).abs().max().item() <= 0.02 * ref.abs().max().item()
+
+
 def attn_oracle(c, B, T):
     qkv = c["qkv"].float().view(B, T, NQ + 2 * NKV, D)
     kc, vc = c["kc"].float().clone(), c["vc"].float().clone()
