@@ -94,8 +94,8 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   if (a->parts_out && (f != QDEC_RES_OUT || a->ksplit < 2))
     return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: parts_out needs RES_OUT alone and ksplit > 1");
   if (a->x_parts) {
-    if (!(f & QDEC_NORM_IN) || (f & QDEC_GLU) || a->ksplit != 1 || a->x_attn)
-      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_parts needs NORM_IN without GLU, ksplit 1 and no x_attn");
+    if (!(f & QDEC_NORM_IN) || a->ksplit != 1 || a->x_attn)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_parts needs NORM_IN, ksplit 1 and no x_attn");
     if (a->x_nparts < 1 || a->x_nparts > 8) return set_error(QDEC_EINVAL, "qdec_gemm: x_nparts %d not in [1, 8]", a->x_nparts);
     if (need_scratch && (!a->x_merged || a->x_merged == a->x))
       return set_error(QDEC_EINVAL, "qdec_gemm: x_parts needs x_merged, a buffer other than x");
@@ -180,9 +180,9 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     // its arithmetic is that of the plan below (pre-pass + direct path).
     if (a->resident != 1) return set_error(QDEC_EINVAL, "qdec_gemm: resident %d not 0 or 1", a->resident);
     if (f != (QDEC_NORM_IN | QDEC_GLU) || a->ksplit != 1 || a->waves != 4 || a->tiles_per_wg != 1 || a->x_frag ||
-        xa || a->x_parts || a->next_norm_w)
+        xa || a->next_norm_w)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs NORM_IN | GLU, ksplit 1, 4 waves, one tile per "
-                       "workgroup and row-major x (no x_frag, x_attn, x_parts or next_norm_w)");
+                       "workgroup and row-major x (no x_frag, x_attn or next_norm_w)");
     const bool two = a->rows >= kResMinRows2 && a->rows <= kResMaxRows2;
     if (!two && (a->rows < kResMinRows || a->rows > kResMaxRows))
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d or %d..%d rows, not %d", kResMinRows,
@@ -196,10 +196,17 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     p->kp = 0;
     p->npass = 0;
     p->lds_bytes = 0;  // static LDS
+    if (a->x_parts && !two)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident with x_parts takes %d..%d rows (the pre-pass merges "
+                       "them), not %d", kResMinRows2, kResMaxRows2, a->rows);
     if (two) {
       // the normalisation pre-pass writes the rows in fragment order first
+      // (merging a pending split residual update into x_merged on the way)
       p->xpre = 1;
       p->xt = 2;
+      p->xparts = a->x_parts;
+      p->xnparts = a->x_parts ? a->x_nparts : 0;
+      p->xmerged = reinterpret_cast<uint16_t *>(a->x_merged);
     }
     size_t pb = 0, cb = 0, xn_off = 0;
     gemm_scratch(a, *p, &pb, &cb, &xn_off);
@@ -290,7 +297,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
   p->xparts = a->x_parts;
   p->xnparts = a->x_parts ? a->x_nparts : 0;
   p->xmerged = reinterpret_cast<uint16_t *>(a->x_merged);
-  if (a->x_parts && !(a->rows == 1 && p->xfast && p->rw > 0 && a->x_nparts <= 4)) {
+  if (a->x_parts && !(a->rows == 1 && !glu && p->xfast && p->rw > 0 && a->x_nparts <= 4)) {
     if (!ring_d)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: x_parts at %d rows needs the direct path, which this tile "
                        "grouping does not allow", a->rows);

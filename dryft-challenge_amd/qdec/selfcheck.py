@@ -251,7 +251,8 @@ def _shape_gemms(state, t):
         or (down split) zero rows plus one-hot split partials, which the call
         merges into x_merged first."""
         if a.x_parts:
-            state._hb(layer - 1)[:R].zero_()
+            # (with a split O the down projection's update belongs to hpost)
+            (state._hb(layer - 1) if state.o_parts is None else state.hpost)[:R].zero_()
             parts = split_parts()
             state.down_parts.zero_()
             parts[rows_i % parts.shape[0], rows_i, cols(k)] = 1.0
@@ -259,10 +260,11 @@ def _shape_gemms(state, t):
         else:
             state._hb(layer)[:R].copy_(one_hot(k))
 
-    def split_parts():
-        # the down projection's partials of an R-row call: [ks][R][hidden]
-        ks = state.down_parts.shape[0]
-        return state.down_parts.view(-1)[:ks * R * c.hidden].view(ks, R, c.hidden)
+    def split_parts(buf=None):
+        # a split projection's partials of an R-row call: [ks][R][hidden]
+        buf = state.down_parts if buf is None else buf
+        ks = buf.shape[0]
+        return buf.view(-1)[:ks * R * c.hidden].view(ks, R, c.hidden)
 
     def check_merged(a, layer, k, role):
         if a.x_parts and not torch.equal(state._hb(layer)[:R].float(), one_hot(k).float()):
@@ -278,22 +280,43 @@ def _shape_gemms(state, t):
     if not torch.equal(state.qkv[:R].float(), want):
         _fail("qkv", f"{R} rows: {int((state.qkv[:R].float() != want).sum())} outputs differ")
 
-    # O: residual + weight column
+    # O: residual + weight column, or the k split's partials
     a = state._gemm_args("o", 0, R)
     kq = c.nq * c.head_dim
     _put_rows(state.attn_out, one_hot(kq), a.x_frag)
     res0 = (torch.linspace(-3, 3, c.hidden, device=dev)[None] + 0.25 * rows_i[:, None]).to(torch.bfloat16)
-    state._hb(0)[:R].copy_(res0)
-    lib.gemm(a, s)
-    want = _bf16(res0.float() + wcols(m.w_o[0], c.hidden, kq))
-    if not torch.equal(state._hb(0)[:R].float(), want):
-        _fail("o", f"{R} rows: {int((state._hb(0)[:R].float() != want).sum())} outputs differ "
-                   "from weight column + residual")
+    wo = wcols(m.w_o[0], c.hidden, kq)
+    if a.parts_out:
+        state.o_parts.fill_(float("nan"))
+        lib.gemm(a, s)
+        parts = split_parts(state.o_parts)
+        ko = parts.shape[0]
+        want = torch.zeros((ko, R, c.hidden), device=dev)
+        want[cols(kq) // (kq // ko), rows_i] = wo
+        if not torch.equal(parts, want):
+            _fail("o", f"{R} rows: split partials differ from the weight column")
+    else:
+        state._hb(0)[:R].copy_(res0)
+        lib.gemm(a, s)
+        want = _bf16(res0.float() + wo)
+        if not torch.equal(state._hb(0)[:R].float(), want):
+            _fail("o", f"{R} rows: {int((state._hb(0)[:R].float() != want).sum())} outputs differ "
+                       "from weight column + residual")
 
-    # gate/up + SwiGLU (output in fragment order from FRAG_ROWS rows)
+    # gate/up + SwiGLU (output in fragment order from FRAG_ROWS rows); with a
+    # split O it first merges one-hot split partials into hpost
     a = state._gemm_args("gate_up", 0, R)
-    state._hb(0)[:R].copy_(one_hot(c.hidden))
+    if a.x_parts:
+        state._hb(0)[:R].zero_()
+        parts = split_parts(state.o_parts)
+        state.o_parts.zero_()
+        parts[rows_i % parts.shape[0], rows_i, cols(c.hidden)] = 1.0
+        state.hpost[:R].fill_(float("nan"))
+    else:
+        state._hb(0)[:R].copy_(one_hot(c.hidden))
     lib.gemm(a, s)
+    if a.x_parts and not torch.equal(state.hpost[:R].float(), one_hot(c.hidden).float()):
+        _fail("gate_up", f"{R} rows: the merged residual differs from the split partials' sum")
     got = _get_rows(state.act, R, c.inter, a.out_frag).float()
     wc = wcols(m.w_gu[0], 2 * c.inter, c.hidden)
     v = scale(c.hidden, m.post_w[0])

@@ -182,13 +182,14 @@ typedef struct {
    * parts_out[split][rows][n]; res is not touched and no counters are used.
    * The consumer passes the same buffer as x_parts. */
   float *parts_out;
-  /* NORM_IN: the residual x still owes a RES_OUT update held in k-split
-   * partials x_parts[j][rows][k], j < x_nparts (1..8).  The call first forms
-   * x = bf16(x + bf16(((p0 + p1) + p2) + ...)) per element -- the rounding a
-   * RES_OUT call applies -- uses it as its input and writes it to x_merged
-   * ([rows, k] bf16, not x itself: other workgroups of the call still read
-   * x).  Needs ksplit 1 and a plan that stages x from registers (few rows)
-   * or through the normalisation pre-pass (QDEC_EUNSUPPORTED otherwise). */
+  /* NORM_IN (with or without GLU): the residual x still owes a RES_OUT
+   * update held in k-split partials x_parts[j][rows][k], j < x_nparts
+   * (1..8).  The call first forms x = bf16(x + bf16(((p0 + p1) + p2) + ...))
+   * per element -- the rounding a RES_OUT call applies -- uses it as its
+   * input and writes it to x_merged ([rows, k] bf16, not x itself: other
+   * workgroups of the call still read x).  Needs ksplit 1 and a plan that
+   * stages x from registers (one row, without GLU) or through the
+   * normalisation pre-pass (QDEC_EUNSUPPORTED otherwise). */
   const float *x_parts;
   int32_t x_nparts;
   void *x_merged;

@@ -177,6 +177,22 @@ def test_gemm_resident_split_validation(qlib, kw, needle):
     assert qlib.gemm_workspace(_gemm(**DS_RES)) == (0, 0)
 
 
+def test_gemm_glu_takes_pending_split_update():
+    """gate/up merges a split O projection's partials (x_parts) in its
+    normalisation pre-pass: accepted wherever its plan has one, resident or
+    not; the resident 6..8-row plan (no pre-pass) refuses them."""
+    from qdec import capi as c
+    lib = c.lib()
+    gu = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4, x_parts=16, x_nparts=2, x_merged=32)
+    for rows in (1, 4, 8, 17, 32):
+        lib.gemm_workspace(_gemm(rows=rows, **gu))
+    for rows in (17, 24, 32):
+        lib.gemm_workspace(_gemm(rows=rows, resident=1, **gu))
+        assert lib.gemm_prepass(_gemm(rows=rows, resident=1, **gu))[0]
+    with pytest.raises(capi.QdecError, match="resident with x_parts"):
+        lib.gemm_workspace(_gemm(rows=8, resident=1, **gu))
+
+
 def test_gemm_resident_res_out_needs_no_workspace(qlib):
     for rows in (1, 2, 5, 8):
         assert qlib.gemm_workspace(_gemm(**dict(DN_RES, rows=rows))) == (0, 0)

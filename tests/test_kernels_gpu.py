@@ -547,6 +547,41 @@ def test_down_split_parts_in_lds_bitexact(lib, rows):
     assert (got - ref).abs().max().item() <= 0.02 * ref.abs().max().item()
 
 
+@pytest.mark.parametrize("rows,resident", [(5, 0), (24, 0), (24, 1), (32, 1)])
+def test_glu_merges_split_update_bitexact(lib, rows, resident):
+    """gate/up with a pending split residual update (x_parts: a split O
+    projection's partials) merges it in its pre-pass: x_merged holds
+    bf16(x + bf16(p0 + p1)) and the output has the bits of the same call on
+    the merged rows."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    ks, waves, _ = role_plan(I, H, "gate_up")
+    x = rnd(rows, H, scale=2.0, seed=111 + rows)
+    parts = (torch.randn(2, rows, H, generator=torch.Generator().manual_seed(112)) * 0.5).float()
+    W = rnd(2 * I, H, scale=0.02, seed=113)
+    nw = bf16(1 + 0.2 * torch.randn(H, generator=torch.Generator().manual_seed(114))).to(torch.bfloat16)
+    merged_ref = bf16(x.float() + bf16(parts[0] + parts[1])).to(torch.bfloat16)
+    xd, pd, Wt, nwd = x.to(DEV), parts.to(DEV), pack(lib, W.to(DEV)), nw.to(DEV)
+    g = Gemm(lib, capi.NORM_IN | capi.GLU, I, H, ksplit=ks, waves=waves)
+    outs = []
+    for with_parts in (True, False):
+        out = torch.zeros(((rows + 15) // 16 * 16, I), dtype=torch.bfloat16, device=DEV)
+        merged = torch.full((rows, H), float("nan"), dtype=torch.bfloat16, device=DEV)
+        src = xd if with_parts else merged_ref.to(DEV)
+        a = capi.GemmArgs(x=src.data_ptr(), w=Wt.data_ptr(), out=out.data_ptr(), norm_w=nwd.data_ptr(), eps=1e-6,
+                          rows=rows, n=I, k=H, flags=capi.NORM_IN | capi.GLU, ksplit=ks, waves=waves,
+                          tiles_per_wg=1, resident=resident, partial=g.partial.data_ptr(),
+                          counters=g.counters.data_ptr())
+        if with_parts:
+            a.x_parts, a.x_nparts, a.x_merged = pd.data_ptr(), 2, merged.data_ptr()
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        if with_parts:
+            assert torch.equal(merged.cpu().view(torch.int16), merged_ref.view(torch.int16))
+        outs.append(out[:rows].cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 def attn_oracle(c, B, T):
     qkv = c["qkv"].float().view(B, T, NQ + 2 * NKV, D)
     kc, vc = c["kc"].float().clone(), c["vc"].float().clone()
@@ -794,7 +829,8 @@ def test_two_tiles_per_wave_bitexact(lib, role, rows):
                       "gate_up": (I, H, capi.NORM_IN | capi.GLU, "gate_up"), "down": (H, I, capi.RES_OUT, "down"),
                       "down_split": (H, I, capi.RES_OUT, "down"), "lm": (V, H, capi.NORM_IN | capi.ARGMAX, "lm")}[role]
     ks, waves, _ = role_plan(n, k, r, batch=1 if role == "down" else 32)
-    assert (ks > 1) == (role == "down_split")
+    # at batch 32 the down and O projections split k (partials to parts_out)
+    assert (ks > 1) == (role in ("down_split", "o"))
     seed = (zlib.crc32(role.encode()) + 5 * rows) % 1000
     mt_rows = (rows + 15) // 16 * 16
     frag = role in ("o", "down", "down_split")
@@ -845,7 +881,7 @@ def test_two_tiles_per_wave_bitexact(lib, role, rows):
         elif t1.dtype == torch.float32:
             t1, t2 = t1.view(torch.int32), t2.view(torch.int32)
         assert torch.equal(t1, t2)
-    if role == "down_split":
+    if role in ("down_split", "o"):
         assert not torch.isnan(two[1]).any()  # every partial written
 
 
