@@ -179,20 +179,23 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     // One workgroup per CU normalising the rows into LDS (gemm_resident.hip);
     // its arithmetic is that of the plan below (pre-pass + direct path).
     if (a->resident != 1) return set_error(QDEC_EINVAL, "qdec_gemm: resident %d not 0 or 1", a->resident);
-    if (f != (QDEC_NORM_IN | QDEC_GLU) || a->ksplit != 1 || a->waves != 4 || a->tiles_per_wg != 1 || a->x_frag ||
-        xa || a->next_norm_w)
-      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs NORM_IN | GLU, ksplit 1, 4 waves, one tile per "
-                       "workgroup and row-major x (no x_frag, x_attn or next_norm_w)");
-    const bool two = a->rows >= kResMinRows2 && a->rows <= kResMaxRows2;
+    if ((f != (QDEC_NORM_IN | QDEC_GLU) && f != QDEC_NORM_IN) || a->ksplit != 1 || a->waves != 4 ||
+        a->tiles_per_wg != 1 || a->x_frag || xa || a->next_norm_w)
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs NORM_IN (with or without GLU), ksplit 1, 4 waves, "
+                       "one tile per workgroup and row-major x (no x_frag, x_attn or next_norm_w)");
+    const bool two = glu && a->rows >= kResMinRows2 && a->rows <= kResMaxRows2;
     if (!two && (a->rows < kResMinRows || a->rows > kResMaxRows))
-      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d or %d..%d rows, not %d", kResMinRows,
-                       kResMaxRows, kResMinRows2, kResMaxRows2, a->rows);
-    if (KS > kResMaxKSteps || p->ksw % kResRing)
+      return glu ? set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d or %d..%d rows, not %d", kResMinRows,
+                             kResMaxRows, kResMinRows2, kResMaxRows2, a->rows)
+                 : set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident NORM_IN takes %d..%d rows, not %d", kResMinRows,
+                             kResMaxRows, a->rows);
+    const int ring = glu ? kResRing : kResRing1;
+    if (KS > kResMaxKSteps || p->ksw % ring)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs k <= %d with k/128 a multiple of %d (k %d)",
-                       kResMaxKSteps * 32, kResRing, a->k);
-    if (ntiles < 2) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs at least two tile pairs");
-    p->resident = 1;
-    p->rw = kResRing;
+                       kResMaxKSteps * 32, ring, a->k);
+    if (ntiles < 2) return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs at least two output tiles");
+    p->resident = glu ? 1 : 4;
+    p->rw = ring;
     p->kp = 0;
     p->npass = 0;
     p->lds_bytes = 0;  // static LDS

@@ -29,6 +29,10 @@
 // 24.0 for the pre-pass and the direct call, and batch-8 decode 2.912 ->
 // 2.797 ms per step (config 3, same box).
 //
+// NORM_IN alone (the QKV projection) runs the same kernel with GLU = false:
+// single output tiles in place of the pairs, one or two per workgroup, and
+// the plain bf16 epilogue (QKV at 8 rows: 11.5 -> 8.7 us per launch).
+//
 // Reference behaviour replaced: the NORM_IN + GLU path of
 // engine/kernels/fused.py:33-172 (_gemv_kernel with the RMSNorm prologue and
 // the SiLU-gated epilogue).
@@ -72,10 +76,13 @@ __device__ __forceinline__ void res_signal(uint32_t *flag) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-template <int RW>
-__global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident_kernel(const GemmParams p) {
+// GLU: (gate, up) tile pairs and the SwiGLU epilogue; otherwise single
+// tiles (NORM_IN alone: QKV) and a bf16 store.
+template <int RW, bool GLU>
+__global__ void __launch_bounds__(64 * 4 * (GLU ? kResMaxPairs : kResMaxTiles1)) glu_resident_kernel(const GemmParams p) {
+  constexpr int NA = GLU ? 2 : 1;
   __shared__ __align__(16) uint4 s_x[kResMaxKSteps * 64];                  // [k step][slot]
-  __shared__ __align__(16) float4 s_red[kResMaxPairs * 3 * 2 * 64];       // [pair][wave 1..3][gate, up][lane]
+  __shared__ __align__(16) float4 s_red[kResMaxPairs * 3 * NA * 64];      // [unit][wave 1..3][gate, up][lane]
   __shared__ float s_part[kResMaxRows * 4];                               // [row][virtual wave]
   // Arrivals of the four normalising waves: [0] row loads issued, [1]
   // statistic partials written, [2] rows normalised into s_x.
@@ -85,7 +92,7 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident_kernel(con
   const int nw = p.res_waves;  // blockDim.x / 64, from the kernel arguments (a scalar load)
   const int rows = p.rows, k = p.k, KS = p.KS, ksw = p.ksw;
   const int col = lane & 15, grp = lane >> 4;
-  const unsigned P = (unsigned)p.n >> 4;  // tile pairs
+  const unsigned P = (unsigned)p.n >> 4;  // units: tile pairs (GLU) or tiles
   const unsigned pair0 = blockIdx.x * P / gridDim.x;
   const int npairs = (int)((blockIdx.x + 1) * P / gridDim.x - pair0);
   const int j = wave >> 2, q = wave & 3;  // pair within the workgroup, k quarter
@@ -98,13 +105,13 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident_kernel(con
   const size_t up_off = (size_t)p.up_tiles * KS * 64;
   const int ksw_w = active ? ksw : 0;
   const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + lane;
-  uint4 wg[RW], wu[RW];
+  uint4 wg[RW], wu[GLU ? RW : 1];
   // The first RW k steps of this wave's range.
   auto issue_ring = [&]() {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       wg[r] = ldw(wq + r * 64);
-      wu[r] = ldw(wq + r * 64 + up_off);
+      if constexpr (GLU) wu[r] = ldw(wq + r * 64 + up_off);
     }
   };
 
@@ -196,16 +203,16 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident_kernel(con
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       ag = mfma16x16x32(wg[r], bq[r], ag);
-      au = mfma16x16x32(wu[r], bq[r], au);
+      if constexpr (GLU) au = mfma16x16x32(wu[r], bq[r], au);
       if (refill) {
         wg[r] = ldw(qn + r * 64);
-        wu[r] = ldw(qn + r * 64 + up_off);
+        if constexpr (GLU) wu[r] = ldw(qn + r * 64 + up_off);
       }
     }
   }
   if (active && q > 0) {
-    s_red[((j * 3 + q - 1) * 2 + 0) * 64 + lane] = make_float4(ag[0], ag[1], ag[2], ag[3]);
-    s_red[((j * 3 + q - 1) * 2 + 1) * 64 + lane] = make_float4(au[0], au[1], au[2], au[3]);
+    s_red[((j * 3 + q - 1) * NA + 0) * 64 + lane] = make_float4(ag[0], ag[1], ag[2], ag[3]);
+    if constexpr (GLU) s_red[((j * 3 + q - 1) * NA + 1) * 64 + lane] = make_float4(au[0], au[1], au[2], au[3]);
   }
   __syncthreads();
   if (!active || q != 0) return;
@@ -214,25 +221,32 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident_kernel(con
   // epilogue).
 #pragma unroll
   for (int w2 = 1; w2 < 4; ++w2) {
-    const float4 rg = s_red[((j * 3 + w2 - 1) * 2 + 0) * 64 + lane];
-    const float4 ru = s_red[((j * 3 + w2 - 1) * 2 + 1) * 64 + lane];
+    const float4 rg = s_red[((j * 3 + w2 - 1) * NA + 0) * 64 + lane];
     ag[0] += rg.x; ag[1] += rg.y; ag[2] += rg.z; ag[3] += rg.w;
-    au[0] += ru.x; au[1] += ru.y; au[2] += ru.z; au[3] += ru.w;
+    if constexpr (GLU) {
+      const float4 ru = s_red[((j * 3 + w2 - 1) * NA + 1) * 64 + lane];
+      au[0] += ru.x; au[1] += ru.y; au[2] += ru.z; au[3] += ru.w;
+    }
   }
   const int m = col;
   if (m >= rows) return;
   const int n0 = tile * 16 + grp * 4;
-  float o4[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float g = rbf(ag[i]);
-    const float u = rbf(au[i]);
-    const float sg = rbf(g / (1.0f + expf(-g)));
-    o4[i] = sg * u;
-  }
   uint2 o;
-  o.x = pack2(o4[0], o4[1]);
-  o.y = pack2(o4[2], o4[3]);
+  if constexpr (GLU) {
+    float o4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float g = rbf(ag[i]);
+      const float u = rbf(au[i]);
+      const float sg = rbf(g / (1.0f + expf(-g)));
+      o4[i] = sg * u;
+    }
+    o.x = pack2(o4[0], o4[1]);
+    o.y = pack2(o4[2], o4[3]);
+  } else {
+    o.x = pack2(ag[0], ag[1]);
+    o.y = pack2(ag[2], ag[3]);
+  }
   uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
   *reinterpret_cast<uint2 *>(p.ofrag ? out + frag_off(m, n0, p.ofrag) : out + (size_t)m * p.n + n0) = o;
 }
@@ -618,22 +632,30 @@ hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
   if (e != hipSuccess) return e;
   e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess) return e;
+  const bool glu = p.resident == 1;  // otherwise NORM_IN alone (4)
   const int P = p.n / 16;
-  // One workgroup per CU with two or three tile pairs each: more workgroups
-  // than CUs for a matrix past kResMaxPairs per CU, fewer for one below two.
-  const int grid = std::max((P + kResMaxPairs - 1) / kResMaxPairs, std::min(ncu, P / 2));
+  // One workgroup per CU with two or three tile pairs each (GLU), or one or
+  // more single tiles: more workgroups than CUs for a matrix past
+  // kResMaxPairs units per CU, fewer for one below two pairs (one tile).
+  const int umax = glu ? kResMaxPairs : kResMaxTiles1;
+  const int grid = std::max((P + umax - 1) / umax, std::min(ncu, glu ? P / 2 : P));
   if (grid < 1) return hipErrorInvalidValue;
   const int pairs = (P + grid - 1) / grid;
-  if (pairs > kResMaxPairs || p.rw != kResRing || p.ksw % kResRing) return hipErrorInvalidValue;
+  if (pairs > umax || (p.rw != kResRing && p.rw != kResRing1) || p.ksw % p.rw) return hipErrorInvalidValue;
   GemmParams q = p;
   q.res_waves = 4 * pairs;
   if (p.rows <= kResMaxRows) {
     // The last four waves normalise the rows, so the others are at least one
     // pair's.
     if (pairs < 2) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((glu_resident_kernel<kResRing>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+    if (glu && p.rw == kResRing)
+      hipLaunchKernelGGL((glu_resident_kernel<kResRing, true>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+    else if (!glu && p.rw == kResRing1)
+      hipLaunchKernelGGL((glu_resident_kernel<kResRing1, false>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+    else
+      return hipErrorInvalidValue;
   } else {
-    if (p.rows > 32 || !p.xn || p.KS > kResMaxKSteps) return hipErrorInvalidValue;
+    if (!glu || p.rows > 32 || !p.xn || p.KS > kResMaxKSteps) return hipErrorInvalidValue;
     hipLaunchKernelGGL((glu_resident2_kernel<kResRing>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
   }
   return hipSuccess;

@@ -28,7 +28,8 @@ constexpr int kArgSlots = 16;
 // kResMaxRows rows normalised by the workgroup itself, kResMinRows2..
 // kResMaxRows2 rows (two M tiles) normalised by the pre-pass and copied in;
 // at most kResMaxPairs tile pairs (4 waves each) per workgroup and
-// kResMaxKSteps k steps (k <= 2560).
+// kResMaxKSteps k steps (k <= 2560).  NORM_IN alone (QKV) takes the first
+// kind with single tiles in place of the pairs.
 constexpr int kResMinRows = 6;
 constexpr int kResMaxRows = 8;
 constexpr int kResMinRows2 = 17;
@@ -36,6 +37,8 @@ constexpr int kResMaxRows2 = 32;
 constexpr int kResMaxPairs = 3;
 constexpr int kResMaxKSteps = 80;
 constexpr int kResRing = 10;  // weight ring slots (gate|up block pairs) per wave
+constexpr int kResRing1 = 20;  // weight ring slots per wave without GLU (NORM_IN alone)
+constexpr int kResMaxTiles1 = 2;  // tiles per workgroup without GLU
 // RES_OUT with its rows staged in LDS by DMA (gemm_resident.hip): 2..
 // kResLdsRows rows, at most kResLdsKSteps k steps (8 rows x 64 bytes each),
 // kResLdsRing weight blocks in flight per wave.
@@ -100,7 +103,7 @@ struct GemmParams {
   int hthreads, hxt;
   uint32_t *hsync;
   int resident;  // gemm_resident.hip: 1 NORM_IN | GLU with the normalised rows in LDS, 2 RES_OUT with the rows in LDS,
-                 // 3 RES_OUT split into k parts, each part's rows in LDS
+                 // 3 RES_OUT split into k parts, each part's rows in LDS, 4 NORM_IN alone as 1
   int res_waves;  // resident: waves per workgroup (set by the launcher)
   size_t lds_bytes;
 };

@@ -124,6 +124,11 @@ RESIDENT_RES_ROWS = (1, 8)
 # batch 32 at 4096-token prompts 5.635 -> 5.551, batch 20 at 1024 3.393 ->
 # 3.311; down 15.1 -> 12.7 us per launch).
 RESIDENT_SPLIT_ROWS = (17, 32)
+# QKV (NORM_IN alone) at these rows takes gate/up's resident plan with single
+# tiles: the workgroup normalises its rows into LDS itself.  Same-box A/B at
+# batch 8 and 1024-token prompts: QKV 11.5 -> 8.7 us per launch, 2.651 ->
+# 2.549 ms per step, the same tokens.
+RESIDENT_QKV_ROWS = (6, 8)
 
 
 def round_up(x, m):
@@ -531,6 +536,8 @@ class DecodeState:
             return False
         if role == "gate_up":
             ok = not a.x_frag and any(lo <= a.rows <= hi for lo, hi in RESIDENT_ROWS)
+        elif role == "qkv":
+            ok = not a.x_frag and not a.x_parts and RESIDENT_QKV_ROWS[0] <= a.rows <= RESIDENT_QKV_ROWS[1]
         elif role not in RESIDENT_RES_ROLES:
             ok = False
         elif a.parts_out:
@@ -666,7 +673,7 @@ class DecodeState:
         if hasattr(self, "gemm_partial"):
             a.partial = self.gemm_partial.data_ptr()
             a.counters = self.gemm_counters.data_ptr()
-        if role in ("gate_up",) + RESIDENT_RES_ROLES:
+        if role in ("gate_up", "qkv") + RESIDENT_RES_ROLES:
             a.resident = 1 if self._resident(a, role) else 0
         if hand:
             L = c.n_layers

@@ -118,7 +118,7 @@ GU_RES = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4, rows=8, re
 
 @pytest.mark.parametrize("kw,code,needle", [
     (dict(resident=2), -1, "resident 2"),
-    (dict(flags=capi.NORM_IN), -3, "NORM_IN | GLU"),
+    (dict(flags=capi.GLU, x_frag=1, out_frag=1), -3, "NORM_IN (with or without GLU)"),
     (dict(ksplit=2), -3, "ksplit 1"),
     (dict(waves=8), -3, "4 waves"),
     (dict(tiles_per_wg=2), -3, "one tile"),
@@ -127,9 +127,13 @@ GU_RES = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4, rows=8, re
     (dict(rows=9), -3, "6..8 or 17..32 rows"),
     (dict(rows=16), -3, "6..8 or 17..32 rows"),
     (dict(rows=33), -3, "6..8 or 17..32 rows"),
-    (dict(n=16), -3, "two tile pairs"),
+    (dict(n=16), -3, "two output tiles"),
     (dict(k=4096), -3, "k <= 2560"),
     (dict(k=1024), -3, "multiple of 10"),
+    (dict(flags=capi.NORM_IN, n=6144, rows=5), -3, "NORM_IN takes 6..8 rows"),
+    (dict(flags=capi.NORM_IN, n=6144, rows=17), -3, "NORM_IN takes 6..8 rows"),
+    (dict(flags=capi.NORM_IN, n=6144, k=1280), -3, "multiple of 20"),
+    (dict(flags=capi.NORM_IN, n=16), -3, "two output tiles"),
 ])
 def test_gemm_resident_validation(qlib, kw, code, needle):
     """The resident gate/up plan takes exactly the shapes its kernel was
@@ -206,6 +210,10 @@ def test_gemm_resident_workspace_and_prepass(qlib):
         assert qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows))) == (0, 0)
         assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows))) == (False, 256)
         assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows, resident=0))) == (True, 256)
+        # QKV (NORM_IN alone) likewise
+        qkv = dict(GU_RES, flags=capi.NORM_IN, n=6144, rows=rows)
+        assert qlib.gemm_workspace(_gemm(**qkv)) == (0, 0)
+        assert qlib.gemm_prepass(_gemm(**qkv)) == (False, 256)
     for rows in (17, 32):
         ws = qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows)))
         assert ws == qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows, resident=0)))

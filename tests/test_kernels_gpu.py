@@ -485,6 +485,40 @@ def test_glu_resident_bitexact(lib, rows, frag):
     agree(outs[1], silu_mul(linear(xin, W[:I].float()), linear(xin, W[I:].float())), min_exact=0.97)
 
 
+@pytest.mark.parametrize("frag", [0, 1])
+@pytest.mark.parametrize("rows", [6, 7, 8])
+def test_qkv_resident_bitexact(lib, rows, frag):
+    """QKV (NORM_IN alone) on the resident plan with single tiles -- the
+    workgroup normalises its rows into LDS itself, 1 or 2 tiles per
+    workgroup -- gives the bits of the plain call, in row-major and
+    fragment-order output, and agrees with the oracle."""
+    from qdec import capi
+    from qdec.runtime import role_plan
+    n = 6144
+    ks, waves, _ = role_plan(n, H, "qkv", batch=rows)
+    x = rnd(rows, H, scale=3.0, seed=80 + rows)
+    x[0] = (x[0].float() * 40.0).to(torch.bfloat16)
+    x[rows - 1] = (x[rows - 1].float() * 0.01).to(torch.bfloat16)
+    W = rnd(n, H, scale=0.02, seed=81)
+    nw = bf16(1 + 0.2 * torch.randn(H, generator=torch.Generator().manual_seed(82))).to(torch.bfloat16)
+    xd, Wt, nwd = x.to(DEV), pack(lib, W.to(DEV)), nw.to(DEV)
+    g = Gemm(lib, capi.NORM_IN, n, H, ksplit=ks, waves=waves)
+    outs = []
+    for resident in (0, 1):
+        out = torch.full(((rows + 15) // 16 * 16, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+        a = capi.GemmArgs(x=xd.data_ptr(), w=Wt.data_ptr(), out=out.data_ptr(), norm_w=nwd.data_ptr(), eps=1e-6,
+                          rows=rows, n=n, k=H, flags=capi.NORM_IN, ksplit=ks, waves=waves, tiles_per_wg=1,
+                          out_frag=frag, resident=resident, partial=g.partial.data_ptr(),
+                          counters=g.counters.data_ptr())
+        if resident:
+            assert lib.gemm_workspace(a)[0] == 0 and not lib.gemm_prepass(a)[0]
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        outs.append(frag_to_rows(out, rows, n).cpu() if frag else out[:rows].cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    agree(outs[1], linear(rms_norm(x.float(), nw.float(), 1e-6), W.float()), min_exact=0.97)
+
+
 @pytest.mark.parametrize("role,rows", [("down", 1), ("down", 2), ("down", 3), ("down", 5), ("down", 8), ("o", 1),
                                       ("o", 3), ("o", 4), ("o", 8)])
 def test_res_out_rows_in_lds_bitexact(lib, role, rows):
