@@ -327,6 +327,7 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
     p->a_chunk = xa->chunk;
     p->a_nchunks = (xa->cap + xa->chunk - 1) / xa->chunk;
     p->a_cap = xa->cap;
+    p->a_strided = xa->strided;
   }
   size_t pb = 0, cb = 0, xn_off = 0;
   gemm_scratch(a, *p, &pb, &cb, &xn_off);
@@ -398,6 +399,9 @@ static int plan_attn(const qdec_attn_args *a, AttnParams *p, bool need_scratch) 
   if (a->out_partials != 0 && a->out_partials != 1)
     return set_error(QDEC_EINVAL, "qdec_attn: out_partials %d not 0 or 1", a->out_partials);
   if (a->out_frag != 0 && a->out_frag != 1) return set_error(QDEC_EINVAL, "qdec_attn: out_frag %d not 0 or 1", a->out_frag);
+  if (a->strided != 0 && a->strided != 1) return set_error(QDEC_EINVAL, "qdec_attn: strided %d not 0 or 1", a->strided);
+  if (a->strided && a->waves != 8)
+    return set_error(QDEC_EUNSUPPORTED, "qdec_attn: strided chunks run 8 waves (waves %d)", a->waves);
   const int nchunks = (a->cap + a->chunk - 1) / a->chunk;
   if (!need_scratch) goto fill;
   if (!a->qkv || !a->q_norm_w || !a->k_norm_w || !a->cos_tab || !a->sin_tab || !a->lens || !a->k_cache ||
@@ -421,6 +425,7 @@ fill:
   p->out_partials = a->out_partials;
   p->ofrag = (a->out_frag && !a->out_partials) ? (a->batch * a->t_rows + 15) / 16 : 0;
   p->head_dim = a->head_dim;
+  p->strided = a->strided;
   return QDEC_OK;
 }
 

@@ -16,10 +16,10 @@ namespace {
 
 // Up to 32 query rows per kv head the body fits 256 registers without
 // spills: two 4-wave workgroups per CU, or one of 8 waves.
-template <int D, int GQ, int MTQ, int NW>
+template <int D, int GQ, int MTQ, int NW, bool STR = false>
 __global__ void __launch_bounds__(64 * NW, NW == 4 && MTQ <= 2 ? 2 : 1) attn_kernel(const AttnParams p) {
   __shared__ __align__(16) unsigned char smem[AttnLds<NW>::bytes];
-  attn_block<D, GQ, MTQ, NW>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+  attn_block<D, GQ, MTQ, NW, false, STR>(p, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }
 
 }  // namespace
@@ -27,13 +27,16 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MTQ <= 2 ? 2 : 1) attn_ker
 template <int GQ>
 hipError_t launch_attn_g(const AttnParams &p, int mtq, dim3 grid, dim3 block, hipStream_t s) {
   if (p.waves == 8) {
-    switch (mtq) {
-      case 1: hipLaunchKernelGGL((attn_kernel<128, GQ, 1, 8>), grid, block, 0, s, p); break;
-      case 2: hipLaunchKernelGGL((attn_kernel<128, GQ, 2, 8>), grid, block, 0, s, p); break;
+    switch (mtq * 2 + (p.strided ? 1 : 0)) {
+      case 2: hipLaunchKernelGGL((attn_kernel<128, GQ, 1, 8>), grid, block, 0, s, p); break;
+      case 3: hipLaunchKernelGGL((attn_kernel<128, GQ, 1, 8, true>), grid, block, 0, s, p); break;
+      case 4: hipLaunchKernelGGL((attn_kernel<128, GQ, 2, 8>), grid, block, 0, s, p); break;
+      case 5: hipLaunchKernelGGL((attn_kernel<128, GQ, 2, 8, true>), grid, block, 0, s, p); break;
       default: return hipErrorInvalidValue;
     }
     return hipSuccess;
   }
+  if (p.strided) return hipErrorInvalidValue;  // strided chunks run 8 waves
   switch (mtq) {
     case 1: hipLaunchKernelGGL((attn_kernel<128, GQ, 1, 4>), grid, block, 0, s, p); break;
     case 2: hipLaunchKernelGGL((attn_kernel<128, GQ, 2, 4>), grid, block, 0, s, p); break;

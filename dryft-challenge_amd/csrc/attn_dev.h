@@ -3,18 +3,21 @@
 //
 // Grid (chunk, kv head, sequence); a workgroup of NW = 4 or 8 wavefronts per
 // cell (the wave count, like the chunk, is part of the call: a row's
-// arithmetic depends on both, never on t_rows).
-//   1. Every wave issues the K/V loads of its first 32-slot block (of its
-//      first two in chunk 0; a later chunk issues the second once the length
-//      says the chunk needs it), then the raw loads of its share of the query
-//      rows (row r = G*t + g goes to wave r % NW) and of the new key/value
-//      rows (t % NW), all before the sequence length arrives (no address
-//      depends on it); a lane holds two
+// arithmetic depends on both, never on t_rows).  A chunk is a contiguous
+// slot range, or (strided, 8 waves) every C-th 32-slot block of the cache.
+//   1. Query row r = G*t + g and new key/value row t go to the wave whose
+//      row index rw (wave + 4 mod 8 with 8 waves, else the wave) is r or t
+//      mod NW.  A wave holding rows loads them, and a lane holds two
 //      channels of a row, so the head RMSNorm is one wave reduction and the
 //      rotate_half partner sits in lane ^ 32.  Normalised, rotated queries
 //      go to LDS; new keys go to LDS in row layout, new values in the
 //      channel-major cache layout, and the chunk owning a new slot writes it
 //      to the cache (nobody reads those cache slots in this launch).
+//      K/V blocks: a wave issues its first 32-slot block before the sequence
+//      length arrives (its first two in contiguous chunk 0) and a second one
+//      once the length says the chunk needs it -- except, with fewer query
+//      rows than waves (plain decode at 8 waves), the waves holding rows,
+//      which prepare them first and then issue their blocks.
 //   2. Each wave reads the queries back in the B-operand layout of
 //      v_mfma_f32_16x16x32_bf16 (query row r sits in MFMA column r % 16 of M
 //      tile r / 16) and walks its blocks (block j to wave j % NW, two blocks in
@@ -64,7 +67,8 @@ struct AttnLds {
 // GQ: query heads per kv head, 4 (Qwen3-4B and -8B) or 0 for the group
 // size of the call (nq / nkv: 2 for Qwen3-0.6B and -1.7B, 5 for -14B, 8 for
 // -32B), with at most 16 * MTQ query rows per kv head.
-template <int D, int GQ, int MTQ, int NW, bool COH = false>
+// STR: strided chunks (the call's strided flag, as a constant).
+template <int D, int GQ, int MTQ, int NW, bool COH = false, bool STR = false>
 __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, const int kvh, const int b,
                                            unsigned char *smem) {
   static_assert((D == 128 && (GQ == 4 || GQ == 0)) || (D == 64 && GQ == 0),
@@ -100,8 +104,15 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   const bool lv = lane < LH;
   const int T = p.t_rows;
   const int R = T * G;
-  const int c0 = c * p.chunk;
-  const int c1 = c0 + p.chunk;  // exclusive end of this chunk
+  // Chunk c takes the contiguous slots [c0, c1), or with strided chunks the
+  // 32-slot blocks c, c + C, c + 2C, ... of the cache (C = p.nchunks): then
+  // every chunk of a partly filled cache has the same number of blocks, give
+  // or take one.  Local block j of the chunk starts at slot bs0(j).
+  const int C = p.nchunks;
+  constexpr bool strided = STR;
+  const int c0 = strided ? 32 * c : c * p.chunk;
+  const int c1 = c0 + p.chunk;  // exclusive end of a contiguous chunk
+  auto bs0 = [&](int j) { return strided ? 32 * (c + C * j) : c0 + 32 * j; };
   const int nq = p.nq, nkv = p.nkv;
   const int width = (nq + 2 * nkv) * D;
   const uint16_t *qkv = reinterpret_cast<const uint16_t *>(p.qkv);
@@ -138,29 +149,58 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   // newest slots is usually part-filled, and the one after it empty
   // (MI355X, ms per step: batch 8 at 1300 tokens 2.987 -> 2.963, batch 4 at
   // 1024 2.486 -> 2.464).
-  auto block_in = [&](int j) { return 32 * j < p.chunk && c0 + 32 * (j + 1) <= p.cap; };
+  //
+  // Rows go to waves by rw: with 8 waves the query rows and new key rows
+  // start at wave 4, whose blocks (4..7 mod 8) are a chunk's last to get a
+  // second one.  With fewer query rows than waves (a plain step at 8 waves)
+  // the waves holding rows load and prepare them first and only then issue
+  // their blocks: a wave that has issued its block loads stalls in that
+  // issue until the memory pipeline drains (measured on MI355X), and the
+  // rows would wait with it.  The other waves issue their blocks first.
+  const int rw = NW == 8 ? (wave + 4) & 7 : wave;
+  const bool late = R < NW && rw < R;
+  auto block_in = [&](int j) { return (strided || 32 * j < p.chunk) && bs0(j) + 32 <= p.cap; };
   Frag f0, f1;
-  if (block_in(wave)) load_block(c0 + 32 * wave, f0);
-  if constexpr (DB) {
-    if (c == 0 && block_in(wave + NW)) load_block(c0 + 32 * (wave + NW), f1);
+  if (!late) {
+    if (block_in(wave)) load_block(bs0(wave), f0);
+    if constexpr (DB) {
+      if constexpr (!STR) {
+        if (c == 0 && block_in(wave + NW)) load_block(bs0(wave + NW), f1);
+      }
+    }
   }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // Only the waves holding rows load them (and their norm weights and
+  // rotation tables): an unused load still pending where its register is
+  // reused would make the wave wait for every load issued after it.
   uint32_t qraw[QPW], kraw[KPW], vraw[KPW];
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
-    const int r = min(wave + NW * i, R - 1);
-    const int t = r / G, hq = r % G;
-    qraw[i] = ldv4<COH>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + cl);
-    if (!lv) qraw[i] = 0u;
+    const int r = rw + NW * i;
+    qraw[i] = 0u;
+    if (r < R) {  // uniform per wave
+      const int t = r / G, hq = r % G;
+      qraw[i] = ldv4<COH>(qkv + (size_t)(b * T + t) * width + (size_t)(kvh * G + hq) * D + cl);
+      if (!lv) qraw[i] = 0u;
+    }
   }
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
-    const uint16_t *row = qkv + (size_t)(b * T + min(wave + NW * i, T - 1)) * width;
-    kraw[i] = ldv4<COH>(row + (size_t)(nq + kvh) * D + cl);
-    vraw[i] = ldv4<COH>(row + (size_t)(nq + nkv + kvh) * D + cl);
-    if (!lv) kraw[i] = 0u;
+    const int t = rw + NW * i;
+    kraw[i] = vraw[i] = 0u;
+    if (t < T) {
+      const uint16_t *row = qkv + (size_t)(b * T + t) * width;
+      kraw[i] = ldv4<COH>(row + (size_t)(nq + kvh) * D + cl);
+      vraw[i] = ldv4<COH>(row + (size_t)(nq + nkv + kvh) * D + cl);
+      if (!lv) kraw[i] = 0u;
+    }
   }
-  const uint32_t qw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + cl);
-  const uint32_t kw = *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + cl);
+  const bool has_q = rw < R, has_k = rw < T;
+  const uint32_t qw =
+      has_q ? *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.q_norm_w) + cl) : 0u;
+  const uint32_t kw =
+      has_k ? *reinterpret_cast<const uint32_t *>(reinterpret_cast<const uint16_t *>(p.k_norm_w) + cl) : 0u;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
   const int L = p.lens[b];
   const int last = L + T - 1;
@@ -180,26 +220,34 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
     }
     return;
   }
-  if (c0 > last) return;
-  const int n_active = last / p.chunk + 1;
-  const int nb = (min(c1, last + 1) - c0 + 31) / 32;  // blocks in this chunk
+  if (c0 > last) return;  // (strided: the chunk's first block lies past the last slot)
+  const int n_active = strided ? min(C, (last >> 5) + 1) : last / p.chunk + 1;
+  const int nb = strided ? ((last >> 5) - c) / C + 1 : (min(c1, last + 1) - c0 + 31) / 32;  // blocks in this chunk
   if constexpr (DB) {
-    if (c > 0 && wave + NW < nb) load_block(c0 + 32 * (wave + NW), f1);
+    if (!late && (c > 0 || strided) && wave + NW < nb) load_block(bs0(wave + NW), f1);
   }
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
   // ---- 1. rotation tables of the rows' positions.
-  const bool overlap = c1 > L;  // this chunk holds some of the new slots
+  // this chunk holds some of the new slots L..last (blocks L/32 .. last/32)
+  const bool overlap = strided ? ((last >> 5) - (L >> 5) + 1 >= C || (c - (L >> 5) % C + C) % C <= (last >> 5) - (L >> 5))
+                               : c1 > L;
   uint32_t qcos[QPW], qsin[QPW], kcos[KPW], ksin[KPW];
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
-    const int t = min(wave + NW * i, R - 1) / G;
-    qcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + cl);
-    qsin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + cl);
+    const int r = rw + NW * i;
+    qcos[i] = qsin[i] = 0u;
+    if (r < R) {
+      const int t = r / G;
+      qcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + cl);
+      qsin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + cl);
+    }
   }
-  if (overlap) {
 #pragma unroll
-    for (int i = 0; i < KPW; ++i) {
-      const int t = min(wave + NW * i, T - 1);
+  for (int i = 0; i < KPW; ++i) {
+    const int t = rw + NW * i;
+    kcos[i] = ksin[i] = 0u;
+    if (overlap && t < T) {
       kcos[i] = *reinterpret_cast<const uint32_t *>(cos_t + (size_t)(L + t) * D + cl);
       ksin[i] = *reinterpret_cast<const uint32_t *>(sin_t + (size_t)(L + t) * D + cl);
     }
@@ -211,37 +259,59 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   };
 #pragma unroll
   for (int i = 0; i < QPW; ++i) {
-    const int r = wave + NW * i;
+    const int r = rw + NW * i;
     if (r < R) {  // uniform per wave: the norm's wave sum runs on every lane
       const uint32_t qo = norm_rope(qraw[i], qw, qcos[i], qsin[i]);
       if (lv) *reinterpret_cast<uint32_t *>(s_q + r * RS + cl) = qo;
     }
   }
+  uint32_t kout[KPW];
   if (overlap) {
     const int g0 = L >> 3;
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
-      const int t = wave + NW * i;
+      const int t = rw + NW * i;
       if (t < T) {
-        const uint32_t kout = norm_rope(kraw[i], kw, kcos[i], ksin[i]);
+        kout[i] = norm_rope(kraw[i], kw, kcos[i], ksin[i]);
         const uint32_t vr = vraw[i];
         const int slot = L + t;
         const int gi = (slot >> 3) - g0, e = slot & 7;
         if (lv) {
-          *reinterpret_cast<uint32_t *>(s_kn + t * RS + cl) = kout;
+          *reinterpret_cast<uint32_t *>(s_kn + t * RS + cl) = kout[i];
           s_vp[(gi * D + cl) * 8 + e] = (uint16_t)(vr & 0xffffu);
           s_vp[(gi * D + cl + 1) * 8 + e] = (uint16_t)(vr >> 16);
-          if (slot >= c0 && slot < c1) {  // this chunk owns the slot
-            *reinterpret_cast<uint32_t *>(kc + (size_t)slot * D + cl) = kout;
-            uint16_t *vb = vc + ((size_t)(slot >> 3) * D) * 8 + e;
-            vb[(size_t)cl * 8] = (uint16_t)(vr & 0xffffu);
-            vb[(size_t)(cl + 1) * 8] = (uint16_t)(vr >> 16);
-          }
         }
       }
     }
   }
-  __syncthreads();
+  // The late waves' blocks go out before the cache write below (a pending
+  // store would hold them back).
+  if (late) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (wave < nb) load_block(bs0(wave), f0);
+    if constexpr (DB) {
+      if (wave + NW < nb) load_block(bs0(wave + NW), f1);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  }
+  // The chunk owning a new slot writes it to the cache (nobody reads those
+  // cache slots in this launch).
+  if (overlap) {
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int t = rw + NW * i;
+      const int slot = L + t;
+      if (t < T && lv && (strided ? (slot >> 5) % C == c : (slot >= c0 && slot < c1))) {
+        const uint32_t vr = vraw[i];
+        const int e = slot & 7;
+        *reinterpret_cast<uint32_t *>(kc + (size_t)slot * D + cl) = kout[i];
+        uint16_t *vb = vc + ((size_t)(slot >> 3) * D) * 8 + e;
+        vb[(size_t)cl * 8] = (uint16_t)(vr & 0xffffu);
+        vb[(size_t)(cl + 1) * 8] = (uint16_t)(vr >> 16);
+      }
+    }
+  }
+  lds_barrier();  // the rows are in LDS; the blocks may still be in flight
 
   // ---- 2. flash-decode over this wave's blocks.
   uint4 qf[MTQ][DS];
@@ -301,7 +371,7 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   };
 
   auto process = [&](Frag &f, int j) {
-    const int s0 = c0 + 32 * j;
+    const int s0 = bs0(j);
     if (s0 + 32 > L) patch(f, s0);  // block touches new or unwritten slots
 #pragma unroll
     for (int mt = 0; mt < MTQ; ++mt) {
@@ -347,15 +417,15 @@ __device__ __forceinline__ void attn_block(const AttnParams &p, const int c, con
   if constexpr (DB) {
     for (int j = wave; j < nb; j += 2 * NW) {
       process(f0, j);
-      if (j + 2 * NW < nb) load_block(c0 + 32 * (j + 2 * NW), f0);
+      if (j + 2 * NW < nb) load_block(bs0(j + 2 * NW), f0);
       if (j + NW < nb) {
         process(f1, j + NW);
-        if (j + 3 * NW < nb) load_block(c0 + 32 * (j + 3 * NW), f1);
+        if (j + 3 * NW < nb) load_block(bs0(j + 3 * NW), f1);
       }
     }
   } else {
     for (int j = wave; j < nb; j += NW) {
-      if (j != wave) load_block(c0 + 32 * j, f0);
+      if (j != wave) load_block(bs0(j), f0);
       process(f0, j);
     }
   }

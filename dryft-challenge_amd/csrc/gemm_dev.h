@@ -104,7 +104,7 @@ __device__ __forceinline__ uint4 attn_merge8(const GemmParams &p, int m, int kk)
   // a merge of stale partials; the NaN reaches the argmax, whose pick is
   // then an out-of-vocabulary id the host refuses.
   if (L < 0 || L + T - 1 >= p.a_cap) return make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u);
-  const int n_active = min((L + T - 1) / p.a_chunk + 1, p.a_nchunks);
+  const int n_active = min((p.a_strided ? (L + T - 1) >> 5 : (L + T - 1) / p.a_chunk) + 1, p.a_nchunks);
   const float NEG_INF = -__builtin_huge_valf();
   float mc[CB], lc[CB];
   f32x4_t a0[CB], a1[CB];

@@ -90,6 +90,16 @@ __device__ __forceinline__ uint4 ld_nt(const void *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Workgroup barrier for an LDS hand-over: waits for this wave's LDS
+// operations only (lgkmcnt 0), not for its outstanding global loads, which
+// the workgroup-scope release fence of __syncthreads() also drains.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Global loads that bypass caches which another XCD may hold stale, for data
 // written by other workgroups of the same grid (split partials).
 __device__ __forceinline__ float load_coherent(const float *p) {

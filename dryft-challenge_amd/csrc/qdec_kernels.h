@@ -85,7 +85,7 @@ struct GemmParams {
   int amerge;
   const float *apart;
   const int32_t *alens;
-  int a_t_rows, a_nkv, a_chunk, a_nchunks, a_cap;
+  int a_t_rows, a_nkv, a_chunk, a_nchunks, a_cap, a_strided;
   // Split residual updates: a RES_OUT producer writes its k-split partials
   // (parts_out); a NORM_IN consumer merges xnparts of them into x first
   // (xparts) and writes the merged residual rows to xmerged.
@@ -142,6 +142,7 @@ struct AttnParams {
   int out_partials;
   int ofrag;  // > 0: out is written in fragment order with this many M tiles
   int head_dim;  // 128, or 64 (four waves)
+  int strided;   // chunk c takes blocks c, c + nchunks, ... (else contiguous slots)
 };
 hipError_t launch_attn(const AttnParams &p, hipStream_t s);
 

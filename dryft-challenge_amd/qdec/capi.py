@@ -57,7 +57,7 @@ class AttnArgs(ctypes.Structure):
                 ("lens", P), ("k_cache", P), ("v_cache", P), ("out", P), ("partial", P),
                 ("counters", P), ("eps", F32), ("sm_scale", F32), ("batch", I32), ("t_rows", I32),
                 ("nq", I32), ("nkv", I32), ("head_dim", I32), ("cap", I32), ("chunk", I32),
-                ("waves", I32), ("out_partials", I32), ("out_frag", I32)]
+                ("waves", I32), ("out_partials", I32), ("out_frag", I32), ("strided", I32)]
 
 
 class LayerArgs(ctypes.Structure):

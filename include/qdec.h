@@ -318,6 +318,16 @@ typedef struct qdec_attn_args {
                            arguments merges them (no arrival pass) */
   int32_t out_frag;     /* 1: out in the fragment order of qdec_gemm_args
                            (rows = batch*t_rows, columns nq*head_dim) */
+  int32_t strided;      /* 0: chunk c holds slots [c*chunk, (c+1)*chunk).
+                           1: with C = ceil(cap / chunk) chunks, chunk c
+                           holds the 32-slot blocks c, c + C, c + 2C, ...,
+                           so a partly filled cache spreads evenly over the
+                           chunks.  Either way the dealing is keyed to
+                           absolute slots: a row's result depends on chunk,
+                           waves and strided, never on t_rows.  No
+                           counterpart in the reference, whose split
+                           attention takes contiguous ranges
+                           (engine/kernels/ops.py:219-431). */
 } qdec_attn_args;
 int qdec_attn(const qdec_attn_args *a, qdec_stream_t stream);
 int qdec_attn_workspace(const qdec_attn_args *a, size_t *partial_bytes,

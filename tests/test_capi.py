@@ -283,6 +283,7 @@ def _attn(**kw):
     (dict(nq=40, t_rows=13), -3),  # 5 per kv head: 65 > 64
     (dict(chunk=48), -1), (dict(waves=5), -1), (dict(waves=2), -1), (dict(out=None), -1), (dict(partial=None), -1), (dict(qkv=8), -2),
     (dict(waves=8, t_rows=9), -3),
+    (dict(strided=1), -3), (dict(strided=2, waves=8), -1),  # strided chunks run 8 waves; the flag is 0 or 1
 ])
 def test_attn_validation(qlib, kw, code):
     assert qlib.so.qdec_attn(ctypes.byref(_attn(**kw)), None) == code

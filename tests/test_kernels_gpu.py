@@ -270,7 +270,7 @@ def v_layout(v):
     return v.reshape(*lead, cap // 8, 8, d).transpose(-1, -2).contiguous()
 
 
-def attn_case(lib, B, T, lens, cap, chunk, seed, waves=4, out_frag=0, valid=True):
+def attn_case(lib, B, T, lens, cap, chunk, seed, waves=4, out_frag=0, valid=True, strided=0):
     from qdec import capi
     g = torch.Generator().manual_seed(seed)
     W = (NQ + 2 * NKV) * D
@@ -293,7 +293,7 @@ def attn_case(lib, B, T, lens, cap, chunk, seed, waves=4, out_frag=0, valid=True
     a.k_cache, a.v_cache, a.out = dk.data_ptr(), dv.data_ptr(), out.data_ptr()
     a.eps, a.sm_scale = 1e-6, D ** -0.5
     a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = B, T, NQ, NKV, D, cap, chunk
-    a.waves, a.out_frag = waves, out_frag
+    a.waves, a.out_frag, a.strided = waves, out_frag, strided
     pb, cb = lib.attn_workspace(a)
     part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
     cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
@@ -308,10 +308,13 @@ def attn_case(lib, B, T, lens, cap, chunk, seed, waves=4, out_frag=0, valid=True
 
 
 @pytest.mark.parametrize("waves", [4, 8])
-@pytest.mark.parametrize("B,lens,cap,chunk", [(1, [640], 800, 96), (1, [767], 800, 96), (1, [640], 800, 128),
-                                               (1, [100], 800, 128), (3, [700, 31, 257], 800, 128),
-                                               (2, [200, 90], 256, 256), (1, [4000], 4384, 256)])
-def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chunk, waves):
+@pytest.mark.parametrize("B,lens,cap,chunk,strided", [
+    (1, [640], 800, 96, 0), (1, [767], 800, 96, 0), (1, [640], 800, 128, 0), (1, [100], 800, 128, 0),
+    (3, [700, 31, 257], 800, 128, 0), (2, [200, 90], 256, 256, 0), (1, [4000], 4384, 256, 0),
+    (1, [640], 800, 96, 1), (3, [700, 31, 257], 800, 224, 1), (2, [4000, 33], 4384, 1120, 1)])
+def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chunk, strided, waves):
+    if strided and waves != 8:
+        pytest.skip("strided chunks run 8 waves")
     """Attention with out_partials + an O projection reading x_attn gives the
     same bits as the attention's own merged output fed to the O projection
     (one chunk and several; the attention's out buffer is left untouched).
@@ -339,7 +342,7 @@ def test_o_projection_merges_attention_partials_bitexact(lib, B, lens, cap, chun
         a = capi.AttnArgs(qkv=qkv.data_ptr(), q_norm_w=qn.data_ptr(), k_norm_w=kn.data_ptr(), cos_tab=dcos.data_ptr(),
                           sin_tab=dsin.data_ptr(), lens=dl.data_ptr(), k_cache=kc.data_ptr(), v_cache=vc.data_ptr(),
                           out=out.data_ptr(), eps=1e-6, sm_scale=D ** -0.5, batch=B, t_rows=1, nq=NQ, nkv=NKV,
-                          head_dim=D, cap=cap, chunk=chunk, waves=waves, out_partials=partials)
+                          head_dim=D, cap=cap, chunk=chunk, waves=waves, out_partials=partials, strided=strided)
         pb, cb = lib.attn_workspace(a)
         part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
         cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
@@ -658,6 +661,22 @@ def test_attention_vs_oracle(lib, B, T, lens, cap, chunk, waves):
     check_attention(c, B, T, lens)
 
 
+# Strided chunks (chunk c takes blocks c, c + C, ...): config 3's plan (batch
+# 8, 1568-slot cache, 4 chunks of 416, 8 waves) at lengths around its decode,
+# lengths that leave chunks empty, and verify-shaped rows over block bounds.
+@pytest.mark.parametrize("B,T,lens,cap,chunk,waves", [
+    (8, 1, [1024, 1023, 1055, 1300, 0, 31, 96, 1535], 1568, 416, 8),
+    (8, 2, [1000, 1017, 31, 64, 0, 511, 512, 700], 1056, 288, 8),
+    (2, 8, [0, 170], 256, 64, 8),
+    (3, 1, [5, 64, 129], 192, 64, 8),
+    (2, 4, [3, 170], 256, 64, 8),
+    (1, 1, [4000], 4384, 576, 8),
+])
+def test_attention_strided_vs_oracle(lib, B, T, lens, cap, chunk, waves):
+    c = attn_case(lib, B, T, lens, cap, chunk, seed=B * 100 + T * 10 + lens[0] + 1, waves=waves, strided=1)
+    check_attention(c, B, T, lens)
+
+
 # Config 4's decode attention as the engine plans it (qdec.runtime attn_chunk /
 # attn_waves / FRAG_ROWS for batch 32, capacity 4096 + 256 + 2 -> 4384): one
 # whole-cache chunk per (sequence, kv head), 8 waves, output in fragment order
@@ -691,24 +710,27 @@ def check_attention(c, B, T, lens):
     near_exact(k_after[new], kc[new])
 
 
-@pytest.mark.parametrize("cap,chunk,L,T,waves", [(256, 64, 100, 9, 4), (256, 64, 63, 9, 4), (1056, 96, 1000, 9, 4),
-                                                (512, 128, 0, 9, 4), (256, 64, 100, 8, 8), (1056, 512, 1000, 8, 8)])
-def test_attention_t_invariance_bitexact(lib, cap, chunk, L, T, waves):
+@pytest.mark.parametrize("cap,chunk,L,T,waves,strided", [
+    (256, 64, 100, 9, 4, 0), (256, 64, 63, 9, 4, 0), (1056, 96, 1000, 9, 4, 0), (512, 128, 0, 9, 4, 0),
+    (256, 64, 100, 8, 8, 0), (1056, 512, 1000, 8, 8, 0),
+    (1056, 96, 1000, 8, 8, 1), (256, 64, 100, 8, 8, 1), (1568, 416, 1020, 8, 8, 1),
+    (1056, 288, 90, 8, 8, 1)])
+def test_attention_t_invariance_bitexact(lib, cap, chunk, L, T, waves, strided):
     """Verify row t (t_rows = T) at position L + t equals the plain T = 1 step
     at that position, bit for bit, given the same cache contents (4 waves up
     to 16 rows per sequence, 8 waves up to 8)."""
     B = 2
-    c9 = attn_case(lib, B, T, [L, L + 3], cap, chunk, seed=77, waves=waves)
+    c9 = attn_case(lib, B, T, [L, L + 3], cap, chunk, seed=77, waves=waves, strided=strided)
     for t in range(T):
         # plain step at position L + t: cache holds the verify pass's K/V for
         # slots < L + t (the first pass already wrote them) and the same qkv row.
         pos_lens = [L + t, L + 3 + t]
-        one = attn_case_from(lib, c9, B, T, t, pos_lens, cap, chunk, waves=waves)
+        one = attn_case_from(lib, c9, B, T, t, pos_lens, cap, chunk, waves=waves, strided=strided)
         for b in range(B):
             assert torch.equal(one[b].view(torch.int16), c9["out"][b * T + t].view(torch.int16)), (t, b)
 
 
-def attn_case_from(lib, c9, B, T, t, lens, cap, chunk, waves=4):
+def attn_case_from(lib, c9, B, T, t, lens, cap, chunk, waves=4, strided=0):
     """Run T = 1 on row t of every sequence of case c9, with the cache as the
     T = 9 call left it."""
     from qdec import capi
@@ -725,7 +747,7 @@ def attn_case_from(lib, c9, B, T, t, lens, cap, chunk, waves=4):
     a.k_cache, a.v_cache, a.out = dk.data_ptr(), dv.data_ptr(), out.data_ptr()
     a.eps, a.sm_scale = 1e-6, D ** -0.5
     a.batch, a.t_rows, a.nq, a.nkv, a.head_dim, a.cap, a.chunk = B, 1, NQ, NKV, D, cap, chunk
-    a.waves = waves
+    a.waves, a.strided = waves, strided
     pb, cb = lib.attn_workspace(a)
     part = torch.zeros(max(pb, 16) // 4, dtype=torch.float32, device=DEV)
     cnt = torch.zeros(max(cb, 4) // 4, dtype=torch.int32, device=DEV)
@@ -1036,6 +1058,8 @@ def test_gemm_epilogues_stay_in_bounds(lib, rows):
 
 @pytest.mark.parametrize("B,T,lens,cap,chunk,waves,frag,partials,layout", [
     (1, 1, [640], 800, 96, 4, 0, 1, None), (3, 1, [700, 31, 257], 800, 128, 4, 0, 0, None),
+    (8, 1, [1024, 1023, 0, 1535, 5, 416, 832, 1300], 1568, 416, 8, 1, 0, "strided"),
+    (8, 2, [1024, 1023, 0, 1534, 5, 416, 832, 1300], 1568, 416, 8, 0, 1, "strided"),
     (20, 1, [100 + 37 * i for i in range(20)], 896, 896, 8, 1, 0, None), (4, 4, [60, 0, 7, 100], 128, 64, 4, 0, 0, None),
     # the tiny model's 4 / 2 heads at head_dim 64, and Qwen3-14B's 40 / 8
     (1, 1, [300], 416, 96, 4, 0, 1, (4, 2, 64)), (5, 4, [60, 0, 7, 100, 33], 128, 64, 4, 1, 0, (4, 2, 64)),
@@ -1045,7 +1069,8 @@ def test_attention_stays_in_bounds(lib, B, T, lens, cap, chunk, waves, frag, par
     counters written into the middle of larger buffers: the bands and every
     cache slot outside the new ones stay untouched."""
     from qdec import capi
-    NQ, NKV, D = layout or HEADS_4B
+    strided = int(layout == "strided")
+    NQ, NKV, D = HEADS_4B if layout in (None, "strided") else layout
     g = torch.Generator().manual_seed(cap + B)
     W = (NQ + 2 * NKV) * D
     qkv = (torch.randn(B * T, W, generator=g) * 2).to(torch.bfloat16).to(DEV)
@@ -1065,7 +1090,8 @@ def test_attention_stays_in_bounds(lib, B, T, lens, cap, chunk, waves, frag, par
     a = capi.AttnArgs(qkv=qkv.data_ptr(), q_norm_w=qn.data_ptr(), k_norm_w=kn.data_ptr(), cos_tab=dcos.data_ptr(),
                       sin_tab=dsin.data_ptr(), lens=dl.data_ptr(), k_cache=kc.data_ptr(), v_cache=vc.data_ptr(),
                       out=out.data_ptr(), eps=1e-6, sm_scale=D ** -0.5, batch=B, t_rows=T, nq=NQ, nkv=NKV,
-                      head_dim=D, cap=cap, chunk=chunk, waves=waves, out_partials=partials, out_frag=frag)
+                      head_dim=D, cap=cap, chunk=chunk, waves=waves, out_partials=partials, out_frag=frag,
+                      strided=strided)
     pb, cb = lib.attn_workspace(a)
     pw_whole, pw = banded(max(pb, 4) // 4, dtype=torch.float32)
     cw_whole, cw = banded(max(cb, 4) // 4, dtype=torch.int32, fill=0)
