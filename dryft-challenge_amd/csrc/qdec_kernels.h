@@ -30,7 +30,7 @@ constexpr int kArgSlots = 16;
 // at most kResMaxPairs tile pairs (4 waves each) per workgroup and
 // kResMaxKSteps k steps (k <= 2560).  NORM_IN alone (QKV) takes the first
 // kind with single tiles in place of the pairs.
-constexpr int kResMinRows = 6;
+constexpr int kResMinRows = 1;
 constexpr int kResMaxRows = 8;
 constexpr int kResMinRows2 = 17;
 constexpr int kResMaxRows2 = 32;

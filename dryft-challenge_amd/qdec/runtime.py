@@ -125,10 +125,12 @@ RESIDENT_RES_ROWS = (1, 8)
 # 3.311; down 15.1 -> 12.7 us per launch).
 RESIDENT_SPLIT_ROWS = (17, 32)
 # QKV (NORM_IN alone) at these rows takes gate/up's resident plan with single
-# tiles: the workgroup normalises its rows into LDS itself.  Same-box A/B at
-# batch 8 and 1024-token prompts: QKV 11.5 -> 8.7 us per launch, 2.651 ->
-# 2.549 ms per step, the same tokens.
-RESIDENT_QKV_ROWS = (6, 8)
+# tiles: the workgroup normalises its rows into LDS itself.  Same-box A/B,
+# QKV us per launch and ms per step, the same tokens: batch 8 (1024-token
+# prompts) 11.5 -> 8.7, 2.651 -> 2.549; batch 4 9.65 -> 7.81, 2.364 ->
+# 2.320; batch 1 (512) 8.82 -> 7.80.  gate/up stays off the resident plan
+# below 6 rows: 19.0 -> 21.0 us at batch 1, 20.1 -> 21.1 at batch 4.
+RESIDENT_QKV_ROWS = (1, 8)
 
 
 def round_up(x, m):

@@ -224,17 +224,17 @@ typedef struct {
   int32_t next_threads;
   /* 1: gate/up with its rows resident in LDS.  For NORM_IN | GLU with
    * ksplit 1, 4 waves, one tile per workgroup, row-major x (no x_frag,
-   * x_attn, x_parts or next_norm_w), 6..8 or 17..32 rows, k <= 2560 and
+   * x_attn, x_parts or next_norm_w), 1..8 or 17..32 rows, k <= 2560 and
    * k / 128 a multiple of 10: one workgroup per compute unit takes a
    * contiguous run of (gate, up) tile pairs and reads its MFMA operands
    * from one copy of the normalised rows in LDS, so no workgroup re-reads
-   * the activations from L2.  At 6..8 rows the workgroup normalises the
+   * the activations from L2.  At 1..8 rows the workgroup normalises the
    * rows itself (no normalisation pre-pass is launched, no workspace); at
    * 17..32 rows the pre-pass still normalises them into the workspace and
    * each workgroup copies them in.  The output is bit-identical to the same
    * call with resident = 0 (the statistic, the k split over 4 waves and the
    * epilogue are the same).
-   * NORM_IN alone (QKV), under the same bounds at 6..8 rows with k / 128 a
+   * NORM_IN alone (QKV), under the same bounds at 1..8 rows with k / 128 a
    * multiple of 20: the same plan with single output tiles in place of the
    * pairs (one or two per workgroup); the same bits as resident = 0.
    * For RES_OUT with ksplit 1, one tile per workgroup, row-major x (no

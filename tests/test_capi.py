@@ -123,15 +123,14 @@ GU_RES = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4, rows=8, re
     (dict(waves=8), -3, "4 waves"),
     (dict(tiles_per_wg=2), -3, "one tile"),
     (dict(x_frag=1, flags=capi.GLU), -3, "row-major x"),
-    (dict(rows=5), -3, "6..8 or 17..32 rows"),
-    (dict(rows=9), -3, "6..8 or 17..32 rows"),
-    (dict(rows=16), -3, "6..8 or 17..32 rows"),
-    (dict(rows=33), -3, "6..8 or 17..32 rows"),
+    (dict(rows=9), -3, "1..8 or 17..32 rows"),
+    (dict(rows=16), -3, "1..8 or 17..32 rows"),
+    (dict(rows=33), -3, "1..8 or 17..32 rows"),
     (dict(n=16), -3, "two output tiles"),
     (dict(k=4096), -3, "k <= 2560"),
     (dict(k=1024), -3, "multiple of 10"),
-    (dict(flags=capi.NORM_IN, n=6144, rows=5), -3, "NORM_IN takes 6..8 rows"),
-    (dict(flags=capi.NORM_IN, n=6144, rows=17), -3, "NORM_IN takes 6..8 rows"),
+    (dict(flags=capi.NORM_IN, n=6144, rows=9), -3, "NORM_IN takes 1..8 rows"),
+    (dict(flags=capi.NORM_IN, n=6144, rows=17), -3, "NORM_IN takes 1..8 rows"),
     (dict(flags=capi.NORM_IN, n=6144, k=1280), -3, "multiple of 20"),
     (dict(flags=capi.NORM_IN, n=16), -3, "two output tiles"),
 ])
@@ -206,10 +205,10 @@ def test_gemm_resident_workspace_and_prepass(qlib):
     """At 6..8 rows the resident call normalises its rows itself (no
     workspace, no pre-pass); at 17..32 the pre-pass still writes the two M
     tiles of normalised rows into the workspace, as without resident."""
-    for rows in (6, 7, 8):
+    for rows in (1, 3, 6, 7, 8):
         assert qlib.gemm_workspace(_gemm(**dict(GU_RES, rows=rows))) == (0, 0)
         assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows))) == (False, 256)
-        assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows, resident=0))) == (True, 256)
+        assert qlib.gemm_prepass(_gemm(**dict(GU_RES, rows=rows, resident=0))) == (rows >= 6, 256)
         # QKV (NORM_IN alone) likewise
         qkv = dict(GU_RES, flags=capi.NORM_IN, n=6144, rows=rows)
         assert qlib.gemm_workspace(_gemm(**qkv)) == (0, 0)
