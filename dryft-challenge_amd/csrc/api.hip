@@ -183,12 +183,10 @@ static int plan_gemm(const qdec_gemm_args *a, GemmParams *p, bool need_scratch) 
         a->tiles_per_wg != 1 || a->x_frag || xa || a->next_norm_w)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs NORM_IN (with or without GLU), ksplit 1, 4 waves, "
                        "one tile per workgroup and row-major x (no x_frag, x_attn or next_norm_w)");
-    const bool two = glu && a->rows >= kResMinRows2 && a->rows <= kResMaxRows2;
+    const bool two = a->rows >= kResMinRows2 && a->rows <= kResMaxRows2;
     if (!two && (a->rows < kResMinRows || a->rows > kResMaxRows))
-      return glu ? set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d or %d..%d rows, not %d", kResMinRows,
-                             kResMaxRows, kResMinRows2, kResMaxRows2, a->rows)
-                 : set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident NORM_IN takes %d..%d rows, not %d", kResMinRows,
-                             kResMaxRows, a->rows);
+      return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident takes %d..%d or %d..%d rows, not %d", kResMinRows,
+                       kResMaxRows, kResMinRows2, kResMaxRows2, a->rows);
     const int ring = glu ? kResRing : kResRing1;
     if (KS > kResMaxKSteps || p->ksw % ring)
       return set_error(QDEC_EUNSUPPORTED, "qdec_gemm: resident needs k <= %d with k/128 a multiple of %d (k %d)",

@@ -274,9 +274,10 @@ constexpr int res_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) |
 // ring operands (608 x 164 KB per launch for Qwen3-4B at 32 rows).  The
 // ring then holds weights only (RW slots of gate and up blocks).  Sums,
 // order and epilogue are the direct path's at two M tiles.
-template <int RW>
+template <int RW, bool GLU>
 __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(const GemmParams p) {
   constexpr int MT = 2;
+  constexpr int NA = GLU ? 2 : 1;
   __shared__ __align__(16) uint4 s_x[kResMaxKSteps * MT * 64];  // [k step][M tile][lane]; then the wave merge
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -303,26 +304,29 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   const size_t up_off = (size_t)p.up_tiles * KS * 64;
   const int ksw_w = active ? ksw : 0;
   const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + lane;
-  uint4 wg[RW], wu[RW];
+  uint4 wg[RW], wu[GLU ? RW : 1];
   if (active) {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       wg[r] = ldw(wq + r * 64);
-      wu[r] = ldw(wq + r * 64 + up_off);
+      if constexpr (GLU) wu[r] = ldw(wq + r * 64 + up_off);
     }
   }
-  // The copies are older than every ring load: once at most 2 RW loads are
-  // outstanding (RW when the wave has no pair), they have landed.
+  // The copies are older than every ring load: once at most NA RW loads are
+  // outstanding (none when the wave has no unit), they have landed.
   if (active)
-    __builtin_amdgcn_s_waitcnt(res_vmcnt(2 * RW));
+    __builtin_amdgcn_s_waitcnt(res_vmcnt(NA * RW));
   else
     __builtin_amdgcn_s_waitcnt(res_vmcnt(0));
   (void)ndma;
   __syncthreads();
 
-  f32x4_t ag[MT], au[MT];
+  f32x4_t ag[MT], au[GLU ? MT : 1];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) ag[mt] = au[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int mt = 0; mt < MT; ++mt) {
+    ag[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if constexpr (GLU) au[mt] = ag[mt];
+  }
   const bool xrow0 = col < rows, xrow1 = 16 + col < rows;
   constexpr int CH = 5;  // k steps whose B operands are read from LDS ahead
   static_assert(RW % CH == 0, "chunks within a ring pass");
@@ -343,25 +347,28 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
         const int r = c0 + c;
         ag[0] = mfma16x16x32(wg[r], b0[c], ag[0]);
         ag[1] = mfma16x16x32(wg[r], b1[c], ag[1]);
-        au[0] = mfma16x16x32(wu[r], b0[c], au[0]);
-        au[1] = mfma16x16x32(wu[r], b1[c], au[1]);
+        if constexpr (GLU) {
+          au[0] = mfma16x16x32(wu[r], b0[c], au[0]);
+          au[1] = mfma16x16x32(wu[r], b1[c], au[1]);
+        }
         if (refill) {
           wg[r] = ldw(qn + r * 64);
-          wu[r] = ldw(qn + r * 64 + up_off);
+          if constexpr (GLU) wu[r] = ldw(qn + r * 64 + up_off);
         }
       }
     }
   }
 
-  // ---- the pair's four waves in wave order (the merge reuses the rows' LDS),
-  // then SwiGLU.
+  // ---- the unit's four waves in wave order (the merge reuses the rows'
+  // LDS), then SwiGLU or the plain store.
   __syncthreads();
-  float4 *red = reinterpret_cast<float4 *>(s_x);  // [pair][wave 1..3][gate, up][M tile][lane]
+  float4 *red = reinterpret_cast<float4 *>(s_x);  // [unit][wave 1..3][gate, up][M tile][lane]
   if (active && q > 0) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      red[((((j * 3 + q - 1) * 2 + 0) * MT + mt) * 64) + lane] = make_float4(ag[mt][0], ag[mt][1], ag[mt][2], ag[mt][3]);
-      red[((((j * 3 + q - 1) * 2 + 1) * MT + mt) * 64) + lane] = make_float4(au[mt][0], au[mt][1], au[mt][2], au[mt][3]);
+      red[((((j * 3 + q - 1) * NA + 0) * MT + mt) * 64) + lane] = make_float4(ag[mt][0], ag[mt][1], ag[mt][2], ag[mt][3]);
+      if constexpr (GLU)
+        red[((((j * 3 + q - 1) * NA + 1) * MT + mt) * 64) + lane] = make_float4(au[mt][0], au[mt][1], au[mt][2], au[mt][3]);
     }
   }
   __syncthreads();
@@ -370,10 +377,12 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   for (int w2 = 1; w2 < 4; ++w2) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const float4 rg = red[((((j * 3 + w2 - 1) * 2 + 0) * MT + mt) * 64) + lane];
-      const float4 ru = red[((((j * 3 + w2 - 1) * 2 + 1) * MT + mt) * 64) + lane];
+      const float4 rg = red[((((j * 3 + w2 - 1) * NA + 0) * MT + mt) * 64) + lane];
       ag[mt][0] += rg.x; ag[mt][1] += rg.y; ag[mt][2] += rg.z; ag[mt][3] += rg.w;
-      au[mt][0] += ru.x; au[mt][1] += ru.y; au[mt][2] += ru.z; au[mt][3] += ru.w;
+      if constexpr (GLU) {
+        const float4 ru = red[((((j * 3 + w2 - 1) * NA + 1) * MT + mt) * 64) + lane];
+        au[mt][0] += ru.x; au[mt][1] += ru.y; au[mt][2] += ru.z; au[mt][3] += ru.w;
+      }
     }
   }
   const int n0 = tile * 16 + grp * 4;
@@ -382,17 +391,22 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + col;
     if (m >= rows) continue;
-    float o4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float g = rbf(ag[mt][i]);
-      const float u = rbf(au[mt][i]);
-      const float sg = rbf(g / (1.0f + expf(-g)));
-      o4[i] = sg * u;
-    }
     uint2 o;
-    o.x = pack2(o4[0], o4[1]);
-    o.y = pack2(o4[2], o4[3]);
+    if constexpr (GLU) {
+      float o4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float g = rbf(ag[mt][i]);
+        const float u = rbf(au[mt][i]);
+        const float sg = rbf(g / (1.0f + expf(-g)));
+        o4[i] = sg * u;
+      }
+      o.x = pack2(o4[0], o4[1]);
+      o.y = pack2(o4[2], o4[3]);
+    } else {
+      o.x = pack2(ag[mt][0], ag[mt][1]);
+      o.y = pack2(ag[mt][2], ag[mt][3]);
+    }
     *reinterpret_cast<uint2 *>(p.ofrag ? out + frag_off(m, n0, p.ofrag) : out + (size_t)m * p.n + n0) = o;
   }
 }
@@ -655,8 +669,13 @@ hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
     else
       return hipErrorInvalidValue;
   } else {
-    if (!glu || p.rows > 32 || !p.xn || p.KS > kResMaxKSteps) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((glu_resident2_kernel<kResRing>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+    if (p.rows > 32 || !p.xn || p.KS > kResMaxKSteps) return hipErrorInvalidValue;
+    if (glu && p.rw == kResRing)
+      hipLaunchKernelGGL((glu_resident2_kernel<kResRing, true>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+    else if (!glu && p.rw == kResRing1)
+      hipLaunchKernelGGL((glu_resident2_kernel<kResRing1, false>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
+    else
+      return hipErrorInvalidValue;
   }
   return hipSuccess;
 }

@@ -129,8 +129,10 @@ RESIDENT_SPLIT_ROWS = (17, 32)
 # QKV us per launch and ms per step, the same tokens: batch 8 (1024-token
 # prompts) 11.5 -> 8.7, 2.651 -> 2.549; batch 4 9.65 -> 7.81, 2.364 ->
 # 2.320; batch 1 (512) 8.82 -> 7.80.  gate/up stays off the resident plan
-# below 6 rows: 19.0 -> 21.0 us at batch 1, 20.1 -> 21.1 at batch 4.
-RESIDENT_QKV_ROWS = (1, 8)
+# below 6 rows: 19.0 -> 21.0 us at batch 1, 20.1 -> 21.1 at batch 4.  At
+# 17..32 rows the pre-pass's rows are copied in and k splits over 4 waves
+# (role_plan): batch 32 at 4096-token prompts 5.481 -> 5.449 ms per step.
+RESIDENT_QKV_ROWS = ((1, 8), (17, 32))
 
 
 def round_up(x, m):
@@ -241,8 +243,9 @@ def role_plan(n, k, role, batch=1):
         # Same-box A/B at batch 32 and 4096-token prompts: O 10.5 -> 7.6 us
         # per launch.
         return O_SPLIT, 4, 1
-    if role == "qkv" and batch >= WIDE_MIN_ROWS:
-        # two tiles per wave (WIDE_TILES): 192 workgroups, 8 waves each
+    if role == "qkv" and batch >= WIDE_MIN_ROWS and not any(lo <= batch <= hi for lo, hi in RESIDENT_QKV_ROWS[1:]):
+        # two tiles per wave (WIDE_TILES): 192 workgroups, 8 waves each; the
+        # resident plan (RESIDENT_QKV_ROWS) splits k over 4 waves
         waves = 8
     if role == "o" and batch >= O_FOUR_WAVES_MIN_BATCH:
         # From 8 rows O's activations no longer fit the LDS and it takes the
@@ -548,7 +551,8 @@ class DecodeState:
         if role == "gate_up":
             ok = not a.x_frag and any(lo <= a.rows <= hi for lo, hi in RESIDENT_ROWS)
         elif role == "qkv":
-            ok = not a.x_frag and not a.x_parts and RESIDENT_QKV_ROWS[0] <= a.rows <= RESIDENT_QKV_ROWS[1]
+            ok = (not a.x_frag and any(lo <= a.rows <= hi for lo, hi in RESIDENT_QKV_ROWS)
+                  and (not a.x_parts or a.rows >= WIDE_MIN_ROWS))
         elif role not in RESIDENT_RES_ROLES:
             ok = False
         elif a.parts_out:
@@ -685,7 +689,12 @@ class DecodeState:
             a.partial = self.gemm_partial.data_ptr()
             a.counters = self.gemm_counters.data_ptr()
         if role in ("gate_up", "qkv") + RESIDENT_RES_ROLES:
+            wide = a.tiles_per_wg
+            if role == "qkv":
+                a.tiles_per_wg = 1  # the resident plan takes one tile per workgroup
             a.resident = 1 if self._resident(a, role) else 0
+            if not a.resident:
+                a.tiles_per_wg = wide
         if hand:
             L = c.n_layers
             if role in ("o", "down"):

@@ -234,9 +234,10 @@ typedef struct {
    * each workgroup copies them in.  The output is bit-identical to the same
    * call with resident = 0 (the statistic, the k split over 4 waves and the
    * epilogue are the same).
-   * NORM_IN alone (QKV), under the same bounds at 1..8 rows with k / 128 a
-   * multiple of 20: the same plan with single output tiles in place of the
-   * pairs (one or two per workgroup); the same bits as resident = 0.
+   * NORM_IN alone (QKV), under the same bounds at 1..8 or 17..32 rows with
+   * k / 128 a multiple of 20: the same plan with single output tiles in
+   * place of the pairs (one or two per workgroup); the same bits as
+   * resident = 0.
    * For RES_OUT with ksplit 1, one tile per workgroup, row-major x (no
    * x_frag, x_attn, parts_out or next_norm_w), 1..8 rows and k / 32 a
    * multiple of 16 and at most 304: every workgroup first copies the rows

@@ -129,8 +129,8 @@ GU_RES = dict(flags=capi.NORM_IN | capi.GLU, n=9728, k=2560, waves=4, rows=8, re
     (dict(n=16), -3, "two output tiles"),
     (dict(k=4096), -3, "k <= 2560"),
     (dict(k=1024), -3, "multiple of 10"),
-    (dict(flags=capi.NORM_IN, n=6144, rows=9), -3, "NORM_IN takes 1..8 rows"),
-    (dict(flags=capi.NORM_IN, n=6144, rows=17), -3, "NORM_IN takes 1..8 rows"),
+    (dict(flags=capi.NORM_IN, n=6144, rows=9), -3, "1..8 or 17..32 rows"),
+    (dict(flags=capi.NORM_IN, n=6144, rows=33), -3, "1..8 or 17..32 rows"),
     (dict(flags=capi.NORM_IN, n=6144, k=1280), -3, "multiple of 20"),
     (dict(flags=capi.NORM_IN, n=16), -3, "two output tiles"),
 ])
@@ -371,7 +371,9 @@ def test_role_plans_do_not_depend_on_rows():
     assert role_plan(2560, 9728, "down", batch=16)[:2] == (4, 4)
     assert role_plan(2560, 9728, "down", batch=8) == (1, 8, 1)
     assert role_plan(2560, 4096, "o", batch=7) == (1, 8, 1) and role_plan(2560, 4096, "o", batch=8) == (1, 4, 1)
-    assert role_plan(6144, 2560, "qkv", batch=17)[:2] == (1, 8) and role_plan(6144, 2560, "qkv", batch=16)[:2] == (1, 4)
+    # QKV from 17 rows: k over 4 waves on the resident plan, else 8 waves of two tiles
+    assert role_plan(6144, 2560, "qkv", batch=17)[:2] == (1, 4) and role_plan(6144, 2560, "qkv", batch=16)[:2] == (1, 4)
+    assert role_plan(6144, 2560, "qkv", batch=33)[:2] == (1, 8)
     # the 160-tile roles run 8 waves, the others 4; the lm_head 4 tiles per workgroup
     assert [role_plan(n, k, r)[1] for r, n, k in (("qkv", 6144, 2560), ("o", 2560, 4096),
                                                   ("gate_up", 9728, 2560), ("down", 2560, 9728),

@@ -177,7 +177,7 @@ def test_full_depth_config4_plan_vs_fp32():
     prompt = torch.randint(0, cfg["vocab_size"], (B, S), generator=g)
     st = DecodeState(eng.model, B, 4096 + 256 + 2, max_t=1, keep_logits=True)
     assert st.cap == 4384 and st.chunk == 4384 and st.attn_waves == 8 and B >= FRAG_ROWS
-    assert st.down_parts is not None and st.plans["down"][0] == 4 and st.plans["qkv"][1] == 8
+    assert st.down_parts is not None and st.plans["down"][0] == 4 and st.plans["qkv"][1] == 4
     toks, logits = _run_engine(st, prompt, n)
     _say(f"engine B={B}: prefill + {n - 1} decode steps ({time.perf_counter() - t0:.0f}s)")
     del st, eng

@@ -489,12 +489,13 @@ def test_glu_resident_bitexact(lib, rows, frag):
 
 
 @pytest.mark.parametrize("frag", [0, 1])
-@pytest.mark.parametrize("rows", [1, 3, 5, 6, 7, 8])
+@pytest.mark.parametrize("rows", [1, 3, 5, 6, 7, 8, 17, 24, 32])
 def test_qkv_resident_bitexact(lib, rows, frag):
-    """QKV (NORM_IN alone) on the resident plan with single tiles -- the
-    workgroup normalises its rows into LDS itself, 1 or 2 tiles per
-    workgroup -- gives the bits of the plain call, in row-major and
-    fragment-order output, and agrees with the oracle."""
+    """QKV (NORM_IN alone) on the resident plan with single tiles -- 1 or 2
+    tiles per workgroup; up to 8 rows the workgroup normalises its rows into
+    LDS itself, at 17..32 it copies the pre-pass's rows in -- gives the bits
+    of the plain call, in row-major and fragment-order output, and agrees
+    with the oracle."""
     from qdec import capi
     from qdec.runtime import role_plan
     n = 6144
@@ -513,8 +514,10 @@ def test_qkv_resident_bitexact(lib, rows, frag):
                           rows=rows, n=n, k=H, flags=capi.NORM_IN, ksplit=ks, waves=waves, tiles_per_wg=1,
                           out_frag=frag, resident=resident, partial=g.partial.data_ptr(),
                           counters=g.counters.data_ptr())
-        if resident:
-            assert lib.gemm_workspace(a)[0] == 0 and not lib.gemm_prepass(a)[0]
+        pb, _ = lib.gemm_workspace(a)
+        assert pb <= g.partial.numel() * 4
+        if resident and rows <= 8:
+            assert pb == 0 and not lib.gemm_prepass(a)[0]
         lib.gemm(a, stream())
         torch.cuda.synchronize()
         outs.append(frag_to_rows(out, rows, n).cpu() if frag else out[:rows].cpu())
