@@ -648,11 +648,12 @@ hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
   if (e != hipSuccess) return e;
   const bool glu = p.resident == 1;  // otherwise NORM_IN alone (4)
   const int P = p.n / 16;
-  // One workgroup per CU with two or three tile pairs each (GLU), or one or
-  // more single tiles: more workgroups than CUs for a matrix past
-  // kResMaxPairs units per CU, fewer for one below two pairs (one tile).
+  // One workgroup per CU with two or three tile pairs each (GLU) or up to
+  // two single tiles: more workgroups than CUs for a matrix past that many
+  // units per CU, fewer for a small one -- but always a workgroup with two
+  // units, whose last four waves normalise the rows (at most 8 rows).
   const int umax = glu ? kResMaxPairs : kResMaxTiles1;
-  const int grid = std::max((P + umax - 1) / umax, std::min(ncu, glu ? P / 2 : P));
+  const int grid = std::max((P + umax - 1) / umax, std::min(ncu, glu ? P / 2 : P - 1));
   if (grid < 1) return hipErrorInvalidValue;
   const int pairs = (P + grid - 1) / grid;
   if (pairs > umax || (p.rw != kResRing && p.rw != kResRing1) || p.ksw % p.rw) return hipErrorInvalidValue;

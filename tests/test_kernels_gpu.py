@@ -525,6 +525,31 @@ def test_qkv_resident_bitexact(lib, rows, frag):
     agree(outs[1], linear(rms_norm(x.float(), nw.float(), 1e-6), W.float()), min_exact=0.97)
 
 
+@pytest.mark.parametrize("n", [32, 48, 64, 4096])
+def test_norm_in_resident_small_grids_bitexact(lib, n):
+    """NORM_IN alone on the resident plan for matrices of 2, 3, 4 and 256
+    tiles: every workgroup gets two tiles or one beside the normalising
+    waves, and the output equals the plain call's bits."""
+    from qdec import capi
+    rows = 8
+    x = rnd(rows, H, scale=2.0, seed=70 + n)
+    W = rnd(n, H, scale=0.02, seed=71)
+    nw = bf16(1 + 0.2 * torch.randn(H, generator=torch.Generator().manual_seed(72))).to(torch.bfloat16)
+    xd, Wt, nwd = x.to(DEV), pack(lib, W.to(DEV)), nw.to(DEV)
+    g = Gemm(lib, capi.NORM_IN, n, H)
+    outs = []
+    for resident in (0, 1):
+        out = torch.full((rows, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+        a = capi.GemmArgs(x=xd.data_ptr(), w=Wt.data_ptr(), out=out.data_ptr(), norm_w=nwd.data_ptr(), eps=1e-6,
+                          rows=rows, n=n, k=H, flags=capi.NORM_IN, ksplit=1, waves=4, tiles_per_wg=1,
+                          resident=resident, partial=g.partial.data_ptr(), counters=g.counters.data_ptr())
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    agree(outs[1], linear(rms_norm(x.float(), nw.float(), 1e-6), W.float()), min_exact=0.97)
+
+
 @pytest.mark.parametrize("role,rows", [("down", 1), ("down", 2), ("down", 3), ("down", 5), ("down", 8), ("o", 1),
                                       ("o", 3), ("o", 4), ("o", 8)])
 def test_res_out_rows_in_lds_bitexact(lib, role, rows):
