@@ -272,10 +272,12 @@ def role_plan(n, k, role, batch=1):
 # prompts, 8 waves / 4 waves: batch 8 2.964 / 3.017, batch 6 2.891 / 2.953;
 # once the 8-wave chunks were equal over all CUs also batch 5 2.685 /
 # 2.718 (2048 tokens 2.833 / 2.962), batch 4 2.460 / 2.482 (2048 tokens
-# 2.545 / 2.554, 4096 tokens 2.728 / 2.774).  Batch 3 is mixed (1024
-# tokens 2.388 / 2.414, 2048 tokens 2.506 / 2.468), and batch 2 2.281 /
-# 2.275 and batch 1 2.163 / 2.130 stay on 4.
-ATTN8_MIN_BATCH = 4
+# 2.545 / 2.554, 4096 tokens 2.728 / 2.774).  With strided chunks batch
+# 3 gains too (512 tokens 2.234 / 2.281, 1024 2.263 / 2.307, 2048 2.372 /
+# 2.359, 4096 2.542 / 2.554).  Batch 2, whose attention partials O merges,
+# is mixed (1024 tokens 2.195 / 2.228, 2048 2.404 / 2.283: ten chunks to
+# merge), and batch 1 (2.089 / 2.077) stays on 4.
+ATTN8_MIN_BATCH = 3
 # Rows per sequence an 8-wave attention workgroup takes (two M tiles of
 # query rows per kv head).
 ATTN8_MAX_T = 8
@@ -798,10 +800,10 @@ class DecodeState:
 
     def layer_attn_args(self, layer):
         """The attention stage of qdec_layer: this state's arguments with
-        the layer kernel's 4 waves (its one block size), partials left for
-        the O stage."""
+        the layer kernel's 4 waves (its one block size) and contiguous
+        chunks (strided ones run 8 waves), partials left for the O stage."""
         at = self._attn_args(layer, 1, partials=True)
-        at.waves = 4
+        at.waves, at.strided = 4, 0
         return at
 
     def layer_gemm_args(self, role, layer, x_attn=None):
