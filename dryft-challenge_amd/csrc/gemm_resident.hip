@@ -76,8 +76,68 @@ __device__ __forceinline__ void res_signal(uint32_t *flag) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Units of a gate/up workgroup owning the half pairs [h0, h1): half pair
+// 2t + h is columns 8h .. 8h + 7 of gate tile t with the same columns of up
+// tile t, and a half pair whose partner lies in the same range joins it as
+// one whole pair.  Unit u of the walk: its pair and kind (0 whole pair,
+// 1 + h half pair h), or false past the last unit.  With at most five half
+// pairs per range a workgroup has at most three units.
+__host__ __device__ inline bool res_unit(unsigned h0, unsigned h1, int u, unsigned &pair, int &kind) {
+  unsigned h = h0;
+  for (int i = 0; i < kResMaxPairs; ++i) {
+    if (h >= h1) return false;
+    const int kd = (h & 1u) ? 2 : (h + 2 <= h1 ? 0 : 1);
+    if (i == u) {
+      pair = h >> 1;
+      kind = kd;
+      return true;
+    }
+    h += kd == 0 ? 2u : 1u;
+  }
+  return false;
+}
+
+// Unit j of this workgroup: runs of half pairs (GLU with p.res_half), else
+// a contiguous run of whole pairs (GLU) or tiles.  False when the workgroup
+// has fewer units.
+template <bool GLU>
+__device__ __forceinline__ bool res_unit_of(const GemmParams &p, int j, unsigned &tile, int &kind) {
+  const unsigned P = (unsigned)p.n >> 4;  // tile pairs (GLU) or tiles
+  if (GLU && p.res_half) {
+    const unsigned H = 2 * P;
+    return res_unit(blockIdx.x * H / gridDim.x, (blockIdx.x + 1) * H / gridDim.x, j, tile, kind);
+  }
+  const unsigned u0 = blockIdx.x * P / gridDim.x;
+  tile = u0 + j;
+  kind = 0;
+  return j < (int)((blockIdx.x + 1) * P / gridDim.x - u0);
+}
+
+// This lane's offset (16-byte units) within a k step's weight block: its
+// own slot, or for half pair h the slot of row 8h + (row % 8) and the same
+// k group in the gate block (rows below 8) or the up block (rows 8..15).
+__device__ __forceinline__ size_t res_lane_off(bool half, int kind, int lane, size_t up_off) {
+  if (!half) return (size_t)lane;
+  const int col = lane & 15, grp = lane >> 4;
+  return (col < 8 ? (size_t)0 : up_off) + (size_t)((col & 7) + 8 * (kind - 1) + 16 * grp);
+}
+
 // GLU: (gate, up) tile pairs and the SwiGLU epilogue; otherwise single
 // tiles (NORM_IN alone: QKV) and a bf16 store.
+//
+// With p.res_half (GLU) a workgroup owns a run of half pairs instead of
+// whole pairs (res_unit): 608 pairs over 256 CUs then put at most 2.5 pairs
+// of weights on a CU instead of 3 (a read-only probe of the two launch
+// shapes on MI355X: 16.5 against 18.3 us for gate/up's 99.6 MB).  A half
+// pair's wave takes the MFMA A operand from two blocks -- rows 8h .. 8h+7
+// of the gate block in lanes whose row is below 8, the same rows of the up
+// block in the others, 128-byte runs of each -- so one MFMA chain gives the
+// gate columns in lanes 0..31 and the up columns in lanes 32..63, and each
+// output element's sum is the whole pair's, bit for bit (the MFMA's sum of
+// one output does not depend on the row it sits in).  The unit's ring puts
+// k steps i .. i+RW-1 in wg and i+RW .. i+2RW-1 in wu, issued in the same
+// register order as a whole pair's, so the compiler's wait counts agree on
+// both paths.
 template <int RW, bool GLU>
 __global__ void __launch_bounds__(64 * 4 * (GLU ? kResMaxPairs : kResMaxTiles1)) glu_resident_kernel(const GemmParams p) {
   constexpr int NA = GLU ? 2 : 1;
@@ -92,26 +152,27 @@ __global__ void __launch_bounds__(64 * 4 * (GLU ? kResMaxPairs : kResMaxTiles1))
   const int nw = p.res_waves;  // blockDim.x / 64, from the kernel arguments (a scalar load)
   const int rows = p.rows, k = p.k, KS = p.KS, ksw = p.ksw;
   const int col = lane & 15, grp = lane >> 4;
-  const unsigned P = (unsigned)p.n >> 4;  // units: tile pairs (GLU) or tiles
-  const unsigned pair0 = blockIdx.x * P / gridDim.x;
-  const int npairs = (int)((blockIdx.x + 1) * P / gridDim.x - pair0);
-  const int j = wave >> 2, q = wave & 3;  // pair within the workgroup, k quarter
-  const bool active = j < npairs;
-  const int tile = (int)pair0 + j;
+  const int j = wave >> 2, q = wave & 3;  // unit within the workgroup, k quarter
+  unsigned tile = 0;
+  int kind = 0;  // 0 a whole pair (or tile), 1 + h half pair h
+  const bool active = res_unit_of<GLU>(p, j, tile, kind);
+  const bool half = GLU && kind != 0;
   if (tid == 0) s_sync[0] = s_sync[1] = s_sync[2] = 0u;
   __syncthreads();
 
   const uint4 *W = reinterpret_cast<const uint4 *>(p.w);
   const size_t up_off = (size_t)p.up_tiles * KS * 64;
   const int ksw_w = active ? ksw : 0;
-  const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + lane;
+  const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + res_lane_off(half, kind, lane, up_off);
+  // wu[r]'s block: the up tile's, or (half pair) RW k steps on
+  const size_t second = half ? (size_t)RW * 64 : up_off;
   uint4 wg[RW], wu[GLU ? RW : 1];
-  // The first RW k steps of this wave's range.
+  // The first RW k steps of this wave's range (2 RW for a half pair).
   auto issue_ring = [&]() {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       wg[r] = ldw(wq + r * 64);
-      if constexpr (GLU) wu[r] = ldw(wq + r * 64 + up_off);
+      if constexpr (GLU) wu[r] = ldw(wq + r * 64 + second);
     }
   };
 
@@ -191,23 +252,47 @@ __global__ void __launch_bounds__(64 * 4 * (GLU ? kResMaxPairs : kResMaxTiles1))
   // ---- the ring: slot r holds k step r (mod RW) of the wave's range.
   f32x4_t ag = f32x4_t{0.f, 0.f, 0.f, 0.f}, au = ag;
   const bool xrow_ok = col < rows;  // lanes past the last row multiply zeros
-  for (int i0 = 0; i0 < ksw_w; i0 += RW) {
-    const bool refill = i0 + RW < ksw_w;
-    const uint4 *qn = wq + (size_t)(i0 + RW) * 64;
-    uint4 bq[RW];
+  if (!half) {
+    for (int i0 = 0; i0 < ksw_w; i0 += RW) {
+      const bool refill = i0 + RW < ksw_w;
+      const uint4 *qn = wq + (size_t)(i0 + RW) * 64;
+      uint4 bq[RW];
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const int s = q * ksw + i0 + r;  // k step
-      bq[r] = xrow_ok ? s_x[s * 64 + res_pos(lane, s)] : zero4();
-    }
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      ag = mfma16x16x32(wg[r], bq[r], ag);
-      if constexpr (GLU) au = mfma16x16x32(wu[r], bq[r], au);
-      if (refill) {
-        wg[r] = ldw(qn + r * 64);
-        if constexpr (GLU) wu[r] = ldw(qn + r * 64 + up_off);
+      for (int r = 0; r < RW; ++r) {
+        const int s = q * ksw + i0 + r;  // k step
+        bq[r] = xrow_ok ? s_x[s * 64 + res_pos(lane, s)] : zero4();
       }
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        ag = mfma16x16x32(wg[r], bq[r], ag);
+        if constexpr (GLU) au = mfma16x16x32(wu[r], bq[r], au);
+        if (refill) {
+          wg[r] = ldw(qn + r * 64);
+          if constexpr (GLU) wu[r] = ldw(qn + r * 64 + up_off);
+        }
+      }
+    }
+  } else if constexpr (GLU) {
+    // A half pair: k steps i0 .. i0+RW-1 from wg, then the next RW from wu,
+    // one MFMA chain in k order.
+    for (int i0 = 0; i0 < ksw_w; i0 += 2 * RW) {
+      const bool refill = i0 + 2 * RW < ksw_w;
+      const uint4 *qn = wq + (size_t)(i0 + 2 * RW) * 64;
+      auto pass = [&](uint4(&a)[RW], const int hh) {
+        uint4 bq[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          const int s = q * ksw + i0 + hh * RW + r;  // k step
+          bq[r] = xrow_ok ? s_x[s * 64 + res_pos(lane, s)] : zero4();
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          ag = mfma16x16x32(a[r], bq[r], ag);
+          if (refill) a[r] = ldw(qn + (size_t)(hh * RW + r) * 64);
+        }
+      };
+      pass(wg, 0);
+      pass(wu, 1);
     }
   }
   if (active && q > 0) {
@@ -228,9 +313,15 @@ __global__ void __launch_bounds__(64 * 4 * (GLU ? kResMaxPairs : kResMaxTiles1))
       au[0] += ru.x; au[1] += ru.y; au[2] += ru.z; au[3] += ru.w;
     }
   }
+  if constexpr (GLU) {
+    if (half) {  // lanes 32..63 hold the up columns of lanes 0..31's gate columns
+#pragma unroll
+      for (int i = 0; i < 4; ++i) au[i] = shfl_xor(ag[i], 32);
+    }
+  }
   const int m = col;
-  if (m >= rows) return;
-  const int n0 = tile * 16 + grp * 4;
+  if (m >= rows || (half && grp >= 2)) return;
+  const int n0 = tile * 16 + (half ? 8 * (kind - 1) : 0) + grp * 4;
   uint2 o;
   if constexpr (GLU) {
     float o4[4];
@@ -284,12 +375,11 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   const int nw = p.res_waves;
   const int rows = p.rows, KS = p.KS, ksw = p.ksw;
   const int col = lane & 15, grp = lane >> 4;
-  const unsigned P = (unsigned)p.n >> 4;
-  const unsigned pair0 = blockIdx.x * P / gridDim.x;
-  const int npairs = (int)((blockIdx.x + 1) * P / gridDim.x - pair0);
-  const int j = wave >> 2, q = wave & 3;
-  const bool active = j < npairs;
-  const int tile = (int)pair0 + j;
+  const int j = wave >> 2, q = wave & 3;  // unit within the workgroup, k quarter
+  unsigned tile = 0;
+  int kind = 0;  // 0 a whole pair (or tile), 1 + h half pair h
+  const bool active = res_unit_of<GLU>(p, j, tile, kind);
+  const bool half = GLU && kind != 0;
 
   // ---- the rows into LDS: fragment f = (k step, M tile) is one KiB, wave w
   // copies fragments w, w + nw, ...  (LDS DMA, no registers).
@@ -303,13 +393,15 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   const uint4 *W = reinterpret_cast<const uint4 *>(p.w);
   const size_t up_off = (size_t)p.up_tiles * KS * 64;
   const int ksw_w = active ? ksw : 0;
-  const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + lane;
+  const uint4 *wq = W + ((size_t)(active ? tile : 0) * KS + (size_t)q * ksw) * 64 + res_lane_off(half, kind, lane, up_off);
+  // wu[r]'s block: the up tile's, or (half pair) RW k steps on
+  const size_t second = half ? (size_t)RW * 64 : up_off;
   uint4 wg[RW], wu[GLU ? RW : 1];
   if (active) {
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       wg[r] = ldw(wq + r * 64);
-      if constexpr (GLU) wu[r] = ldw(wq + r * 64 + up_off);
+      if constexpr (GLU) wu[r] = ldw(wq + r * 64 + second);
     }
   }
   // The copies are older than every ring load: once at most NA RW loads are
@@ -330,32 +422,62 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
   const bool xrow0 = col < rows, xrow1 = 16 + col < rows;
   constexpr int CH = 5;  // k steps whose B operands are read from LDS ahead
   static_assert(RW % CH == 0, "chunks within a ring pass");
-  for (int i0 = 0; i0 < ksw_w; i0 += RW) {
-    const bool refill = i0 + RW < ksw_w;
-    const uint4 *qn = wq + (size_t)(i0 + RW) * 64;
+  if (!half) {
+    for (int i0 = 0; i0 < ksw_w; i0 += RW) {
+      const bool refill = i0 + RW < ksw_w;
+      const uint4 *qn = wq + (size_t)(i0 + RW) * 64;
 #pragma unroll
-    for (int c0 = 0; c0 < RW; c0 += CH) {
-      uint4 b0[CH], b1[CH];
+      for (int c0 = 0; c0 < RW; c0 += CH) {
+        uint4 b0[CH], b1[CH];
 #pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const int s = q * ksw + i0 + c0 + c;
-        b0[c] = xrow0 ? s_x[(s * MT + 0) * 64 + lane] : zero4();
-        b1[c] = xrow1 ? s_x[(s * MT + 1) * 64 + lane] : zero4();
-      }
-#pragma unroll
-      for (int c = 0; c < CH; ++c) {
-        const int r = c0 + c;
-        ag[0] = mfma16x16x32(wg[r], b0[c], ag[0]);
-        ag[1] = mfma16x16x32(wg[r], b1[c], ag[1]);
-        if constexpr (GLU) {
-          au[0] = mfma16x16x32(wu[r], b0[c], au[0]);
-          au[1] = mfma16x16x32(wu[r], b1[c], au[1]);
+        for (int c = 0; c < CH; ++c) {
+          const int s = q * ksw + i0 + c0 + c;
+          b0[c] = xrow0 ? s_x[(s * MT + 0) * 64 + lane] : zero4();
+          b1[c] = xrow1 ? s_x[(s * MT + 1) * 64 + lane] : zero4();
         }
-        if (refill) {
-          wg[r] = ldw(qn + r * 64);
-          if constexpr (GLU) wu[r] = ldw(qn + r * 64 + up_off);
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          const int r = c0 + c;
+          ag[0] = mfma16x16x32(wg[r], b0[c], ag[0]);
+          ag[1] = mfma16x16x32(wg[r], b1[c], ag[1]);
+          if constexpr (GLU) {
+            au[0] = mfma16x16x32(wu[r], b0[c], au[0]);
+            au[1] = mfma16x16x32(wu[r], b1[c], au[1]);
+          }
+          if (refill) {
+            wg[r] = ldw(qn + r * 64);
+            if constexpr (GLU) wu[r] = ldw(qn + r * 64 + up_off);
+          }
         }
       }
+    }
+  } else if constexpr (GLU) {
+    // A half pair: k steps i0 .. i0+RW-1 from wg, then the next RW from wu,
+    // one MFMA chain per M tile in k order.
+    for (int i0 = 0; i0 < ksw_w; i0 += 2 * RW) {
+      const bool refill = i0 + 2 * RW < ksw_w;
+      const uint4 *qn = wq + (size_t)(i0 + 2 * RW) * 64;
+      auto pass = [&](uint4(&a)[RW], const int hh) {
+#pragma unroll
+        for (int c0 = 0; c0 < RW; c0 += CH) {
+          uint4 b0[CH], b1[CH];
+#pragma unroll
+          for (int c = 0; c < CH; ++c) {
+            const int s = q * ksw + i0 + hh * RW + c0 + c;
+            b0[c] = xrow0 ? s_x[(s * MT + 0) * 64 + lane] : zero4();
+            b1[c] = xrow1 ? s_x[(s * MT + 1) * 64 + lane] : zero4();
+          }
+#pragma unroll
+          for (int c = 0; c < CH; ++c) {
+            const int r = c0 + c;
+            ag[0] = mfma16x16x32(a[r], b0[c], ag[0]);
+            ag[1] = mfma16x16x32(a[r], b1[c], ag[1]);
+            if (refill) a[r] = ldw(qn + (size_t)(hh * RW + r) * 64);
+          }
+        }
+      };
+      pass(wg, 0);
+      pass(wu, 1);
     }
   }
 
@@ -385,7 +507,16 @@ __global__ void __launch_bounds__(64 * 4 * kResMaxPairs) glu_resident2_kernel(co
       }
     }
   }
-  const int n0 = tile * 16 + grp * 4;
+  if constexpr (GLU) {
+    if (half) {  // lanes 32..63 hold the up columns of lanes 0..31's gate columns
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) au[mt][i] = shfl_xor(ag[mt][i], 32);
+    }
+  }
+  if (half && grp >= 2) return;
+  const int n0 = tile * 16 + (half ? 8 * (kind - 1) : 0) + grp * 4;
   uint16_t *out = reinterpret_cast<uint16_t *>(p.out);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -653,16 +784,35 @@ hipError_t launch_glu_resident(const GemmParams &p, hipStream_t s) {
   // units per CU, fewer for a small one -- but always a workgroup with two
   // units, whose last four waves normalise the rows (at most 8 rows).
   const int umax = glu ? kResMaxPairs : kResMaxTiles1;
-  const int grid = std::max((P + umax - 1) / umax, std::min(ncu, glu ? P / 2 : P - 1));
-  if (grid < 1) return hipErrorInvalidValue;
-  const int pairs = (P + grid - 1) / grid;
-  if (pairs > umax || (p.rw != kResRing && p.rw != kResRing1) || p.ksw % p.rw) return hipErrorInvalidValue;
+  if ((p.rw != kResRing && p.rw != kResRing1) || p.ksw % p.rw || P < 1) return hipErrorInvalidValue;
+  // gate/up takes runs of half pairs (res_unit) when a wave's k range is
+  // whole ring passes of 2 RW k steps: at most five half pairs per
+  // workgroup, so at most three units.
+  const bool half = glu && p.ksw % (2 * p.rw) == 0;
+  int grid, units = 0;
+  if (half) {
+    grid = std::max((2 * P + 4) / 5, std::min(ncu, P / 2));
+    for (int b = 0; b < grid; ++b) {
+      const unsigned h0 = (unsigned)b * 2u * P / grid, h1 = (unsigned)(b + 1) * 2u * P / grid;
+      unsigned t = 0;
+      int kd = 0, u = 0;
+      while (u < kResMaxPairs && res_unit(h0, h1, u, t, kd)) ++u;
+      if (h1 - h0 > 5) return hipErrorInvalidValue;
+      units = std::max(units, u);
+    }
+  } else {
+    grid = std::max((P + umax - 1) / umax, std::min(ncu, glu ? P / 2 : P - 1));
+    if (grid < 1) return hipErrorInvalidValue;
+    units = (P + grid - 1) / grid;
+  }
+  if (units > umax) return hipErrorInvalidValue;
   GemmParams q = p;
-  q.res_waves = 4 * pairs;
+  q.res_waves = 4 * units;
+  q.res_half = half ? 1 : 0;
   if (p.rows <= kResMaxRows) {
     // The last four waves normalise the rows, so the others are at least one
-    // pair's.
-    if (pairs < 2) return hipErrorInvalidValue;
+    // unit's.
+    if (units < 2) return hipErrorInvalidValue;
     if (glu && p.rw == kResRing)
       hipLaunchKernelGGL((glu_resident_kernel<kResRing, true>), dim3(grid), dim3(64 * q.res_waves), 0, s, q);
     else if (!glu && p.rw == kResRing1)

@@ -27,7 +27,8 @@ constexpr int kArgSlots = 16;
 // workgroup per CU holding the normalised rows in LDS -- kResMinRows..
 // kResMaxRows rows normalised by the workgroup itself, kResMinRows2..
 // kResMaxRows2 rows (two M tiles) normalised by the pre-pass and copied in;
-// at most kResMaxPairs tile pairs (4 waves each) per workgroup and
+// at most kResMaxPairs units (tile pairs or half pairs, 4 waves each) per
+// workgroup and
 // kResMaxKSteps k steps (k <= 2560).  NORM_IN alone (QKV) takes the first
 // kind with single tiles in place of the pairs.
 constexpr int kResMinRows = 1;
@@ -105,6 +106,7 @@ struct GemmParams {
   int resident;  // gemm_resident.hip: 1 NORM_IN | GLU with the normalised rows in LDS, 2 RES_OUT with the rows in LDS,
                  // 3 RES_OUT split into k parts, each part's rows in LDS, 4 NORM_IN alone as 1
   int res_waves;  // resident: waves per workgroup (set by the launcher)
+  int res_half;   // resident GLU: the units are runs of half pairs (set by the launcher)
   size_t lds_bytes;
 };
 // Template flag of the hand-over instantiations (beside the QDEC_* flags).

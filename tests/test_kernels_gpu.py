@@ -550,6 +550,35 @@ def test_norm_in_resident_small_grids_bitexact(lib, n):
     agree(outs[1], linear(rms_norm(x.float(), nw.float(), 1e-6), W.float()), min_exact=0.97)
 
 
+@pytest.mark.parametrize("rows", [8, 24])
+@pytest.mark.parametrize("n", [32, 48, 80, 1040])
+def test_glu_resident_half_pairs_bitexact(lib, n, rows):
+    """gate/up on the resident plan with workgroups owning runs of half
+    pairs: 2, 3, 5 and 65 tile pairs give workgroups of two whole pairs, a
+    whole pair beside a half pair (either side), two whole pairs beside a
+    half pair, and mixes of four and five half pairs.  The output equals the
+    plain call's bits."""
+    from qdec import capi
+    x = rnd(rows, H, scale=2.0, seed=60 + n + rows)
+    x[rows - 1] = (x[rows - 1].float() * 0.05).to(torch.bfloat16)
+    W = rnd(2 * n, H, scale=0.02, seed=61)
+    nw = bf16(1 + 0.2 * torch.randn(H, generator=torch.Generator().manual_seed(62))).to(torch.bfloat16)
+    xd, Wt, nwd = x.to(DEV), pack(lib, W.to(DEV)), nw.to(DEV)
+    g = Gemm(lib, capi.NORM_IN | capi.GLU, n, H)
+    outs = []
+    for resident in (0, 1):
+        out = torch.full(((rows + 15) // 16 * 16, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+        a = capi.GemmArgs(x=xd.data_ptr(), w=Wt.data_ptr(), out=out.data_ptr(), norm_w=nwd.data_ptr(), eps=1e-6,
+                          rows=rows, n=n, k=H, flags=capi.NORM_IN | capi.GLU, ksplit=1, waves=4, tiles_per_wg=1,
+                          resident=resident, partial=g.partial.data_ptr(), counters=g.counters.data_ptr())
+        lib.gemm(a, stream())
+        torch.cuda.synchronize()
+        outs.append(out[:rows].cpu())
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    xin = rms_norm(x.float(), nw.float(), 1e-6)
+    agree(outs[1], silu_mul(linear(xin, W[:n].float()), linear(xin, W[n:].float())), min_exact=0.97)
+
+
 @pytest.mark.parametrize("role,rows", [("down", 1), ("down", 2), ("down", 3), ("down", 5), ("down", 8), ("o", 1),
                                       ("o", 3), ("o", 4), ("o", 8)])
 def test_res_out_rows_in_lds_bitexact(lib, role, rows):
