@@ -107,11 +107,15 @@ WIDE_TILES = 2
 WIDE_MIN_ROWS = 17
 # gate/up at RESIDENT_ROWS rows runs with its rows resident in LDS
 # (qdec_gemm's resident: one workgroup per CU reads its operands from one
-# LDS copy of the normalised rows; at 6..8 rows it normalises them itself,
-# no pre-pass launch; the same bits as the pre-pass path) wherever the
-# library's plan takes the shape.
+# LDS copy of the normalised rows; up to 8 rows it normalises them itself,
+# no pre-pass launch; the same bits as the plain path) wherever the
+# library's plan takes the shape.  With runs of half pairs, same-box A/B at
+# 1024-token prompts, gate/up us per launch and ms per step (plain /
+# resident): batch 5 23.3 / 20.1 and 2.489 / 2.342, batch 4 20.05 / 20.2
+# and 2.308 / 2.302; batch 3 19.4 / 20.2 and 2.262 / 2.278, batch 2 19.0 /
+# 20.2, batch 1 (512 tokens) 19.06 / 20.2 and 2.074 / 2.121.
 RESIDENT_GLU = True
-RESIDENT_ROWS = ((6, 8), (17, 32))
+RESIDENT_ROWS = ((4, 8), (17, 32))
 # The RES_OUT roles that copy their 1..8 rows into LDS first (qdec_gemm's
 # resident for RES_OUT: a weights-only ring; the same bits).  Same-box A/B,
 # ms per step at 1024-token prompts (neither / down / down and O): batch 8

@@ -197,7 +197,7 @@ def motif_prompts(B, S, seed, vocab=151936, motif=64, noise=0.1):
 def test_speculative_equals_plain_greedy(ckpt, engine):
     from engine import Engine
     spec = Engine.from_tensors(engine.model.cfg.raw, load_tensors(ckpt[0]), speculate=True)
-    for B, S, n, seed in ((4, 200, 40, 7), (2, 64, 25, 8), (1, 30, 17, 9), (3, 100, 12, 13), (6, 90, 12, 12),
+    for B, S, n, seed in ((4, 200, 40, 7), (2, 64, 25, 8), (1, 30, 17, 9), (3, 100, 12, 13), (5, 90, 12, 14), (6, 90, 12, 12),
                           (8, 40, 12, 11), (16, 40, 9, 10)):
         prompt = motif_prompts(B, S, seed)
         plain = list(engine.generate(prompt.tolist(), n))
