@@ -92,7 +92,7 @@ DOWN_SPLIT = 4
 DOWN_SPLIT_MIN_BATCH = 16
 # From this batch the O projection runs 4 waves per workgroup instead of 8
 # (see role_plan).
-O_FOUR_WAVES_MIN_BATCH = 8
+O_FOUR_WAVES_MIN_BATCH = 9
 # k splits of the O projection at O_SPLIT_MIN_BATCH..O_SPLIT_MAX_BATCH (see
 # role_plan): the partials go to the gate/up call's normalisation pre-pass.
 O_SPLIT = 2
@@ -252,13 +252,14 @@ def role_plan(n, k, role, batch=1):
         # resident plan (RESIDENT_QKV_ROWS) splits k over 4 waves
         waves = 8
     if role == "o" and batch >= O_FOUR_WAVES_MIN_BATCH:
-        # From 8 rows O's activations no longer fit the LDS and it takes the
-        # direct path (fragments loaded beside each weight block), where 4
-        # waves of 32 k steps beat 8 of 16.  Same-box A/B, ms per step at
-        # 1024-token prompts (8 waves / 4): batch 8 2.969 / 2.943, 10 3.091 /
-        # 3.073, 12 3.143 / 3.123, 16 3.126 / 3.096, 32 3.609 / 3.610; below
-        # 8 (LDS-staged rows) 4 waves lose: batch 7 2.993 / 3.073, 5 2.710 /
-        # 2.802, 3 2.404 / 2.449.
+        # From 9 rows O takes the direct path (fragments loaded beside each
+        # weight block), where 4 waves of 32 k steps beat 8 of 16.  Same-box
+        # A/B, ms per step at 1024-token prompts (8 waves / 4), measured on
+        # the direct path: batch 8 2.969 / 2.943, 10 3.091 / 3.073, 12 3.143 /
+        # 3.123, 16 3.126 / 3.096, 32 3.609 / 3.610; with the rows staged in
+        # LDS 4 waves lose: batch 7 2.993 / 3.073, 5 2.710 / 2.802, 3 2.404 /
+        # 2.449, and, since 8 rows copy their rows into LDS too (the resident
+        # plan), batch 8: O 7.21 / 7.78 us per launch, 2.448 / 2.467 ms.
         waves = 4
     while ks % waves:
         waves //= 2

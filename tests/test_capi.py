@@ -370,7 +370,7 @@ def test_role_plans_do_not_depend_on_rows():
     assert role_plan(2560, 9728, "down") == (1, 8, 1) and role_plan(2560, 4096, "o")[0] == 1
     assert role_plan(2560, 9728, "down", batch=16)[:2] == (4, 4)
     assert role_plan(2560, 9728, "down", batch=8) == (1, 8, 1)
-    assert role_plan(2560, 4096, "o", batch=7) == (1, 8, 1) and role_plan(2560, 4096, "o", batch=8) == (1, 4, 1)
+    assert role_plan(2560, 4096, "o", batch=8) == (1, 8, 1) and role_plan(2560, 4096, "o", batch=9) == (1, 4, 1)
     # QKV from 17 rows: k over 4 waves on the resident plan, else 8 waves of two tiles
     assert role_plan(6144, 2560, "qkv", batch=17)[:2] == (1, 4) and role_plan(6144, 2560, "qkv", batch=16)[:2] == (1, 4)
     assert role_plan(6144, 2560, "qkv", batch=33)[:2] == (1, 8)
