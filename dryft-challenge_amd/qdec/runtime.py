@@ -62,7 +62,10 @@ LM_TILES_BATCHED = 8
 # prompt), 2.228 / 2.320 (2048); batch 2 2.282 / 2.347 (512), 2.294 / 2.353
 # (1024), 2.507 / 2.551 (4096); batch 3 2.427 / 2.413 (1024), 2.403 / 2.385
 # (256); batch 4 2.538 / 2.474 (512), 2.569 / 2.483 (1024), 2.866 / 2.767
-# (4096).  Both give the same bits.
+# (4096).  Both give the same bits.  Measured again once O could copy its
+# rows into LDS when it merges nothing (O / attention us per launch, ms per
+# step, merge in O / in the attention): batch 1 8.27 / 6.95 and 6.82 / 10.86,
+# 2.070 / 2.143 ms; batch 2 (1024) 9.5 / 8.85 and 6.9 / 12.9, 2.228 / 2.256.
 MERGE_IN_O_MAX_BATCH = 2
 # qdec_layer (one launch per layer) takes plain decode up to this batch: its
 # GEMM stages stage their rows from registers (kLayerMaxRows).
