@@ -54,7 +54,8 @@ PREFILL_SKINNY_ROWS = GEMM_MAX_ROWS
 # 1 row).  Grouping changes no sum and the argmax partials are scanned
 # lowest index first, so tokens and logits do not depend on it (MI355X,
 # ms/step at 4 vs 8 tiles: batch 8 3.055 -> 3.031, batch 32 3.78 -> 3.72;
-# batch 1 2.160 vs 2.170).
+# batch 1 2.160 vs 2.170; again with the resident plans, 4 / 8 tiles: batch 8
+# 2.443 / 2.442, batch 32 5.407 / 5.404).
 LM_TILES_BATCHED = 8
 # Plain decode up to this batch merges attention chunks in the O projection;
 # above it the attention's last-arriving chunk merges them.  Same-box A/B,
